@@ -1,0 +1,245 @@
+"""Pin the numpy oracle (oracle/sim.py) before trusting it.
+
+Three kinds of checks, chosen so a plausible mistake (dropped term, wrong
+rounding point, wrong index, transposed operand) fails at least one:
+
+1. golden fixtures written from the reference's own ``filter_util.py``
+   (tests/golden/make_golden.py);
+2. torch's library routines the reference calls, on the whole fp16 domain
+   where it is small (log) and on stress inputs (mean / norm);
+3. closed forms and invariants (brute force on tiny inputs).
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sim
+
+GOLD = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden_sim.npz"))
+
+
+def randn16(seed, shape, scale=1.0):
+    g = np.random.default_rng(seed)
+    return (g.standard_normal(shape, dtype=np.float32) * np.float32(scale)).astype(np.float16)
+
+
+def bits(a):
+    return np.ascontiguousarray(a).view(np.uint16)
+
+
+# ---------------------------------------------------------------- fixtures
+
+@pytest.mark.parametrize("L", [17, 31, 256, 4103])
+def test_metadata_matches_reference_fixture(L):
+    nh = 4 if L < 4096 else 2
+    K = randn16(100 + L, (1, nh, L, 128))
+    V = randn16(200 + L, (1, nh, L, 128))
+    pf = sim.get_max_min_filters(K, 16)
+    vm = sim.compute_page_v_mean(L, 16, V)
+    lvn = sim.log_v_norm(vm)
+    assert np.array_equal(bits(pf), bits(GOLD[f"meta_L{L}_filters"]))
+    assert np.array_equal(bits(vm), bits(GOLD[f"meta_L{L}_vmean"]))
+    assert np.array_equal(bits(lvn), bits(GOLD[f"meta_L{L}_lvn"]))
+
+
+def test_decode_trace_matches_reference_fixture():
+    nh, d, L0, steps = 4, 128, 21, 40
+    K = randn16(300, (1, nh, L0, d))
+    V = randn16(301, (1, nh, L0, d))
+    kn = randn16(302, (steps, 1, nh, 1, d))
+    vn = randn16(303, (steps, 1, nh, 1, d))
+    st = sim.SimLayerState(K, V)
+    for s in range(steps):
+        st.append(kn[s], vn[s])
+        assert np.array_equal(bits(st.v_mean[:, :, -1]),
+                              bits(GOLD["trace_vmean_last_page_per_step"][s])), s
+        assert np.array_equal(bits(st.page_filters[:, :, -1]),
+                              bits(GOLD["trace_filters_last_page_per_step"][s])), s
+    assert np.array_equal(bits(st.page_filters), bits(GOLD["trace_final_filters"]))
+    assert np.array_equal(bits(st.v_mean), bits(GOLD["trace_final_vmean"]))
+
+
+def _selection_inputs(tag):
+    seed, nh, nkvh, L, budget, fixed, va, outlier = [int(x) for x in GOLD[f"sel_{tag}_params"]]
+    d = 128
+    K = randn16(seed, (1, nkvh, L, d))
+    V = randn16(seed + 1, (1, nkvh, L, d))
+    q = randn16(seed + 2, (1, nh, 1, d))
+    if outlier:
+        ch = np.random.default_rng(seed + 3).permutation(d)[:4]
+        K[..., ch] = (K[..., ch].astype(np.float32) * 8).astype(np.float16)
+    if tag == "ties":
+        for dst in range(9, 21):
+            K[:, :, dst * 16:(dst + 1) * 16] = K[:, :, 5 * 16:6 * 16]
+            V[:, :, dst * 16:(dst + 1) * 16] = V[:, :, 5 * 16:6 * 16]
+    return q, K, V, nh, nkvh, L, budget, bool(fixed), bool(va)
+
+
+SEL_TAGS = ["c1_fixed", "c1_free", "c1_quest", "ragged_outlier", "tiny", "gqa", "gqa_quest", "ties"]
+
+
+@pytest.mark.parametrize("tag", SEL_TAGS)
+def test_selection_matches_reference_fixture(tag):
+    q, K, V, nh, nkvh, L, budget, fixed, va = _selection_inputs(tag)
+    st = sim.SimLayerState(K, V)
+    scores, pages = sim.select_pages(st, q, budget, fixed, va, nh // nkvh)
+    # the page bound agrees with the reference's to fp32 summation-order noise
+    pb = sim.page_bound(q, st.page_filters, nh // nkvh)[0]
+    ref_pb = GOLD[f"sel_{tag}_page_bound"]
+    np.testing.assert_allclose(pb, ref_pb, rtol=2e-6, atol=2e-5)
+    ref_sel = GOLD[f"sel_{tag}_pages"]
+    exact = 0
+    for hh in range(ref_sel.shape[0]):
+        kvh = hh // (nh // nkvh)
+        ok, why = sim.selection_matches(pages[0, kvh, 0], ref_sel[hh], scores[0, kvh, 0], fixed)
+        assert ok, (tag, hh, why)
+        exact += why == "exact"
+    if tag != "ties":
+        assert exact == ref_sel.shape[0], f"{tag}: only {exact} heads exact"
+
+
+def test_planted_mistakes_fail_the_fixture():
+    """Mistakes planted in the oracle (on the CPU) must be caught."""
+    q, K, V, nh, nkvh, L, budget, fixed, va = _selection_inputs("c1_fixed")
+    st = sim.SimLayerState(K, V)
+    ref_sel = GOLD["sel_c1_fixed_pages"]
+    scores, _ = sim.select_pages(st, q, budget, fixed, True)
+    k = ref_sel.shape[1]
+
+    def n_fail(pages):
+        return sum(not sim.selection_matches(pages[hh], ref_sel[hh], scores[0, hh, 0], fixed)[0]
+                   for hh in range(nh))
+
+    # dropped value term
+    chunk = sim.page_bound(q, st.page_filters)[:, :, None, :]
+    no_v = sim.topk_pages((2 * (chunk / np.float32(math.sqrt(128))))[:, :, 0], k, fixed)[0]
+    assert n_fail(no_v) > nh // 2
+    # value term with the wrong sign
+    lvn = sim.log_v_norm(st.v_mean)
+    wrong = sim.value_aware_page_scores(chunk, (-lvn.astype(np.float32)).astype(np.float16), 1, 128)
+    assert n_fail(sim.topk_pages(wrong[:, :, 0], k, fixed)[0]) > nh // 2
+    # value term of page p read at p // 16 (the index slip of the kernel tree)
+    slip = sim.value_aware_page_scores(chunk, lvn[:, :, np.arange(lvn.shape[-1]) // 16], 1, 128)
+    assert n_fail(sim.topk_pages(slip[:, :, 0], k, fixed)[0]) > nh // 2
+    # bound from Kmax only (the min/max choice by sign of q dropped)
+    only_max = np.concatenate([st.page_filters[:, :, :, :1]] * 2, axis=3)
+    om = sim.value_aware_page_scores(sim.page_bound(q, only_max)[:, :, None, :], lvn, 1, 128)
+    assert n_fail(sim.topk_pages(om[:, :, 0], k, fixed)[0]) > nh // 2
+    # 1/sqrt(d) scaling dropped
+    nsc = sim.value_aware_page_scores(chunk * np.float32(math.sqrt(128)), lvn, 1, 128)
+    assert n_fail(sim.topk_pages(nsc[:, :, 0], k, fixed)[0]) > nh // 2
+
+
+def test_decode_attention_matches_torch_fixture():
+    nh, d, L = 4, 128, 300
+    q = randn16(400, (1, nh, 1, d))
+    K = randn16(401, (1, nh, L, d))
+    V = randn16(402, (1, nh, L, d))
+    mask = GOLD["attn_mask"]
+    o = sim.masked_decode_attention(q, K, V, mask)
+    ref = GOLD["attn_out"]
+    err = np.abs(o.astype(np.float32) - ref.astype(np.float32)).max()
+    assert err <= 2e-3
+    assert (bits(o) == bits(ref)).mean() > 0.95
+
+
+# ---------------------------------------------------------------- library routines
+
+def test_log_fp16_whole_domain_matches_torch():
+    allh = np.arange(0, 0x7C00, dtype=np.uint16).view(np.float16)
+    ref = torch.log(torch.from_numpy(allh.copy())).numpy()
+    assert np.array_equal(bits(sim.log_fp16(allh)), bits(ref))
+
+
+def test_mean_and_norm_match_torch_on_stress_inputs():
+    g = torch.Generator().manual_seed(5)
+    e = torch.randint(-14, 10, (1, 4, 64 * 16, 128), generator=g).float()
+    v = (torch.randn(1, 4, 64 * 16, 128, generator=g) * torch.exp2(e)).clamp(-6e4, 6e4).half()
+    ref = v.reshape(1, 4, 64, 16, 128).mean(dim=3).numpy()
+    assert np.array_equal(bits(sim.compute_page_v_mean(64 * 16, 16, v.numpy())), bits(ref))
+    part = v[:, :, :13]
+    refp = part.mean(dim=2, keepdim=True).numpy()
+    assert np.array_equal(bits(sim.compute_page_v_mean(13, 16, part.numpy())), bits(refp))
+    nref = v.norm(p=2, dim=-1).numpy()
+    assert np.array_equal(bits(sim.norm_fp16(v.numpy())), bits(nref))
+
+
+def test_running_mean_matches_torch_ops():
+    g = torch.Generator().manual_seed(6)
+    m = torch.randn(8, 128, generator=g).half()
+    x = torch.randn(8, 128, generator=g).half()
+    for n in range(1, 16):
+        ref = ((m * n + x) / (n + 1)).numpy()
+        assert np.array_equal(bits(sim.update_mean_filter(m.numpy(), x.numpy(), n)), bits(ref))
+
+
+# ---------------------------------------------------------------- closed forms / invariants
+
+def test_filters_bound_every_key_and_are_attained():
+    K = randn16(1, (1, 3, 53, 128))
+    pf = sim.get_max_min_filters(K, 16)
+    for p in range(pf.shape[2]):
+        blk = K[:, :, p * 16:(p + 1) * 16].astype(np.float32)
+        assert np.array_equal(pf[:, :, p, 0].astype(np.float32), blk.max(axis=2))
+        assert np.array_equal(pf[:, :, p, 1].astype(np.float32), blk.min(axis=2))
+
+
+def test_page_bound_is_an_upper_bound_and_tight_for_single_token_pages():
+    q = randn16(2, (1, 2, 1, 128))
+    K = randn16(3, (1, 2, 64, 128))
+    pf = sim.get_max_min_filters(K, 16)
+    pb = sim.page_bound(q, pf)
+    qk = np.einsum("bhd,bhld->bhl", q[:, :, 0].astype(np.float64), K.astype(np.float64))
+    pmax = qk.reshape(1, 2, 4, 16).max(-1)
+    assert np.all(pb >= pmax - 1e-4)
+    # one-token pages: bound == q.k exactly (up to fp32 rounding)
+    pf1 = sim.get_max_min_filters(K, 1)
+    np.testing.assert_allclose(sim.page_bound(q, pf1), qk, rtol=1e-5, atol=1e-4)
+
+
+def test_k_rule_and_fixed_forcing():
+    assert sim.num_selected_pages(2048, 16, 2048) == 128
+    assert sim.num_selected_pages(1024, 16, 256) == 64
+    assert sim.num_selected_pages(20, 16, 100) == 3
+    assert sim.num_selected_pages(4096, 16, 10) == 10
+    s = np.array([[0.0, 5, 4, 3, -1.0]], np.float32)
+    assert list(sim.topk_pages(s, 3, True)[0]) == [0, 1, 4]
+    assert list(sim.topk_pages(s, 3, False)[0]) == [1, 2, 3]
+    # ties: lowest index first
+    s = np.array([[1.0, 2, 2, 2, 0]], np.float32)
+    assert list(sim.topk_pages(s, 2, False)[0]) == [1, 2]
+
+
+def test_full_budget_reduces_to_dense_attention():
+    q = randn16(4, (1, 2, 1, 128))
+    # L = 112 = 7 full pages.  (For L not a page multiple the reference's
+    # k = min(L, budget) // 16 leaves one page out even at a huge budget.)
+    K = randn16(5, (1, 2, 112, 128))
+    V = randn16(6, (1, 2, 112, 128))
+    st = sim.SimLayerState(K[:, :, :111], V[:, :, :111])
+    o, _, pages = sim.decode_step(st, q, K[:, :, 111:], V[:, :, 111:], 4096)
+    assert pages.shape[-1] == 7
+    s = np.einsum("hd,hld->hl", q[0, :, 0].astype(np.float64), K[0].astype(np.float64)) / math.sqrt(128)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    dense = np.einsum("hl,hld->hd", p, V[0].astype(np.float64))
+    assert np.abs(o[0, :, 0].astype(np.float64) - dense).max() < 2e-3
+
+
+def test_causal_prefill_rows_small_bruteforce():
+    q = randn16(7, (5, 2, 8))
+    k = randn16(8, (9, 2, 8))
+    v = randn16(9, (9, 2, 8))
+    out = sim.causal_prefill_rows(q, k, v)
+    for i in range(5):
+        last = 9 - 5 + i
+        for hh in range(2):
+            s = np.array([q[i, hh].astype(np.float64) @ k[j, hh].astype(np.float64) for j in range(last + 1)])
+            s /= math.sqrt(8)
+            p = np.exp(s - s.max())
+            p /= p.sum()
+            ref = sum(p[j] * v[j, hh].astype(np.float64) for j in range(last + 1))
+            np.testing.assert_allclose(out[i, hh], ref, rtol=1e-5, atol=1e-6)
