@@ -1,0 +1,16 @@
+"""aoakv -- MI355X (gfx950) implementation of AOA-KV's decode hot path.
+
+Kernels live in libaoakv.so (hand-written HIP, C ABI in include/aoakv.h);
+this package binds them with ctypes and mirrors the reference's
+``quest.utils`` interface in ``aoakv.utils``.  Importing the package loads
+the library and fails if it is missing: there is no fallback.
+"""
+from . import _lib
+from ._lib import AoakvError, version
+
+_lib.load()
+
+from . import ops  # noqa: E402
+from . import utils  # noqa: E402
+
+__all__ = ["ops", "utils", "AoakvError", "version"]

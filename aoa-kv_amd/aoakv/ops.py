@@ -1,0 +1,240 @@
+"""torch-tensor wrappers of the libaoakv.so entry points.
+
+Each function checks dtypes, devices and shapes, then calls the C ABI with
+raw device pointers on torch's current HIP stream.  Tensors are never
+copied or converted here: a wrong dtype / layout is an error, not a cast.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import FLAG_FIXED, FLAG_VALUE_AWARE  # noqa: F401  (re-exported)
+
+NHD = 0
+HND = 1
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _need(t: torch.Tensor, name: str, dtype: torch.dtype) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def cache_dims(kv_data: torch.Tensor, layout: int):
+    """(max_pages, page_size, num_heads, head_dim) of a paged cache tensor
+    [max_pages, 2, S, H, D] (NHD) or [max_pages, 2, H, S, D] (HND)."""
+    if kv_data.dim() != 5 or kv_data.shape[1] != 2:
+        raise ValueError(f"paged cache must be 5-d [pages, 2, ., ., D], got {tuple(kv_data.shape)}")
+    if layout == NHD:
+        P, _, S, H, D = kv_data.shape
+    elif layout == HND:
+        P, _, H, S, D = kv_data.shape
+    else:
+        raise ValueError(f"unknown layout {layout}")
+    return P, S, H, D
+
+
+def append_kv_cache_prefill(k, v, kv_data, kv_indices, num_kv_pages: int, kv_last_page_len: int,
+                            metadata_data, metadata_indices, v_log_norm, v_mean, layout: int):
+    """Reference: quest/ops/csrc/page.cu:107-222 (append_kv_cache_prefill)."""
+    for t, n in ((k, "k"), (v, "v"), (kv_data, "kv_data"), (metadata_data, "metadata_data"),
+                 (v_log_norm, "v_log_norm"), (v_mean, "v_mean")):
+        _need(t, n, torch.float16)
+    _need(kv_indices, "kv_indices", torch.int32)
+    _need(metadata_indices, "metadata_indices", torch.int32)
+    _, S, H, D = cache_dims(kv_data, layout)
+    if k.shape != v.shape or k.dim() != 3 or k.shape[1] != H or k.shape[2] != D:
+        raise ValueError(f"k/v must be [N, {H}, {D}], got {tuple(k.shape)} / {tuple(v.shape)}")
+    if kv_indices.numel() < num_kv_pages:
+        raise ValueError("kv_indices shorter than num_kv_pages")
+    _lib.call("aoakv_append_kv_cache_prefill", k.data_ptr(), v.data_ptr(), k.shape[0],
+              kv_data.data_ptr(), kv_indices.data_ptr(), num_kv_pages, kv_last_page_len,
+              metadata_data.data_ptr(), metadata_indices.data_ptr(), v_log_norm.data_ptr(),
+              v_mean.data_ptr(), H, D, S, layout, _stream())
+
+
+def append_kv_cache_decode(k, v, kv_data, kv_indptr, kv_indices, kv_last_page_len,
+                           metadata_data, metadata_indptr, metadata_indices, v_log_norm, v_mean,
+                           layout: int):
+    """Reference: quest/ops/csrc/page.cu:6-105 (append_kv_cache_decode); k, v
+    are [B, H, D], one new token per sequence."""
+    for t, n in ((k, "k"), (v, "v"), (kv_data, "kv_data"), (metadata_data, "metadata_data"),
+                 (v_log_norm, "v_log_norm"), (v_mean, "v_mean")):
+        _need(t, n, torch.float16)
+    for t, n in ((kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"),
+                 (kv_last_page_len, "kv_last_page_len"), (metadata_indptr, "metadata_indptr"),
+                 (metadata_indices, "metadata_indices")):
+        _need(t, n, torch.int32)
+    _, S, H, D = cache_dims(kv_data, layout)
+    B = k.shape[0]
+    if k.shape != (B, H, D) or v.shape != (B, H, D):
+        raise ValueError(f"k/v must be [B, {H}, {D}]")
+    if kv_indptr.numel() != B + 1 or kv_last_page_len.numel() != B or metadata_indptr.numel() != B + 1:
+        raise ValueError("indptr / last_page_len sizes do not match the batch")
+    _lib.call("aoakv_append_kv_cache_decode", k.data_ptr(), v.data_ptr(), B, kv_data.data_ptr(),
+              kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
+              metadata_data.data_ptr(), metadata_indptr.data_ptr(), metadata_indices.data_ptr(),
+              v_log_norm.data_ptr(), v_mean.data_ptr(), H, D, S, layout, _stream())
+
+
+def estimate_attn_score(q, scores, metadata_data, metadata_indptr, metadata_indices, kv_indptr,
+                        kv_indices, kv_last_page_len, v_log_norm, max_pages: int, layout: int,
+                        flags: int = FLAG_VALUE_AWARE):
+    """Reference: quest/ops/csrc/estimate.cu:6-90.  q [B, Hq, D] fp16 ->
+    scores [B, Hkv, stride] fp32 (stride = scores.shape[-1])."""
+    _need(q, "q", torch.float16)
+    _need(scores, "scores", torch.float32)
+    _need(metadata_data, "metadata_data", torch.float16)
+    for t, n in ((metadata_indptr, "metadata_indptr"), (metadata_indices, "metadata_indices"),
+                 (kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"),
+                 (kv_last_page_len, "kv_last_page_len")):
+        _need(t, n, torch.int32)
+    if flags & FLAG_VALUE_AWARE:
+        _need(v_log_norm, "v_log_norm", torch.float16)
+    _, S, Hkv, D = cache_dims(metadata_data, layout)
+    B, Hq, Dq = q.shape
+    if Dq != D or scores.dim() != 3 or scores.shape[0] != B or scores.shape[1] != Hkv:
+        raise ValueError(f"scores must be [B, {Hkv}, >= max_pages]")
+    _lib.call("aoakv_estimate_attn_score", q.data_ptr(), scores.data_ptr(), scores.shape[2],
+              metadata_data.data_ptr(), metadata_indptr.data_ptr(), metadata_indices.data_ptr(),
+              kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
+              _ptr(v_log_norm), B, max_pages, Hq, Hkv, D, S, layout, flags, _stream())
+
+
+def topk_filtering(scores, kv_indptr, kv_indices, kv_last_page_len, token_budget: int, sel_pages,
+                   page_size: int = 16, flags: int = FLAG_FIXED, token_budgets=None):
+    """Reference: quest/ops/csrc/topk.cu:7-46.  Writes sel_pages [B, Hkv, k_max]
+    (physical page ids, ascending logical order)."""
+    _need(scores, "scores", torch.float32)
+    _need(sel_pages, "sel_pages", torch.int32)
+    for t, n in ((kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"),
+                 (kv_last_page_len, "kv_last_page_len")):
+        _need(t, n, torch.int32)
+    if token_budgets is not None:
+        _need(token_budgets, "token_budgets", torch.int32)
+    B, Hkv, stride = scores.shape
+    if sel_pages.dim() != 3 or sel_pages.shape[:2] != (B, Hkv):
+        raise ValueError("sel_pages must be [B, Hkv, k_max]")
+    _lib.call("aoakv_topk_filtering", scores.data_ptr(), stride, kv_indptr.data_ptr(),
+              kv_indices.data_ptr(), kv_last_page_len.data_ptr(), token_budget,
+              _ptr(token_budgets), sel_pages.data_ptr(), sel_pages.shape[2], B, Hkv, page_size,
+              flags, _stream())
+
+
+def decode_workspace(batch: int, num_qo_heads: int, num_kv_heads: int, max_sel_pages: int,
+                     device="cuda") -> torch.Tensor:
+    """Caller-owned decode workspace (replaces BatchDecodeHandler's buffers,
+    decode_handler.cuh:73-136), counters zeroed."""
+    n = _lib.load().aoakv_decode_workspace_size(batch, num_qo_heads, num_kv_heads, 128,
+                                                 max_sel_pages)
+    ws = torch.empty(n, dtype=torch.uint8, device=device)
+    _lib.call("aoakv_workspace_init", ws.data_ptr(), n, _stream())
+    return ws
+
+
+def decode_sparse_attn(q, o, kv_data, kv_indptr, kv_indices, kv_last_page_len, sel_pages,
+                       token_budget: int, workspace, max_pages: int, num_kv_heads: int,
+                       layout: int, token_budgets=None):
+    """Reference: quest/ops/csrc/approx_attn.cu:68-151.  sel_pages None = dense."""
+    _need(q, "q", torch.float16)
+    _need(o, "o", torch.float16)
+    _need(kv_data, "kv_data", torch.float16)
+    _need(workspace, "workspace", torch.uint8)
+    for t, n in ((kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"),
+                 (kv_last_page_len, "kv_last_page_len")):
+        _need(t, n, torch.int32)
+    if sel_pages is not None:
+        _need(sel_pages, "sel_pages", torch.int32)
+    if token_budgets is not None:
+        _need(token_budgets, "token_budgets", torch.int32)
+    _, S, Hkv, D = cache_dims(kv_data, layout)
+    if Hkv != num_kv_heads:
+        raise ValueError("num_kv_heads does not match kv_data")
+    B, Hq, _ = q.shape
+    if o.shape != q.shape:
+        raise ValueError("o must have q's shape")
+    _lib.call("aoakv_decode_sparse_attn", q.data_ptr(), o.data_ptr(), kv_data.data_ptr(),
+              kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
+              _ptr(sel_pages), 0 if sel_pages is None else sel_pages.shape[-1], token_budget,
+              _ptr(token_budgets), workspace.data_ptr(), workspace.numel(), B, max_pages, Hq,
+              Hkv, D, S, layout, _stream())
+
+
+def sparse_decode_layer(q, o, kv_data, kv_indptr, kv_indices, kv_last_page_len, metadata_data,
+                        metadata_indptr, metadata_indices, v_log_norm, scores, sel_pages,
+                        token_budget: int, workspace, max_pages: int, layout: int,
+                        flags: int = FLAG_VALUE_AWARE | FLAG_FIXED, token_budgets=None):
+    """Fused estimate + top-k + sparse decode for one layer (reference call
+    sequence QuestAttention.py:135-157)."""
+    _need(q, "q", torch.float16)
+    _need(o, "o", torch.float16)
+    _need(kv_data, "kv_data", torch.float16)
+    _need(metadata_data, "metadata_data", torch.float16)
+    _need(scores, "scores", torch.float32)
+    _need(sel_pages, "sel_pages", torch.int32)
+    _need(workspace, "workspace", torch.uint8)
+    if flags & FLAG_VALUE_AWARE:
+        _need(v_log_norm, "v_log_norm", torch.float16)
+    if token_budgets is not None:
+        _need(token_budgets, "token_budgets", torch.int32)
+    _, S, Hkv, D = cache_dims(kv_data, layout)
+    B, Hq, _ = q.shape
+    _lib.call("aoakv_sparse_decode_layer", q.data_ptr(), o.data_ptr(), kv_data.data_ptr(),
+              kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
+              metadata_data.data_ptr(), metadata_indptr.data_ptr(), metadata_indices.data_ptr(),
+              _ptr(v_log_norm), scores.data_ptr(), scores.shape[-1], sel_pages.data_ptr(),
+              sel_pages.shape[-1], token_budget, _ptr(token_budgets), workspace.data_ptr(),
+              workspace.numel(), B, max_pages, Hq, Hkv, D, S, layout, flags, _stream())
+
+
+def estimate_topk(q, metadata_data, metadata_indptr, metadata_indices, kv_indptr, kv_indices,
+                  kv_last_page_len, v_log_norm, scores, sel_pages, token_budget: int, workspace,
+                  max_pages: int, layout: int, flags: int = FLAG_VALUE_AWARE | FLAG_FIXED,
+                  token_budgets=None):
+    """Page scores + top-k in one launch (the first half of sparse_decode_layer)."""
+    _need(q, "q", torch.float16)
+    _need(metadata_data, "metadata_data", torch.float16)
+    _need(scores, "scores", torch.float32)
+    _need(sel_pages, "sel_pages", torch.int32)
+    _need(workspace, "workspace", torch.uint8)
+    if token_budgets is not None:
+        _need(token_budgets, "token_budgets", torch.int32)
+    _, S, Hkv, D = cache_dims(metadata_data, layout)
+    B, Hq, _ = q.shape
+    _lib.call("aoakv_estimate_topk", q.data_ptr(), metadata_data.data_ptr(),
+              metadata_indptr.data_ptr(), metadata_indices.data_ptr(), kv_indptr.data_ptr(),
+              kv_indices.data_ptr(), kv_last_page_len.data_ptr(), _ptr(v_log_norm),
+              scores.data_ptr(), scores.shape[-1], sel_pages.data_ptr(), sel_pages.shape[-1],
+              token_budget, _ptr(token_budgets), workspace.data_ptr(), workspace.numel(), B,
+              max_pages, Hq, Hkv, D, S, layout, flags, _stream())
+
+
+def prefill_with_paged_kv_cache(q, kv_data, kv_indices, num_kv_pages: int, kv_last_page_len: int,
+                                layout: int, causal: bool = True, o=None):
+    """Reference: quest/ops/csrc/batch_prefill.cu:27-117.  q [L, H, D] -> o."""
+    _need(q, "q", torch.float16)
+    _need(kv_data, "kv_data", torch.float16)
+    _need(kv_indices, "kv_indices", torch.int32)
+    _, S, H, D = cache_dims(kv_data, layout)
+    if o is None:
+        o = torch.empty_like(q)
+    _lib.call("aoakv_prefill_with_paged_kv_cache", q.data_ptr(), o.data_ptr(), kv_data.data_ptr(),
+              kv_indices.data_ptr(), num_kv_pages, kv_last_page_len, q.shape[0], int(causal), H,
+              D, S, layout, _stream())
+    return o

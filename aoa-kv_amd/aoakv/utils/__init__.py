@@ -1,0 +1,124 @@
+"""Mirror of the reference's ``quest.utils`` op wrappers
+(kernels/aoa_kv/quest/utils/__init__.py:69-285), backed by libaoakv.so.
+
+Same names, same argument meaning, same call order as QuestAttention.forward
+(QuestAttention.py:99-157)::
+
+    append_kv(k, v, ctrl, layer)                  # [N, H, D] new tokens
+    o = prefill_forward(q, ctrl, layer)           # N > 1
+    s = decode_estimate(q, ctrl, layer)           # [Hkv, P] fp32 page scores
+    decode_topk(s, ctrl)                          # -> ctrl.topk_dindices_buffer
+    o = decode_sparse_attn(q, ctrl, layer, ctrl.topk_dindices_buffer)
+
+``decode_sparse_attn(q, ctrl, layer, ctrl.kv_indices_without_last)`` (or
+``None``) attends every page, as the reference's dense-layer path does.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from .. import ops
+from .controller import InferenceController
+from .kv_cache import KvCache, KvPool
+from .utils import TensorLayout
+
+__all__ = [
+    "TensorLayout",
+    "KvCache",
+    "KvPool",
+    "InferenceController",
+    "append_kv",
+    "prefill_forward",
+    "decode_estimate",
+    "decode_topk",
+    "decode_sparse_attn",
+    "decode_layer",
+]
+
+
+def append_kv(k: torch.Tensor, v: torch.Tensor, iController: InferenceController,
+              layer_idx: int):
+    """Append new k/v [N, H, D] to the layer's cache and metadata
+    (reference __init__.py:69-131).  N > 1: bulk append; N == 1: decode append."""
+    c = iController
+    if k.size(0) > 1:
+        ops.append_kv_cache_prefill(
+            k, v, c.kv_cache.buf_layer(layer_idx), c.kv_indices_with_last,
+            len(c.kv_cache.indicies), c.kv_cache.last_page_len,
+            c.metadata_cache.buf_layer(layer_idx), c.metadata_indices,
+            c.v_log_norm_layer(layer_idx), c.v_mean_layer(layer_idx), c.layout)
+    else:
+        ops.append_kv_cache_decode(
+            k, v, c.kv_cache.buf_layer(layer_idx), c.kv_indptr_for_append,
+            c.kv_indices_with_last, c.kv_last_page_len_t,
+            c.metadata_cache.buf_layer(layer_idx), c.metadata_indptr_for_append,
+            c.metadata_indices, c.v_log_norm_layer(layer_idx), c.v_mean_layer(layer_idx),
+            c.layout)
+
+
+def prefill_forward(q: torch.Tensor, iController: InferenceController, layer_idx: int,
+                    rope_scale: Optional[float] = None, rope_theta: Optional[float] = None
+                    ) -> torch.Tensor:
+    """Causal attention of the new tokens over the cache (reference
+    __init__.py:133-175).  RoPE is applied by the caller (rope_* unused)."""
+    c = iController
+    return ops.prefill_with_paged_kv_cache(
+        q, c.kv_cache.buf_layer(layer_idx), c.kv_indices_with_last, len(c.kv_cache.indicies),
+        c.kv_cache.last_page_len, c.layout, causal=True)
+
+
+def decode_estimate(q: torch.Tensor, iController: InferenceController, layer_idx: int
+                    ) -> torch.Tensor:
+    """Page scores of every page, [Hkv, P] fp32 (reference __init__.py:177-214)."""
+    c = iController
+    P = len(c.kv_cache.indicies)
+    ops.estimate_attn_score(
+        q.view(1, c.num_heads, c.head_dim), c.scores, c.metadata_cache.buf_layer(layer_idx),
+        c.metadata_indptr_for_append, c.metadata_indices, c.kv_indptr_for_append,
+        c.kv_indices_with_last, c.kv_last_page_len_t, c.v_log_norm_layer(layer_idx), P,
+        c.layout, c.flags)
+    return c.scores[0, :, :P]
+
+
+def decode_topk(estimated_attn_score: torch.Tensor, iController: InferenceController):
+    """Top-k pages per kv head into ``topk_dindices_buffer`` [Hkv, k] (physical
+    page ids, ascending) (reference __init__.py:216-246)."""
+    c = iController
+    ops.topk_filtering(c.scores, c.kv_indptr_for_append, c.kv_indices_with_last,
+                       c.kv_last_page_len_t, c.token_budget, c._sel, c.page_size, c.flags)
+    return c.topk_dindices_buffer[0]
+
+
+def decode_sparse_attn(q: torch.Tensor, iController: InferenceController, layer_idx: int,
+                       topk_indices: Optional[torch.Tensor],
+                       rope_scale: Optional[float] = None,
+                       rope_theta: Optional[float] = None) -> torch.Tensor:
+    """Attention of q [1, H, D] over the selected pages (reference
+    __init__.py:248-285); dense over all pages when topk_indices is None or
+    ``iController.kv_indices_without_last``."""
+    c = iController
+    dense = topk_indices is None or topk_indices is c.kv_indices_without_last
+    q3 = q.view(1, c.num_heads, c.head_dim)
+    o = torch.empty_like(q3)
+    ops.decode_sparse_attn(
+        q3, o, c.kv_cache.buf_layer(layer_idx), c.kv_indptr_for_append, c.kv_indices_with_last,
+        c.kv_last_page_len_t, None if dense else c._sel, c.token_budget, c.workspace,
+        len(c.kv_cache.indicies), c.num_kv_heads, c.layout)
+    return o.view_as(q)
+
+
+def decode_layer(q: torch.Tensor, iController: InferenceController, layer_idx: int
+                 ) -> torch.Tensor:
+    """estimate + top-k + sparse decode in two launches (fused entry point)."""
+    c = iController
+    q3 = q.view(1, c.num_heads, c.head_dim)
+    o = torch.empty_like(q3)
+    ops.sparse_decode_layer(
+        q3, o, c.kv_cache.buf_layer(layer_idx), c.kv_indptr_for_append, c.kv_indices_with_last,
+        c.kv_last_page_len_t, c.metadata_cache.buf_layer(layer_idx),
+        c.metadata_indptr_for_append, c.metadata_indices, c.v_log_norm_layer(layer_idx),
+        c.scores, c._sel, c.token_budget, c.workspace, len(c.kv_cache.indicies), c.layout,
+        c.flags)
+    return o.view_as(q)

@@ -1,0 +1,143 @@
+"""InferenceController: host planner of the paged cache for one sequence.
+
+Mirrors the reference's InferenceController (kernels/aoa_kv/quest/utils/
+controller.py:7-164): the same attributes and call order
+(prepare_metadata -> begin_forward -> ops -> end_forward), so a driver can
+switch trees.  Differences, by design:
+
+* selection follows the simulation (every page scored, fixed forcing of the
+  first and last page, k = min(max(3, min(L, budget)/page), P));
+* the decode workspace is allocated once, not per begin_forward, and no op
+  synchronises with the host;
+* scores are fp32 and the per-page value statistic is written for every
+  page, with the page mean of V kept in ``v_mean`` for the running mean.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from .. import ops
+from .kv_cache import KvCache
+from .utils import TensorLayout
+
+
+class InferenceController:
+    def __init__(self, num_layers, num_heads, head_dim, page_size, page_budget, max_seq_len,
+                 dtype, device, layout: int = TensorLayout.HND,
+                 num_kv_heads: Optional[int] = None, fixed: bool = True,
+                 value_aware: bool = True, shuffle_seed: Optional[int] = None):
+        if dtype != torch.float16:
+            raise TypeError("only float16 caches are supported")
+        self.num_layers = num_layers
+        self.num_heads = num_heads
+        self.num_kv_heads = num_kv_heads or num_heads
+        self.head_dim = head_dim
+        self.page_size = page_size
+        self.layout = layout
+        self.device = torch.device(device)
+        self.dtype = dtype
+        self.fixed = fixed
+        self.value_aware = value_aware
+
+        max_kv_pages = (max_seq_len + page_size - 1) // page_size
+        self.max_kv_pages = max_kv_pages
+        self.kv_cache = KvCache(num_layers, self.num_kv_heads, head_dim, max_seq_len, page_size,
+                                dtype, device, layout, shuffle_seed)
+        self.metadata_cache = KvCache(num_layers, self.num_kv_heads, head_dim, max_kv_pages,
+                                      page_size, dtype, device, layout,
+                                      None if shuffle_seed is None else shuffle_seed + 1)
+        # log-norm of the page mean of V per (layer, physical page, kv head)
+        # (reference controller.py:43-47) and the page means themselves
+        self.v_log_norm = torch.zeros((num_layers, max_kv_pages, self.num_kv_heads), dtype=dtype,
+                                      device=device)
+        self.v_mean = torch.zeros((num_layers, max_kv_pages, self.num_kv_heads, head_dim),
+                                  dtype=dtype, device=device)
+
+        self._page_budget = page_budget
+        self.inference_page_budget = None
+
+        self.kv_indices_with_last = None
+        self.kv_indices_without_last = None
+        self.metadata_indices = None
+        self.kv_last_page_idx = None
+        self.metadata_last_page_idx = None
+        self.kv_indptr_for_append = None
+        self.metadata_indptr_for_append = None
+        self.kv_last_page_len_t = None
+
+        # fixed-size decode buffers (one layer at a time)
+        self.scores = torch.empty((1, self.num_kv_heads, max_kv_pages), dtype=torch.float32,
+                                  device=device)
+        self.topk_dindices_buffer = None
+        self._sel = torch.empty((1, self.num_kv_heads, max_kv_pages), dtype=torch.int32,
+                                device=device)
+        self.workspace = ops.decode_workspace(1, num_heads, self.num_kv_heads, max_kv_pages,
+                                              device)
+
+    # ------------------------------------------------------------ budget
+    @property
+    def token_budget(self) -> int:
+        return self._page_budget * self.page_size
+
+    def set_page_budget(self, page_budget: int):
+        self._page_budget = page_budget
+
+    @property
+    def flags(self) -> int:
+        return ((ops.FLAG_VALUE_AWARE if self.value_aware else 0) |
+                (ops.FLAG_FIXED if self.fixed else 0))
+
+    # ------------------------------------------------------------ planning
+    def prepare_metadata(self, seq_len: int):
+        """Reserve cache slots for seq_len new tokens (controller.py:84-88)."""
+        new_pages = self.kv_cache.append_seq(seq_len)
+        self.metadata_cache.append_seq(new_pages)
+
+    def begin_forward(self, seq_len: int, updateTensor: bool = True):
+        """Upload the page tables for the coming ops (controller.py:92-141)."""
+        kv = self.kv_cache.indicies
+        md = self.metadata_cache.indicies
+        if updateTensor:
+            dev = self.device
+            self.kv_indices_with_last = torch.tensor(kv, dtype=torch.int32, device=dev)
+            self.metadata_indices = torch.tensor(md, dtype=torch.int32, device=dev)
+            self.kv_indptr_for_append = torch.tensor([0, len(kv)], dtype=torch.int32, device=dev)
+            self.metadata_indptr_for_append = torch.tensor([0, len(md)], dtype=torch.int32,
+                                                           device=dev)
+            self.kv_last_page_len_t = torch.tensor([self.kv_cache.last_page_len],
+                                                   dtype=torch.int32, device=dev)
+            self.kv_last_page_idx = kv[-1]
+            self.metadata_last_page_idx = md[-1]
+            self.kv_indices_without_last = self.kv_indices_with_last[:-1].repeat(self.num_heads, 1)
+        if seq_len == 1:
+            P = len(kv)
+            self.inference_page_budget = min(self._page_budget, P)
+            k = self.num_selected_pages()
+            self.topk_dindices_buffer = self._sel[:, :, :k]
+
+    def end_forward(self):
+        pass
+
+    def need_estimate(self) -> bool:
+        """True when the sequence has more pages than the page budget."""
+        if self.inference_page_budget is None:
+            return False
+        return len(self.kv_cache.indicies) > self.inference_page_budget
+
+    def num_selected_pages(self) -> int:
+        """k of the simulation's rule (filter_util.py:373)."""
+        L = self.kv_cache.seqlen
+        P = len(self.kv_cache.indicies)
+        return min(max(3, min(L, self.token_budget) // self.page_size), P)
+
+    def clean_states(self):
+        self.kv_cache.release()
+        self.metadata_cache.release()
+
+    def v_log_norm_layer(self, layer_idx: int):
+        return self.v_log_norm[layer_idx]
+
+    def v_mean_layer(self, layer_idx: int):
+        return self.v_mean[layer_idx]

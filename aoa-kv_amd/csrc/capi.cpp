@@ -1,0 +1,412 @@
+// extern "C" boundary of libaoakv.so (declared in include/aoakv.h).
+//
+// Each entry point validates its arguments on the host (shapes the kernels
+// assume, null pointers, budgets), then launches on the caller's stream.
+// Nothing here allocates device memory or synchronises.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/aoakv.h"
+#include "kernels.hpp"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int ok() {
+  g_err.clear();
+  return AOAKV_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(AOAKV_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+#define REQUIRE(cond, ...)                                  \
+  do {                                                      \
+    if (!(cond)) return fail(AOAKV_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+int check_shape(uint32_t head_dim, uint32_t page_size, uint32_t layout, uint32_t num_heads) {
+  if (head_dim != (uint32_t)aoakv::kHeadDim)
+    return fail(AOAKV_ERR_UNSUPPORTED, "head_dim %u unsupported (only 128)", head_dim);
+  if (page_size != (uint32_t)aoakv::kPageSize)
+    return fail(AOAKV_ERR_UNSUPPORTED, "page_size %u unsupported (only 16)", page_size);
+  if (layout > 1u) return fail(AOAKV_ERR_UNSUPPORTED, "layout %u unknown (0=NHD, 1=HND)", layout);
+  if (num_heads == 0u || num_heads > 256u)
+    return fail(AOAKV_ERR_UNSUPPORTED, "num_heads %u out of range [1, 256]", num_heads);
+  return AOAKV_OK;
+}
+
+int check_group(uint32_t hq, uint32_t hkv) {
+  if (hkv == 0u || hq % hkv != 0u)
+    return fail(AOAKV_ERR_INVALID, "num_qo_heads %u not a multiple of num_kv_heads %u", hq, hkv);
+  uint32_t g = hq / hkv;
+  if (g != 1u && g != 2u && g != 4u && g != 8u)
+    return fail(AOAKV_ERR_UNSUPPORTED, "GQA group size %u unsupported (1, 2, 4, 8)", g);
+  return AOAKV_OK;
+}
+
+struct Workspace {
+  uint32_t* est_counters;
+  uint32_t* dec_counters;
+  float* partial;
+  size_t bytes;
+};
+
+size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// [est counters: B*Hkv u32][dec counters: B*Hq u32][partials: B*Hq*chunks*stride f32]
+size_t ws_layout(uint32_t B, uint32_t hq, uint32_t hkv, uint32_t max_sel_pages, void* base,
+                 Workspace* w) {
+  size_t off_dec = round_up((size_t)B * hkv * 4u, 256);
+  size_t off_part = off_dec + round_up((size_t)B * hq * 4u, 256);
+  size_t part = (size_t)B * hq * aoakv::decode_chunks(max_sel_pages) * aoakv::partial_stride() * 4u;
+  size_t total = off_part + round_up(part, 256);
+  if (w) {
+    char* c = static_cast<char*>(base);
+    w->est_counters = reinterpret_cast<uint32_t*>(c);
+    w->dec_counters = reinterpret_cast<uint32_t*>(c + off_dec);
+    w->partial = reinterpret_cast<float*>(c + off_part);
+    w->bytes = total;
+  }
+  return total;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* aoakv_last_error(void) { return g_err.c_str(); }
+
+const char* aoakv_version(void) { return "aoakv-mi355x 0.1 (gfx950)"; }
+
+int aoakv_append_kv_cache_prefill(const void* k, const void* v, uint32_t num_new_tokens,
+                                  void* kv_data, const int32_t* kv_indices,
+                                  uint32_t num_kv_pages, uint32_t kv_last_page_len,
+                                  void* metadata_data, const int32_t* metadata_indices,
+                                  void* v_log_norm, void* v_mean, uint32_t num_heads,
+                                  uint32_t head_dim, uint32_t page_size, uint32_t layout,
+                                  void* stream) {
+  if (int e = check_shape(head_dim, page_size, layout, num_heads)) return e;
+  REQUIRE(k && v && kv_data && kv_indices && metadata_data && metadata_indices && v_log_norm &&
+              v_mean,
+          "append_kv_cache_prefill: null pointer argument");
+  REQUIRE(num_kv_pages >= 1u, "append_kv_cache_prefill: num_kv_pages must be >= 1");
+  REQUIRE(kv_last_page_len >= 1u && kv_last_page_len <= page_size,
+          "append_kv_cache_prefill: kv_last_page_len %u not in [1, %u]", kv_last_page_len,
+          page_size);
+  const uint64_t L = (uint64_t)(num_kv_pages - 1u) * page_size + kv_last_page_len;
+  REQUIRE(num_new_tokens >= 1u && num_new_tokens <= L,
+          "append_kv_cache_prefill: %u new tokens but the cache holds %llu", num_new_tokens,
+          (unsigned long long)L);
+  aoakv::AppendPrefillArgs a{};
+  a.k = static_cast<const aoakv::f16*>(k);
+  a.v = static_cast<const aoakv::f16*>(v);
+  a.kv = static_cast<aoakv::f16*>(kv_data);
+  a.kv_indices = kv_indices;
+  a.meta = static_cast<aoakv::f16*>(metadata_data);
+  a.meta_indices = metadata_indices;
+  a.v_log_norm = static_cast<aoakv::f16*>(v_log_norm);
+  a.v_mean = static_cast<aoakv::f16*>(v_mean);
+  a.N = num_new_tokens;
+  a.H = num_heads;
+  a.S = page_size;
+  a.num_pages = num_kv_pages;
+  a.last_page_len = kv_last_page_len;
+  a.g = aoakv::make_geom(layout, num_heads, page_size, head_dim);
+  return hip_status(aoakv::launch_append_prefill(a, static_cast<hipStream_t>(stream)),
+                    "append_kv_cache_prefill");
+}
+
+int aoakv_append_kv_cache_decode(const void* k, const void* v, uint32_t batch_size,
+                                 void* kv_data, const int32_t* kv_indptr,
+                                 const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                                 void* metadata_data, const int32_t* metadata_indptr,
+                                 const int32_t* metadata_indices, void* v_log_norm,
+                                 void* v_mean, uint32_t num_heads, uint32_t head_dim,
+                                 uint32_t page_size, uint32_t layout, void* stream) {
+  if (int e = check_shape(head_dim, page_size, layout, num_heads)) return e;
+  REQUIRE(k && v && kv_data && kv_indptr && kv_indices && kv_last_page_len && metadata_data &&
+              metadata_indptr && metadata_indices && v_log_norm && v_mean,
+          "append_kv_cache_decode: null pointer argument");
+  REQUIRE(batch_size >= 1u && batch_size <= 65535u,
+          "append_kv_cache_decode: batch_size %u out of range", batch_size);
+  aoakv::AppendDecodeArgs a{};
+  a.k = static_cast<const aoakv::f16*>(k);
+  a.v = static_cast<const aoakv::f16*>(v);
+  a.kv = static_cast<aoakv::f16*>(kv_data);
+  a.kv_indptr = kv_indptr;
+  a.kv_indices = kv_indices;
+  a.kv_last_page_len = kv_last_page_len;
+  a.meta = static_cast<aoakv::f16*>(metadata_data);
+  a.meta_indptr = metadata_indptr;
+  a.meta_indices = metadata_indices;
+  a.v_log_norm = static_cast<aoakv::f16*>(v_log_norm);
+  a.v_mean = static_cast<aoakv::f16*>(v_mean);
+  a.H = num_heads;
+  a.S = page_size;
+  a.g = aoakv::make_geom(layout, num_heads, page_size, head_dim);
+  return hip_status(aoakv::launch_append_decode(a, batch_size, static_cast<hipStream_t>(stream)),
+                    "append_kv_cache_decode");
+}
+
+static int fill_estimate(aoakv::EstimateArgs& a, const void* q, float* scores,
+                         uint32_t score_stride, const void* metadata_data,
+                         const int32_t* metadata_indptr, const int32_t* metadata_indices,
+                         const int32_t* kv_indptr, const int32_t* kv_indices,
+                         const int32_t* kv_last_page_len, const void* v_log_norm,
+                         uint32_t batch_size, uint32_t max_pages, uint32_t num_qo_heads,
+                         uint32_t num_kv_heads, uint32_t head_dim, uint32_t page_size,
+                         uint32_t layout, uint32_t flags) {
+  if (int e = check_shape(head_dim, page_size, layout, num_qo_heads)) return e;
+  if (int e = check_group(num_qo_heads, num_kv_heads)) return e;
+  REQUIRE(q && scores && metadata_data && metadata_indptr && metadata_indices && kv_indptr &&
+              kv_indices && kv_last_page_len,
+          "estimate_attn_score: null pointer argument");
+  REQUIRE(!(flags & AOAKV_FLAG_VALUE_AWARE) || v_log_norm,
+          "estimate_attn_score: value-aware scoring needs v_log_norm");
+  REQUIRE(batch_size >= 1u && batch_size <= 65535u, "estimate_attn_score: bad batch_size %u",
+          batch_size);
+  REQUIRE(max_pages >= 1u && score_stride >= max_pages,
+          "estimate_attn_score: score_stride %u < max_pages %u", score_stride, max_pages);
+  REQUIRE((flags & ~3u) == 0u, "estimate_attn_score: unknown flags 0x%x", flags);
+  a.q = static_cast<const aoakv::f16*>(q);
+  a.scores = scores;
+  a.score_stride = score_stride;
+  a.meta = static_cast<const aoakv::f16*>(metadata_data);
+  a.meta_indptr = metadata_indptr;
+  a.meta_indices = metadata_indices;
+  a.kv_indptr = kv_indptr;
+  a.kv_indices = kv_indices;
+  a.kv_last_page_len = kv_last_page_len;
+  a.v_log_norm = static_cast<const aoakv::f16*>(v_log_norm);
+  a.Hq = num_qo_heads;
+  a.Hkv = num_kv_heads;
+  a.S = page_size;
+  a.flags = flags;
+  a.g = aoakv::make_geom(layout, num_kv_heads, page_size, head_dim);
+  return AOAKV_OK;
+}
+
+int aoakv_estimate_attn_score(const void* q, float* scores, uint32_t score_stride,
+                              const void* metadata_data, const int32_t* metadata_indptr,
+                              const int32_t* metadata_indices, const int32_t* kv_indptr,
+                              const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                              const void* v_log_norm, uint32_t batch_size, uint32_t max_pages,
+                              uint32_t num_qo_heads, uint32_t num_kv_heads, uint32_t head_dim,
+                              uint32_t page_size, uint32_t layout, uint32_t flags,
+                              void* stream) {
+  aoakv::EstimateArgs a{};
+  if (int e = fill_estimate(a, q, scores, score_stride, metadata_data, metadata_indptr,
+                            metadata_indices, kv_indptr, kv_indices, kv_last_page_len,
+                            v_log_norm, batch_size, max_pages, num_qo_heads, num_kv_heads,
+                            head_dim, page_size, layout, flags))
+    return e;
+  return hip_status(
+      aoakv::launch_estimate(a, batch_size, max_pages, static_cast<hipStream_t>(stream)),
+      "estimate_attn_score");
+}
+
+int aoakv_topk_filtering(const float* scores, uint32_t score_stride,
+                         const int32_t* kv_indptr, const int32_t* kv_indices,
+                         const int32_t* kv_last_page_len, uint32_t token_budget,
+                         const int32_t* token_budgets, int32_t* sel_pages, uint32_t sel_stride,
+                         uint32_t batch_size, uint32_t num_kv_heads, uint32_t page_size,
+                         uint32_t flags, void* stream) {
+  REQUIRE(scores && kv_indptr && kv_indices && kv_last_page_len && sel_pages,
+          "topk_filtering: null pointer argument");
+  REQUIRE(page_size == (uint32_t)aoakv::kPageSize, "topk_filtering: page_size %u unsupported",
+          page_size);
+  REQUIRE(batch_size >= 1u && batch_size <= 65535u && num_kv_heads >= 1u &&
+              num_kv_heads <= 65535u,
+          "topk_filtering: bad batch_size %u / num_kv_heads %u", batch_size, num_kv_heads);
+  REQUIRE(sel_stride >= 3u, "topk_filtering: sel_stride %u < 3", sel_stride);
+  REQUIRE((flags & ~3u) == 0u, "topk_filtering: unknown flags 0x%x", flags);
+  aoakv::TopkArgs a{};
+  a.scores = scores;
+  a.score_stride = score_stride;
+  a.kv_indptr = kv_indptr;
+  a.kv_indices = kv_indices;
+  a.kv_last_page_len = kv_last_page_len;
+  a.token_budget = token_budget;
+  a.token_budgets = token_budgets;
+  a.sel = sel_pages;
+  a.sel_stride = sel_stride;
+  a.Hkv = num_kv_heads;
+  a.S = page_size;
+  a.flags = flags;
+  return hip_status(aoakv::launch_topk(a, batch_size, static_cast<hipStream_t>(stream)),
+                    "topk_filtering");
+}
+
+size_t aoakv_decode_workspace_size(uint32_t batch_size, uint32_t num_qo_heads,
+                                   uint32_t num_kv_heads, uint32_t head_dim,
+                                   uint32_t max_sel_pages) {
+  (void)head_dim;
+  return ws_layout(batch_size, num_qo_heads, num_kv_heads, max_sel_pages, nullptr, nullptr);
+}
+
+int aoakv_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
+  REQUIRE(workspace, "workspace_init: null workspace");
+  REQUIRE(workspace_bytes % 4u == 0u, "workspace_init: size not a multiple of 4");
+  return hip_status(aoakv::launch_fill_u32(static_cast<uint32_t*>(workspace),
+                                           workspace_bytes / 4u, 0u,
+                                           static_cast<hipStream_t>(stream)),
+                    "workspace_init");
+}
+
+static int fill_decode(aoakv::DecodeArgs& a, Workspace& w, const void* q, void* o,
+                       const void* kv_data, const int32_t* kv_indptr,
+                       const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                       const int32_t* sel_pages, uint32_t sel_stride, uint32_t token_budget,
+                       const int32_t* token_budgets, void* workspace, size_t workspace_bytes,
+                       uint32_t batch_size, uint32_t max_pages, uint32_t num_qo_heads,
+                       uint32_t num_kv_heads, uint32_t head_dim, uint32_t page_size,
+                       uint32_t layout) {
+  if (int e = check_shape(head_dim, page_size, layout, num_qo_heads)) return e;
+  if (int e = check_group(num_qo_heads, num_kv_heads)) return e;
+  REQUIRE(q && o && kv_data && kv_indptr && kv_indices && kv_last_page_len && workspace,
+          "decode_sparse_attn: null pointer argument");
+  REQUIRE(batch_size >= 1u && batch_size <= 65535u, "decode_sparse_attn: bad batch_size %u",
+          batch_size);
+  REQUIRE(max_pages >= 1u, "decode_sparse_attn: max_pages must be >= 1");
+  const uint32_t max_sel = sel_pages ? (sel_stride < max_pages ? sel_stride : max_pages) : max_pages;
+  REQUIRE(!sel_pages || sel_stride >= 3u, "decode_sparse_attn: sel_stride %u < 3", sel_stride);
+  const size_t need = ws_layout(batch_size, num_qo_heads, num_kv_heads, max_sel, workspace, &w);
+  REQUIRE(workspace_bytes >= need, "decode_sparse_attn: workspace of %zu bytes < %zu needed",
+          workspace_bytes, need);
+  a.q = static_cast<const aoakv::f16*>(q);
+  a.o = static_cast<aoakv::f16*>(o);
+  a.kv = static_cast<const aoakv::f16*>(kv_data);
+  a.kv_indptr = kv_indptr;
+  a.kv_indices = kv_indices;
+  a.kv_last_page_len = kv_last_page_len;
+  a.sel = sel_pages;
+  a.sel_stride = sel_stride;
+  a.token_budget = token_budget;
+  a.token_budgets = token_budgets;
+  a.partial = w.partial;
+  a.counters = w.dec_counters;
+  a.Hq = num_qo_heads;
+  a.Hkv = num_kv_heads;
+  a.S = page_size;
+  a.max_chunks = aoakv::decode_chunks(max_sel);
+  a.g = aoakv::make_geom(layout, num_kv_heads, page_size, head_dim);
+  return AOAKV_OK;
+}
+
+int aoakv_decode_sparse_attn(const void* q, void* o, const void* kv_data,
+                             const int32_t* kv_indptr, const int32_t* kv_indices,
+                             const int32_t* kv_last_page_len, const int32_t* sel_pages,
+                             uint32_t sel_stride, uint32_t token_budget,
+                             const int32_t* token_budgets, void* workspace,
+                             size_t workspace_bytes, uint32_t batch_size, uint32_t max_pages,
+                             uint32_t num_qo_heads, uint32_t num_kv_heads, uint32_t head_dim,
+                             uint32_t page_size, uint32_t layout, void* stream) {
+  aoakv::DecodeArgs a{};
+  Workspace w{};
+  if (int e = fill_decode(a, w, q, o, kv_data, kv_indptr, kv_indices, kv_last_page_len,
+                          sel_pages, sel_stride, token_budget, token_budgets, workspace,
+                          workspace_bytes, batch_size, max_pages, num_qo_heads, num_kv_heads,
+                          head_dim, page_size, layout))
+    return e;
+  return hip_status(aoakv::launch_decode(a, batch_size, static_cast<hipStream_t>(stream)),
+                    "decode_sparse_attn");
+}
+
+int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
+                              const int32_t* kv_indptr, const int32_t* kv_indices,
+                              const int32_t* kv_last_page_len, const void* metadata_data,
+                              const int32_t* metadata_indptr, const int32_t* metadata_indices,
+                              const void* v_log_norm, float* scores, uint32_t score_stride,
+                              int32_t* sel_pages, uint32_t sel_stride, uint32_t token_budget,
+                              const int32_t* token_budgets, void* workspace,
+                              size_t workspace_bytes, uint32_t batch_size, uint32_t max_pages,
+                              uint32_t num_qo_heads, uint32_t num_kv_heads, uint32_t head_dim,
+                              uint32_t page_size, uint32_t layout, uint32_t flags,
+                              void* stream) {
+  REQUIRE(sel_pages, "sparse_decode_layer: sel_pages is required");
+  aoakv::EstimateArgs ea{};
+  if (int e = fill_estimate(ea, q, scores, score_stride, metadata_data, metadata_indptr,
+                            metadata_indices, kv_indptr, kv_indices, kv_last_page_len,
+                            v_log_norm, batch_size, max_pages, num_qo_heads, num_kv_heads,
+                            head_dim, page_size, layout, flags))
+    return e;
+  aoakv::DecodeArgs da{};
+  Workspace w{};
+  if (int e = fill_decode(da, w, q, o, kv_data, kv_indptr, kv_indices, kv_last_page_len,
+                          sel_pages, sel_stride, token_budget, token_budgets, workspace,
+                          workspace_bytes, batch_size, max_pages, num_qo_heads, num_kv_heads,
+                          head_dim, page_size, layout))
+    return e;
+  ea.sel = sel_pages;
+  ea.sel_stride = sel_stride;
+  ea.token_budget = token_budget;
+  ea.token_budgets = token_budgets;
+  ea.counters = w.est_counters;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (int e = hip_status(aoakv::launch_estimate(ea, batch_size, max_pages, s),
+                         "sparse_decode_layer/estimate"))
+    return e;
+  return hip_status(aoakv::launch_decode(da, batch_size, s), "sparse_decode_layer/decode");
+}
+
+int aoakv_estimate_topk(const void* q, const void* metadata_data, const int32_t* metadata_indptr,
+                        const int32_t* metadata_indices, const int32_t* kv_indptr,
+                        const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                        const void* v_log_norm, float* scores, uint32_t score_stride,
+                        int32_t* sel_pages, uint32_t sel_stride, uint32_t token_budget,
+                        const int32_t* token_budgets, void* workspace, size_t workspace_bytes,
+                        uint32_t batch_size, uint32_t max_pages, uint32_t num_qo_heads,
+                        uint32_t num_kv_heads, uint32_t head_dim, uint32_t page_size,
+                        uint32_t layout, uint32_t flags, void* stream) {
+  REQUIRE(sel_pages && workspace, "estimate_topk: sel_pages and workspace are required");
+  REQUIRE(sel_stride >= 3u, "estimate_topk: sel_stride %u < 3", sel_stride);
+  aoakv::EstimateArgs ea{};
+  if (int e = fill_estimate(ea, q, scores, score_stride, metadata_data, metadata_indptr,
+                            metadata_indices, kv_indptr, kv_indices, kv_last_page_len,
+                            v_log_norm, batch_size, max_pages, num_qo_heads, num_kv_heads,
+                            head_dim, page_size, layout, flags))
+    return e;
+  Workspace w{};
+  const uint32_t max_sel = sel_stride < max_pages ? sel_stride : max_pages;
+  const size_t need = ws_layout(batch_size, num_qo_heads, num_kv_heads, max_sel, workspace, &w);
+  REQUIRE(workspace_bytes >= need, "estimate_topk: workspace of %zu bytes < %zu needed",
+          workspace_bytes, need);
+  ea.sel = sel_pages;
+  ea.sel_stride = sel_stride;
+  ea.token_budget = token_budget;
+  ea.token_budgets = token_budgets;
+  ea.counters = w.est_counters;
+  return hip_status(
+      aoakv::launch_estimate(ea, batch_size, max_pages, static_cast<hipStream_t>(stream)),
+      "estimate_topk");
+}
+
+int aoakv_prefill_with_paged_kv_cache(const void* q, void* o, const void* kv_data,
+                                      const int32_t* kv_indices, uint32_t num_kv_pages,
+                                      uint32_t kv_last_page_len, uint32_t qo_len,
+                                      uint32_t causal, uint32_t num_heads, uint32_t head_dim,
+                                      uint32_t page_size, uint32_t layout, void* stream) {
+  (void)q; (void)o; (void)kv_data; (void)kv_indices; (void)num_kv_pages;
+  (void)kv_last_page_len; (void)qo_len; (void)causal; (void)num_heads; (void)head_dim;
+  (void)page_size; (void)layout; (void)stream;
+  return fail(AOAKV_ERR_UNSUPPORTED, "prefill_with_paged_kv_cache: not built yet");
+}
+
+}  // extern "C"

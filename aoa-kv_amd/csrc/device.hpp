@@ -1,0 +1,176 @@
+// Device-side helpers shared by the libaoakv kernels (gfx950 / CDNA4).
+//
+// Wave = 64 lanes.  A 128-dim fp16 row is 256 B = 16 lanes x 16 B, so most
+// kernels view a wave as four 16-lane "rows" (the DPP row of the hardware),
+// each row owning one (page or token, head) vector: lane l holds dims
+// [8*(l%16), 8*(l%16)+8).  Reductions inside a row use DPP; across rows a
+// wave shuffle.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace aoakv {
+
+using f16 = _Float16;
+
+constexpr int kWave = 64;
+constexpr int kHeadDim = 128;
+constexpr int kPageSize = 16;
+constexpr int kLanesPerRow = 16;   // lanes covering one 128-dim fp16 vector
+constexpr int kVec = 8;            // fp16 elements per lane per vector
+
+// sqrt(128) rounded to fp32: the simulation divides by math.sqrt(head_dim)
+// as an fp32 true division (filter_util.py:329, quest_attention.py:268).
+constexpr float kSqrtHeadDim = 11.313708498984761f;
+
+struct alignas(16) H8 {
+  f16 v[8];
+};
+
+// ---------------------------------------------------------------- layout
+
+// Element strides inside one page of a paged cache.
+struct PageGeom {
+  uint32_t page, kv, head, tok;
+};
+
+__host__ __device__ inline PageGeom make_geom(uint32_t layout, uint32_t H, uint32_t S,
+                                              uint32_t D) {
+  PageGeom g;
+  g.page = 2u * S * H * D;
+  g.kv = S * H * D;
+  if (layout == 0u) {  // NHD: [2][S][H][D]
+    g.tok = H * D;
+    g.head = D;
+  } else {  // HND: [2][H][S][D]
+    g.head = S * D;
+    g.tok = D;
+  }
+  return g;
+}
+
+__device__ inline size_t elem_off(const PageGeom& g, uint32_t page, uint32_t kv, uint32_t head,
+                                  uint32_t tok) {
+  return (size_t)page * g.page + (size_t)kv * g.kv + (size_t)head * g.head +
+         (size_t)tok * g.tok;
+}
+
+// ---------------------------------------------------------------- loads/stores
+
+__device__ inline H8 ld16(const f16* p) {
+  uint4 u = *reinterpret_cast<const uint4*>(p);
+  return __builtin_bit_cast(H8, u);
+}
+__device__ inline void st16(f16* p, const H8& x) {
+  *reinterpret_cast<uint4*>(p) = __builtin_bit_cast(uint4, x);
+}
+
+// ---------------------------------------------------------------- DPP / shuffles
+
+template <int CTRL>
+__device__ inline float dpp(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+
+// DPP controls: quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror.
+constexpr int kQuadSwap1 = 0xB1;
+constexpr int kQuadSwap2 = 0x4E;
+constexpr int kRowHalfMirror = 0x141;
+constexpr int kRowMirror = 0x140;
+
+// Sum over the 16 lanes of a DPP row; every lane of the row gets the sum.
+__device__ inline float row_sum16(float x) {
+  x = x + dpp<kQuadSwap1>(x);
+  x = x + dpp<kQuadSwap2>(x);
+  x = x + dpp<kRowHalfMirror>(x);
+  x = x + dpp<kRowMirror>(x);
+  return x;
+}
+
+__device__ inline float row_max16(float x) {
+  x = fmaxf(x, dpp<kQuadSwap1>(x));
+  x = fmaxf(x, dpp<kQuadSwap2>(x));
+  x = fmaxf(x, dpp<kRowHalfMirror>(x));
+  x = fmaxf(x, dpp<kRowMirror>(x));
+  return x;
+}
+
+// Across the four rows of a wave (lanes l, l^16, l^32, l^48).
+__device__ inline float cross_row_sum(float x) {
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+__device__ inline float cross_row_max(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16));
+  x = fmaxf(x, __shfl_xor(x, 32));
+  return x;
+}
+
+// ---------------------------------------------------------------- fp16 arithmetic
+// The reference simulation runs fp16 tensors through torch's CPU kernels:
+// every elementwise op is computed in fp32 and rounded once to fp16 (RNE).
+// These helpers reproduce that; the library is compiled with
+// -ffp-contract=off so no multiply-add is fused across a rounding point.
+
+__device__ inline f16 r16(float x) { return (f16)x; }
+
+// update_mean_filter (filter_util.py:669-679): (m*n + v)/(n+1), each of the
+// three fp16 ops rounded to fp16.  n is the number of tokens already in the
+// page.
+__device__ inline f16 running_mean(f16 m, f16 v, uint32_t n) {
+  f16 t = r16((float)m * (float)n);
+  t = r16((float)t + (float)v);
+  return r16((float)t / (float)(n + 1u));
+}
+
+// log(norm(V̄) + 1e-8) of one 128-dim fp16 vector held by a 16-lane row
+// (8 dims per lane, lane order = dim order), as torch computes it on fp16
+// (filter_util.py:325):
+//   norm: fp32 sum of squares in dim order 0..127, sqrtf, round to fp16;
+//   + 1e-8: fp16 op (leaves every fp16 value unchanged; kept for clarity);
+//   log: correctly rounded fp32 log (via fp64), rounded to fp16.
+// The sequential fp32 chain is carried lane to lane across the row.
+// Returns the fp16 log-norm in every lane of the row.
+__device__ inline f16 log_norm_row(const H8& vbar, uint32_t lane16) {
+  float acc = 0.f;
+#pragma unroll
+  for (int src = 0; src < kLanesPerRow; ++src) {
+    if ((int)lane16 == src) {
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) {
+        float x = (float)vbar.v[j];
+        float sq = x * x;
+        acc = acc + sq;
+      }
+    }
+    // hand the running sum to the next lane of the row
+    acc = __shfl(acc, (int)((__lane_id() & ~15u) | (uint32_t)src), kWave);
+  }
+  f16 nrm = r16(__fsqrt_rn(acc));
+  nrm = r16((float)nrm + 1e-8f);
+  double ln = log((double)(float)nrm);
+  return r16((float)ln);
+}
+
+// Map an fp32 score to a uint32 key with the same order (larger float ->
+// larger key).  -0.0 and +0.0 map to adjacent keys (torch.topk treats them
+// as equal; scores of exactly zero with both signs do not arise).
+__device__ inline uint32_t order_key(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// k = min(max(3, min(L, budget) / page_size), P)  (filter_util.py:373,
+// quest_attention.py:326).
+__host__ __device__ inline uint32_t num_selected_pages(uint32_t L, uint32_t budget,
+                                                       uint32_t page_size, uint32_t P) {
+  uint32_t tb = L < budget ? L : budget;
+  uint32_t k = tb / page_size;
+  if (k < 3u) k = 3u;
+  return k < P ? k : P;
+}
+
+}  // namespace aoakv

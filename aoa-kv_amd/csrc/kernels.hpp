@@ -1,0 +1,99 @@
+// Kernel argument blocks and launchers shared by the HIP translation units
+// and the C ABI (capi.cpp).
+#pragma once
+
+#include "device.hpp"
+
+namespace aoakv {
+
+struct AppendPrefillArgs {
+  const f16* k;            // [N, H, D]
+  const f16* v;            // [N, H, D]
+  f16* kv;                 // paged cache of the layer
+  const int32_t* kv_indices;
+  f16* meta;               // metadata cache of the layer
+  const int32_t* meta_indices;
+  f16* v_log_norm;         // [max_pages, H]
+  f16* v_mean;             // [max_pages, H, D]
+  uint32_t N, H, S, num_pages, last_page_len, first_page;
+  PageGeom g;
+};
+
+struct AppendDecodeArgs {
+  const f16* k;  // [B, H, D]
+  const f16* v;
+  f16* kv;
+  const int32_t* kv_indptr;
+  const int32_t* kv_indices;
+  const int32_t* kv_last_page_len;
+  f16* meta;
+  const int32_t* meta_indptr;
+  const int32_t* meta_indices;
+  f16* v_log_norm;
+  f16* v_mean;
+  uint32_t H, S;
+  PageGeom g;
+};
+
+struct EstimateArgs {
+  const f16* q;  // [B, Hq, D]
+  float* scores; // [B, Hkv, score_stride]
+  uint32_t score_stride;
+  const f16* meta;
+  const int32_t* meta_indptr;
+  const int32_t* meta_indices;
+  const int32_t* kv_indptr;
+  const int32_t* kv_indices;
+  const int32_t* kv_last_page_len;
+  const f16* v_log_norm;  // [max_pages, Hkv]
+  uint32_t Hq, Hkv, S, flags;
+  PageGeom g;
+  // fused top-k (sel == nullptr: scores only)
+  int32_t* sel;
+  uint32_t sel_stride;
+  uint32_t token_budget;
+  const int32_t* token_budgets;
+  uint32_t* counters;  // [B * Hkv]
+};
+
+struct TopkArgs {
+  const float* scores;
+  uint32_t score_stride;
+  const int32_t* kv_indptr;
+  const int32_t* kv_indices;
+  const int32_t* kv_last_page_len;
+  uint32_t token_budget;
+  const int32_t* token_budgets;
+  int32_t* sel;
+  uint32_t sel_stride;
+  uint32_t Hkv, S, flags;
+};
+
+struct DecodeArgs {
+  const f16* q;  // [B, Hq, D]
+  f16* o;        // [B, Hq, D]
+  const f16* kv;
+  const int32_t* kv_indptr;
+  const int32_t* kv_indices;
+  const int32_t* kv_last_page_len;
+  const int32_t* sel;  // [B, Hkv, sel_stride] physical ids, or nullptr (dense)
+  uint32_t sel_stride;
+  uint32_t token_budget;
+  const int32_t* token_budgets;
+  float* partial;      // [B*Hq, max_chunks, kPartialStride]
+  uint32_t* counters;  // [B*Hq]
+  uint32_t Hq, Hkv, S, max_chunks;
+  PageGeom g;
+};
+
+hipError_t launch_append_prefill(const AppendPrefillArgs& a, hipStream_t s);
+hipError_t launch_append_decode(const AppendDecodeArgs& a, uint32_t batch, hipStream_t s);
+hipError_t launch_estimate(const EstimateArgs& a, uint32_t batch, uint32_t max_pages,
+                           hipStream_t s);
+hipError_t launch_topk(const TopkArgs& a, uint32_t batch, hipStream_t s);
+hipError_t launch_decode(const DecodeArgs& a, uint32_t batch, hipStream_t s);
+hipError_t launch_fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s);
+uint32_t decode_chunks(uint32_t max_sel_pages);
+uint32_t partial_stride();
+
+}  // namespace aoakv

@@ -1,0 +1,332 @@
+#!/usr/bin/env python3
+"""Benchmark of AOA-KV's sparse decode layer on one MI355X.
+
+Workload: 32 independent layers, each 32 heads x 128 dims fp16, 32768-token
+context in a page-16 paged cache (2048 pages), token budget 2048 -> 128
+pages per head; keys N(0,1) with 4 of 128 channels x8, values N(0,1).  A
+step is one layer's sparse decode: value-aware page scores of all 2048 pages,
+per-head top-k, split-K attention over the selected pages.  The 32 layers
+(2.15 GB of cache+metadata touched per pass, far above the 256 MB MALL) are
+visited round-robin; the 32 launches pairs of a pass are captured in a HIP
+graph and replayed, as a decode loop would run them.
+
+Prints ONE JSON line (rank 0).  Extra measurements (bulk metadata build,
+decode appends, eager launch path, per-kernel times) go under "extra".
+"""
+from __future__ import annotations
+
+import argparse
+import copy
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "aoa-kv_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "sparse decode µs/layer + achieved HBM GB/s @32k ctx, 2048 budget, 1 GPU"
+H, D, S = 32, 128, 16
+L = 32768
+BUDGET = 2048
+P = L // S                      # 2048 pages
+K_SEL = min(max(3, BUDGET // S), P)   # 128
+HBM_PEAK_GBS = 8000.0
+
+# algorithmic bytes per layer (fp16 = 2 B; value statistic 2 B / page / head)
+EST_BYTES = H * P * 2 * D * 2 + H * P * 2 + H * D * 2 + H * K_SEL * 4          # 33,710,080
+DEC_BYTES = H * K_SEL * S * D * 2 * 2 + H * K_SEL * 4 + 2 * H * D * 2          # 33,587,200
+LAYER_BYTES = EST_BYTES + DEC_BYTES                                           # 67,297,280
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def build_layers(n_layers, layout, dev):
+    """Fill n_layers independent paged caches through the library's bulk
+    append (config 3a) and return the buffers plus append timings."""
+    import torch
+    from aoakv import ops
+    Pm = math.ceil(P / S)
+    if layout == ops.HND:
+        kv = torch.empty((n_layers, P, 2, H, S, D), dtype=torch.float16, device=dev)
+        meta = torch.empty((n_layers, Pm, 2, H, S, D), dtype=torch.float16, device=dev)
+    else:
+        kv = torch.empty((n_layers, P, 2, S, H, D), dtype=torch.float16, device=dev)
+        meta = torch.empty((n_layers, Pm, 2, S, H, D), dtype=torch.float16, device=dev)
+    lvn = torch.empty((n_layers, P, H), dtype=torch.float16, device=dev)
+    vmean = torch.empty((n_layers, P, H, D), dtype=torch.float16, device=dev)
+    idx = torch.empty((n_layers, P), dtype=torch.int32, device=dev)
+    midx = torch.arange(Pm, dtype=torch.int32, device=dev)
+    q = torch.empty((n_layers, 1, H, D), dtype=torch.float16, device=dev)
+    times = []
+    for l in range(n_layers):
+        g = torch.Generator(device=dev).manual_seed(l)
+        k = torch.randn((L, H, D), generator=g, device=dev, dtype=torch.float32)
+        ch = torch.randperm(D, generator=torch.Generator().manual_seed(1000 + l))[:4].to(dev)
+        k[:, :, ch] *= 8.0
+        k = k.half()
+        v = torch.randn((L, H, D), generator=g, device=dev, dtype=torch.float32).half()
+        q[l] = torch.randn((1, H, D), generator=g, device=dev, dtype=torch.float32).half()
+        idx[l] = torch.randperm(P, generator=torch.Generator().manual_seed(2000 + l)).to(
+            device=dev, dtype=torch.int32)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        ops.append_kv_cache_prefill(k, v, kv[l], idx[l], P, S, meta[l], midx, lvn[l], vmean[l],
+                                    layout)
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) * 1e3)
+        if l == 0:
+            k0, v0 = k.cpu(), v.cpu()
+        del k, v
+    return dict(kv=kv, meta=meta, lvn=lvn, vmean=vmean, idx=idx, midx=midx, q=q,
+                append_us=times, k0=k0, v0=v0)
+
+
+def decode_appends(dev, layout, n_app=512):
+    """Config 3b: prefill 4096+7 tokens then 512 single-token appends."""
+    import torch
+    from aoakv import ops
+    from aoakv.utils import InferenceController, append_kv
+    c = InferenceController(1, H, D, S, BUDGET // S, 4096 + 7 + n_app + S, torch.float16, dev,
+                            layout=layout)
+    g = torch.Generator(device=dev).manual_seed(1)
+    c.prepare_metadata(4103)
+    c.begin_forward(4103)
+    append_kv(torch.randn((4103, H, D), generator=g, device=dev).half(),
+              torch.randn((4103, H, D), generator=g, device=dev).half(), c, 0)
+    kn = torch.randn((n_app, 1, H, D), generator=g, device=dev).half()
+    vn = torch.randn((n_app, 1, H, D), generator=g, device=dev).half()
+    # device page tables for all steps are prepared up front; the timed loop
+    # is the append kernels only (the host planner's uploads are not timed)
+    steps = []
+    for i in range(n_app):
+        c.prepare_metadata(1)
+        c.begin_forward(1)
+        steps.append((c.kv_indptr_for_append, c.kv_indices_with_last, c.kv_last_page_len_t,
+                      c.metadata_indptr_for_append, c.metadata_indices))
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i, (ip, ix, lp, mip, mix) in enumerate(steps):
+        ops.append_kv_cache_decode(kn[i], vn[i], c.kv_cache.buf_layer(0), ip, ix, lp,
+                                   c.metadata_cache.buf_layer(0), mip, mix, c.v_log_norm[0],
+                                   c.v_mean[0], layout)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / n_app
+
+
+def cpu_baseline(k0, v0, q0, reps):
+    """The oracle's sparse decode of one config-2 layer on the host cores:
+    page scores of all 2048 pages, top-k mask, masked attention over all
+    32768 tokens (as the reference simulation computes it)."""
+    import numpy as np
+    from oracle import sim
+    K = k0.numpy().transpose(1, 0, 2)[None]
+    V = v0.numpy().transpose(1, 0, 2)[None]
+    q = q0.cpu().numpy()[0][:, None, :][None]
+    st = sim.SimLayerState(K, V)
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:
+        threads = 1
+    times = []
+    o = None
+    for r in range(reps + 1):
+        t0 = time.perf_counter()
+        scores, pages = sim.select_pages(copy.copy(st), q, BUDGET, True, True)
+        mask = sim.pages_to_token_mask(pages, S, L)
+        o = sim.masked_decode_attention(q, K, V, mask)
+        t1 = time.perf_counter()
+        if r > 0:
+            times.append(t1 - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return dict(value=med * 1e6, unit="us/layer", cores=int(threads), kind="port",
+                sample=f"layer 0 of config 2 (32 heads, 32768 tokens, budget 2048), "
+                       f"{reps} reps after 1 warmup, median; numpy oracle, BLAS threads={threads}, "
+                       f"os.cpu_count()={os.cpu_count()}, cpu={cpu_model()}",
+                o=o, pages=pages, scores=scores)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3200, help="layers timed (multiple of 32)")
+    ap.add_argument("--warmup", type=int, default=320)
+    ap.add_argument("--layout", choices=["hnd", "nhd"], default="hnd")
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip appends / eager timings")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the AOA-KV decode path "
+                          "is single-GPU (multi-GPU sharding by heads is a design note in "
+                          "DESIGN.md); run with --gpus 1"}))
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    import aoakv
+    from aoakv import ops
+
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    layout = ops.HND if args.layout == "hnd" else ops.NHD
+    n_layers = 32
+    steps = max(n_layers, (args.steps // n_layers) * n_layers)
+    warm = max(n_layers, (args.warmup // n_layers) * n_layers)
+
+    log(f"[bench] {aoakv.version()} layout={args.layout} building {n_layers} layers ...")
+    B = build_layers(n_layers, layout, dev)
+    kv, meta, lvn, idx, midx, q = B["kv"], B["meta"], B["lvn"], B["idx"], B["midx"], B["q"]
+    indptr = torch.tensor([0, P], dtype=torch.int32, device=dev)
+    mindptr = torch.tensor([0, midx.numel()], dtype=torch.int32, device=dev)
+    lpl = torch.tensor([S], dtype=torch.int32, device=dev)
+    scores = torch.zeros((n_layers, 1, H, P), dtype=torch.float32, device=dev)
+    sel = torch.zeros((n_layers, 1, H, K_SEL), dtype=torch.int32, device=dev)
+    o = torch.zeros((n_layers, 1, H, D), dtype=torch.float16, device=dev)
+    ws = ops.decode_workspace(1, H, H, K_SEL, dev)
+    flags = ops.FLAG_VALUE_AWARE | ops.FLAG_FIXED
+
+    def layer(l):
+        ops.sparse_decode_layer(q[l], o[l], kv[l], indptr, idx[l], lpl, meta[l], mindptr, midx,
+                                lvn[l], scores[l], sel[l], BUDGET, ws, P, layout, flags)
+
+    def est(l):
+        ops.estimate_topk(q[l], meta[l], mindptr, midx, indptr, idx[l], lpl, lvn[l], scores[l],
+                          sel[l], BUDGET, ws, P, layout, flags)
+
+    def dec(l):
+        ops.decode_sparse_attn(q[l], o[l], kv[l], indptr, idx[l], lpl, sel[l], BUDGET, ws, P, H,
+                               layout)
+
+    for l in range(n_layers):
+        layer(l)
+    torch.cuda.synchronize()
+
+    def capture(fn):
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for l in range(n_layers):  # one eager pass on the capture stream
+                fn(l)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            for l in range(n_layers):
+                fn(l)
+        torch.cuda.synchronize()
+        return g
+
+    def time_graph(g, reps_layers):
+        reps = reps_layers // n_layers
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (reps * n_layers)  # us per layer
+
+    g_layer = capture(layer)
+    time_graph(g_layer, warm)
+    # replays must reproduce the eager result exactly
+    o_eager = o.clone()
+    sel_eager = sel.clone()
+    g_layer.replay()
+    torch.cuda.synchronize()
+    replay_exact = bool(torch.equal(o, o_eager) and torch.equal(sel, sel_eager))
+
+    log(f"[bench] timing {steps} layers (graph replay) ...")
+    us_layer = time_graph(g_layer, steps)
+    g_est, g_dec = capture(est), capture(dec)
+    time_graph(g_est, warm)
+    time_graph(g_dec, warm)
+    us_est = time_graph(g_est, steps)
+    us_dec = time_graph(g_dec, steps)
+    extra = {}
+    if not args.no_extra:
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for i in range(steps):
+            layer(i % n_layers)
+        t1.record()
+        torch.cuda.synchronize()
+        extra["eager_us_per_layer"] = round(t0.elapsed_time(t1) * 1e3 / steps, 3)
+        app = B["append_us"][1:]
+        app_bytes = 2 * L * H * D * 2 * 2 + H * P * 2 * D * 2 + H * P * 2 + H * P * D * 2
+        extra["bulk_append_32k_us"] = round(float(np.median(app)), 2)
+        extra["bulk_append_32k_GBps"] = round(app_bytes / (np.median(app) * 1e-6) / 1e9, 1)
+        extra["bulk_append_bytes"] = app_bytes
+        extra["decode_append_us"] = round(decode_appends(dev, layout), 3)
+
+    dom_us, dom_bytes, dom_name = (us_est, EST_BYTES, "estimate_kernel (score + fused top-k)") \
+        if us_est >= us_dec else (us_dec, DEC_BYTES, "decode_kernel (split-K sparse attention)")
+    achieved = dom_bytes / (dom_us * 1e-6) / 1e9
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom_name,
+            "bytes_per_launch": dom_bytes, "us_per_launch": round(dom_us, 3)}
+
+    result = {
+        "metric": METRIC, "value": round(us_layer, 3), "unit": "us/layer", "n_gpus": 1,
+        "steps": steps, "warmup": warm, "ms_per_step": round(us_layer / 1e3, 6),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic: seeded N(0,1) K/V/q, 4 of 128 key channels x8, random page tables",
+        "config": {"workload": "BASELINE config 2: sparse decode layer (value-aware scores of "
+                               "2048 pages + per-head top-128 + split-K attention), 32 heads x "
+                               "128, 32768 ctx, page 16, budget 2048, 32 rotated layers",
+                   "layout": args.layout.upper(), "launches_per_layer": 2,
+                   "hip_graph": True},
+        "layer_GBps": round(LAYER_BYTES / (us_layer * 1e-6) / 1e9, 1),
+        "layer_bytes": LAYER_BYTES,
+        "layer_hbm_frac": round(LAYER_BYTES / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "per_kernel_us": {"estimate_topk": round(us_est, 3), "decode": round(us_dec, 3)},
+        "graph_replay_exact": replay_exact,
+        "roofline": roof,
+    }
+    if not args.no_cpu_baseline:
+        log("[bench] CPU baseline (oracle) ...")
+        cb = cpu_baseline(B["k0"], B["v0"], q[0], args.cpu_reps)
+        # parity of layer 0 against the oracle on the same inputs
+        err = float(np.abs(o[0].cpu().numpy()[0].astype(np.float32) -
+                           cb["o"][0, :, 0].astype(np.float32)).max())
+        inv = np.argsort(idx[0].cpu().numpy())      # physical -> logical
+        sl = inv[sel[0, 0].cpu().numpy()]
+        from oracle import sim
+        sets_ok = all(sim.selection_matches(sl[h], cb["pages"][0, h, 0], cb["scores"][0, h, 0],
+                                            True)[0] for h in range(H))
+        result["cpu_baseline"] = {k: cb[k] for k in ("value", "unit", "cores", "kind", "sample")}
+        result["cpu_baseline"]["value"] = round(cb["value"], 1)
+        result["parity_layer0"] = {"max_abs_o_vs_oracle": err, "selections_match": sets_ok}
+    result["extra"] = extra
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

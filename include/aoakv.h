@@ -1,0 +1,247 @@
+/*
+ * aoakv.h -- C ABI of libaoakv.so, the MI355X (gfx950) implementation of
+ * AOA-KV's single-layer decode hot path.
+ *
+ * The entry points replace the ops of the reference's pybind module
+ * `quest._kernels` (kernels/aoa_kv/quest/ops/csrc/bsk_ops.cu:4-20,
+ * bsk_ops.h:23-126), one for one, with the same argument meaning:
+ *
+ *   append_kv_cache_prefill      -> aoakv_append_kv_cache_prefill
+ *   append_kv_cache_decode       -> aoakv_append_kv_cache_decode
+ *   estimate_attn_score          -> aoakv_estimate_attn_score
+ *   topk_filtering               -> aoakv_topk_filtering
+ *   BatchDecodeWithPagedKVCache  -> aoakv_decode_workspace_size,
+ *     PyTorchWrapper                aoakv_workspace_init,
+ *     .begin/forward/end_forward    aoakv_decode_sparse_attn
+ *   prefill_with_paged_kv_cache  -> aoakv_prefill_with_paged_kv_cache
+ *
+ * plus one fused entry point (aoakv_sparse_decode_layer) that runs
+ * estimate + top-k + sparse decode for one layer.
+ *
+ * Conventions
+ *   - All tensor arguments are device pointers (plain pointers, no torch
+ *     types).  fp16 data is passed as `void*` and holds IEEE binary16.
+ *   - Paged cache of one layer (reference kv_cache.py:19-23):
+ *       layout NHD (0): [max_pages, 2, page_size, num_heads, head_dim]
+ *       layout HND (1): [max_pages, 2, num_heads, page_size, head_dim]
+ *     slot 0 = K, slot 1 = V.  The metadata cache uses the same layout with
+ *     "tokens" = kv pages: slot 0 = per-page Kmax, slot 1 = per-page Kmin
+ *     (reference decode_page.cuh:425-449).
+ *   - v_log_norm: [max_pages, num_kv_heads] fp16, indexed by PHYSICAL kv page
+ *     (reference controller.py:43-47).  v_mean: [max_pages, num_kv_heads,
+ *     head_dim] fp16, the simulation's per-page mean of V
+ *     (filter_util.py:797-834), which the decode append needs for its
+ *     running mean (filter_util.py:669-716).
+ *   - Page tables: kv_indptr[B+1], kv_indices[], kv_last_page_len[B] and
+ *     metadata_indptr[B+1], metadata_indices[] are int32 device arrays
+ *     (reference paged_kv_t, decode_page.cuh:79-352).
+ *   - Semantics are the reference simulation's (filter_util.py:269-407,
+ *     quest_attention.py:196-382): every page, including the partial last
+ *     one, is scored; fixed selection forces the first and last page;
+ *     k = min(max(3, min(L, budget) / page_size), P); scores are fp32.
+ *   - Every call is asynchronous on `stream` (a hipStream_t), allocates no
+ *     device memory and performs no host synchronisation.
+ *   - Return value: 0 on success, otherwise an AOAKV_ERR_* code;
+ *     aoakv_last_error() then describes the failure (thread-local).
+ *   - Supported shapes: head_dim 128, page_size 16, num_heads <= 256,
+ *     num_qo_heads a multiple of num_kv_heads with group size <= 8.
+ */
+#ifndef AOAKV_H_
+#define AOAKV_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AOAKV_OK 0
+#define AOAKV_ERR_INVALID 1     /* bad argument (null pointer, size, budget) */
+#define AOAKV_ERR_UNSUPPORTED 2 /* unsupported head_dim / page_size / layout */
+#define AOAKV_ERR_HIP 3         /* HIP runtime error (launch failure) */
+
+#define AOAKV_LAYOUT_NHD 0u
+#define AOAKV_LAYOUT_HND 1u
+
+/* flags for scoring / selection */
+#define AOAKV_FLAG_VALUE_AWARE 1u /* AOA-KV score (else plain Quest bound)   */
+#define AOAKV_FLAG_FIXED 2u       /* force first and last page (sim `fixed`) */
+
+/* Thread-local description of the last failure ("" when none). */
+const char* aoakv_last_error(void);
+
+/* Library version string. */
+const char* aoakv_version(void);
+
+/*
+ * Bulk append of N new tokens of ONE sequence into the paged cache, with
+ * metadata maintenance.  Replaces append_kv_cache_prefill
+ * (reference bsk_ops.h:53-68, page.cu:107-222, decode_page.cuh:528-692).
+ *
+ * k, v: [N, num_heads, head_dim] fp16 (NHD, contiguous).  The cache pages
+ * must already be reserved: num_kv_pages pages listed in kv_indices (host
+ * count), the last one holding kv_last_page_len tokens after the append.
+ * metadata_indices lists ceil(num_kv_pages / page_size) metadata pages.
+ * For each page touched: K/V stored; Kmax/Kmin folded; on a page that
+ * starts empty V̄ = fp16(sum_fp32 / n) (compute_page_v_mean), on a page
+ * already holding tokens V̄ follows the running mean of
+ * update_mean_filter token by token; log‖V̄‖ stored in v_log_norm.
+ */
+int aoakv_append_kv_cache_prefill(const void* k, const void* v, uint32_t num_new_tokens,
+                                  void* kv_data, const int32_t* kv_indices,
+                                  uint32_t num_kv_pages, uint32_t kv_last_page_len,
+                                  void* metadata_data, const int32_t* metadata_indices,
+                                  void* v_log_norm, void* v_mean, uint32_t num_heads,
+                                  uint32_t head_dim, uint32_t page_size, uint32_t layout,
+                                  void* stream);
+
+/*
+ * Append one token per sequence for a batch of B sequences (decode step).
+ * Replaces append_kv_cache_decode (reference bsk_ops.h:70-85, page.cu:6-105,
+ * decode_page.cuh:398-506); follows filter_util.py:669-716,758-795.
+ *
+ * k, v: [B, num_heads, head_dim] fp16.  The slot of the new token must be
+ * reserved: kv_last_page_len[b] already counts it.
+ */
+int aoakv_append_kv_cache_decode(const void* k, const void* v, uint32_t batch_size,
+                                 void* kv_data, const int32_t* kv_indptr,
+                                 const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                                 void* metadata_data, const int32_t* metadata_indptr,
+                                 const int32_t* metadata_indices, void* v_log_norm,
+                                 void* v_mean, uint32_t num_heads, uint32_t head_dim,
+                                 uint32_t page_size, uint32_t layout, void* stream);
+
+/*
+ * Page scores of every page of every sequence.  Replaces estimate_attn_score
+ * (reference bsk_ops.h:41-51, estimate.cu:6-90, decode_attn.cuh:145-199,
+ * 276-443); follows filter_util.py:269-380,968-1018:
+ *   bound(p) = sum_d max(q_d*Kmax_d, q_d*Kmin_d)                       (fp32)
+ *   value-aware: 2*bound/sqrt(d) [logsumexp over a GQA group]
+ *                + 2*log‖V̄_p‖                                          (fp32)
+ *   plain Quest: bound [summed over a GQA group]
+ *
+ * q: [B, num_qo_heads, head_dim] fp16.  scores: [B, num_kv_heads,
+ * score_stride] fp32, entry p < P_b written.  max_pages >= every P_b.
+ */
+int aoakv_estimate_attn_score(const void* q, float* scores, uint32_t score_stride,
+                              const void* metadata_data, const int32_t* metadata_indptr,
+                              const int32_t* metadata_indices, const int32_t* kv_indptr,
+                              const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                              const void* v_log_norm, uint32_t batch_size, uint32_t max_pages,
+                              uint32_t num_qo_heads, uint32_t num_kv_heads, uint32_t head_dim,
+                              uint32_t page_size, uint32_t layout, uint32_t flags, void* stream);
+
+/*
+ * Per-(sequence, kv head) top-k pages under a token budget.  Replaces
+ * topk_filtering (reference bsk_ops.h:34-39, topk.cu:7-46,
+ * decode_select_k.cuh:26-61); follows filter_util.py:373-380.
+ *
+ * k_b = min(max(3, min(L_b, budget_b) / page_size), P_b) where budget_b is
+ * token_budgets[b] when token_budgets != NULL, else token_budget.  With
+ * AOAKV_FLAG_FIXED pages 0 and P_b-1 are always selected.  Ties are broken
+ * towards the lower page index.  Output: sel_pages[B, num_kv_heads,
+ * sel_stride] int32 PHYSICAL page ids (kv_indices entries) of the selected
+ * pages in ascending logical order; entries >= k_b untouched.
+ * sel_stride >= max_b k_b.  Supports P_b <= 16384.
+ */
+int aoakv_topk_filtering(const float* scores, uint32_t score_stride,
+                         const int32_t* kv_indptr, const int32_t* kv_indices,
+                         const int32_t* kv_last_page_len, uint32_t token_budget,
+                         const int32_t* token_budgets, int32_t* sel_pages, uint32_t sel_stride,
+                         uint32_t batch_size, uint32_t num_kv_heads, uint32_t page_size,
+                         uint32_t flags, void* stream);
+
+/*
+ * Bytes of the caller-owned workspace for aoakv_decode_sparse_attn and
+ * aoakv_sparse_decode_layer (replaces the buffers BatchDecodeHandler
+ * allocates in begin_forward, reference decode_handler.cuh:73-136).
+ * max_sel_pages: upper bound on pages attended per (sequence, head).
+ */
+size_t aoakv_decode_workspace_size(uint32_t batch_size, uint32_t num_qo_heads,
+                                   uint32_t num_kv_heads, uint32_t head_dim,
+                                   uint32_t max_sel_pages);
+
+/*
+ * Zero the workspace's arrival counters.  Call once after allocating a
+ * workspace (the kernels leave the counters at zero on exit).
+ */
+int aoakv_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Sparse decode attention over selected pages, split-K over pages with an
+ * in-kernel merge.  Replaces BatchDecodeWithPagedKVCachePyTorchWrapper
+ * .forward (reference approx_attn.cu:68-151, decode_attn.cuh:482-688,
+ * 1004-1044); follows quest_attention.py:265-268,347-356 (fp16-rounded
+ * logits, fp32 softmax, fp16 output).
+ *
+ * q, o: [B, num_qo_heads, head_dim] fp16.  sel_pages as written by
+ * aoakv_topk_filtering (physical ids, per kv head, sel_stride); the number
+ * of pages per (b, head) is recomputed from the same k rule.  sel_pages ==
+ * NULL attends every page (dense decode).
+ */
+int aoakv_decode_sparse_attn(const void* q, void* o, const void* kv_data,
+                             const int32_t* kv_indptr, const int32_t* kv_indices,
+                             const int32_t* kv_last_page_len, const int32_t* sel_pages,
+                             uint32_t sel_stride, uint32_t token_budget,
+                             const int32_t* token_budgets, void* workspace,
+                             size_t workspace_bytes, uint32_t batch_size, uint32_t max_pages,
+                             uint32_t num_qo_heads, uint32_t num_kv_heads, uint32_t head_dim,
+                             uint32_t page_size, uint32_t layout, void* stream);
+
+/*
+ * One decode layer: estimate + top-k (fused, last-arriving workgroup per
+ * head selects) then sparse decode (fused merge).  Equivalent to the three
+ * calls above; scores and sel_pages are written as they would be.
+ * Reference call sequence: QuestAttention.py:135-157.
+ */
+int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
+                              const int32_t* kv_indptr, const int32_t* kv_indices,
+                              const int32_t* kv_last_page_len, const void* metadata_data,
+                              const int32_t* metadata_indptr, const int32_t* metadata_indices,
+                              const void* v_log_norm, float* scores, uint32_t score_stride,
+                              int32_t* sel_pages, uint32_t sel_stride, uint32_t token_budget,
+                              const int32_t* token_budgets, void* workspace,
+                              size_t workspace_bytes, uint32_t batch_size, uint32_t max_pages,
+                              uint32_t num_qo_heads, uint32_t num_kv_heads, uint32_t head_dim,
+                              uint32_t page_size, uint32_t layout, uint32_t flags, void* stream);
+
+/*
+ * estimate + top-k in one launch (the first launch of
+ * aoakv_sparse_decode_layer): page scores are written to `scores` and the
+ * last workgroup of each (sequence, kv head) selects into sel_pages.
+ * Equivalent to aoakv_estimate_attn_score followed by aoakv_topk_filtering
+ * (reference call sequence QuestAttention.py:135-148).  workspace: as for
+ * aoakv_decode_sparse_attn (its arrival counters are used).
+ */
+int aoakv_estimate_topk(const void* q, const void* metadata_data, const int32_t* metadata_indptr,
+                        const int32_t* metadata_indices, const int32_t* kv_indptr,
+                        const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                        const void* v_log_norm, float* scores, uint32_t score_stride,
+                        int32_t* sel_pages, uint32_t sel_stride, uint32_t token_budget,
+                        const int32_t* token_budgets, void* workspace, size_t workspace_bytes,
+                        uint32_t batch_size, uint32_t max_pages, uint32_t num_qo_heads,
+                        uint32_t num_kv_heads, uint32_t head_dim, uint32_t page_size,
+                        uint32_t layout, uint32_t flags, void* stream);
+
+/*
+ * Dense causal prefill over the paged cache of ONE sequence.  Replaces
+ * prefill_with_paged_kv_cache (reference bsk_ops.h:87-95,
+ * batch_prefill.cu:27-117, prefill.cuh:688-1115).
+ *
+ * q, o: [qo_len, num_heads, head_dim] fp16; the queries are the last qo_len
+ * positions of the L = (num_kv_pages-1)*page_size + kv_last_page_len
+ * cached tokens; query i attends keys <= L - qo_len + i when causal.
+ * fp16 inputs, fp32 accumulation (MFMA), fp16 output.
+ */
+int aoakv_prefill_with_paged_kv_cache(const void* q, void* o, const void* kv_data,
+                                      const int32_t* kv_indices, uint32_t num_kv_pages,
+                                      uint32_t kv_last_page_len, uint32_t qo_len,
+                                      uint32_t causal, uint32_t num_heads, uint32_t head_dim,
+                                      uint32_t page_size, uint32_t layout, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AOAKV_H_ */
