@@ -87,6 +87,38 @@ size_t ws_layout(uint32_t B, uint32_t hq, uint32_t hkv, uint32_t max_sel_pages, 
   return total;
 }
 
+// Scores + top-k: one fused launch when every sequence fits the fused
+// kernel's top-k, else scores then the standalone top-k kernel.
+int launch_estimate_topk(aoakv::EstimateArgs ea, const Workspace& w, int32_t* sel_pages,
+                         uint32_t sel_stride, uint32_t token_budget, const int32_t* token_budgets,
+                         uint32_t batch_size, uint32_t max_pages, uint32_t page_size,
+                         uint32_t flags, hipStream_t s) {
+  if (max_pages <= aoakv::fused_topk_max_pages()) {
+    ea.sel = sel_pages;
+    ea.sel_stride = sel_stride;
+    ea.token_budget = token_budget;
+    ea.token_budgets = token_budgets;
+    ea.counters = w.est_counters;
+    return hip_status(aoakv::launch_estimate(ea, batch_size, max_pages, s), "estimate_topk");
+  }
+  if (int e = hip_status(aoakv::launch_estimate(ea, batch_size, max_pages, s), "estimate"))
+    return e;
+  aoakv::TopkArgs ta{};
+  ta.scores = ea.scores;
+  ta.score_stride = ea.score_stride;
+  ta.kv_indptr = ea.kv_indptr;
+  ta.kv_indices = ea.kv_indices;
+  ta.kv_last_page_len = ea.kv_last_page_len;
+  ta.token_budget = token_budget;
+  ta.token_budgets = token_budgets;
+  ta.sel = sel_pages;
+  ta.sel_stride = sel_stride;
+  ta.Hkv = ea.Hkv;
+  ta.S = page_size;
+  ta.flags = flags;
+  return hip_status(aoakv::launch_topk(ta, batch_size, s), "topk");
+}
+
 }  // namespace
 
 extern "C" {
@@ -287,6 +319,9 @@ static int fill_decode(aoakv::DecodeArgs& a, Workspace& w, const void* q, void* 
   REQUIRE(max_pages >= 1u, "decode_sparse_attn: max_pages must be >= 1");
   const uint32_t max_sel = sel_pages ? (sel_stride < max_pages ? sel_stride : max_pages) : max_pages;
   REQUIRE(!sel_pages || sel_stride >= 3u, "decode_sparse_attn: sel_stride %u < 3", sel_stride);
+  REQUIRE(aoakv::decode_chunks(max_sel) <= aoakv::decode_max_chunks(),
+          "decode_sparse_attn: %u pages per head exceed the %u the split-K merge holds", max_sel,
+          aoakv::decode_max_chunks() * 8u);
   const size_t need = ws_layout(batch_size, num_qo_heads, num_kv_heads, max_sel, workspace, &w);
   REQUIRE(workspace_bytes >= need, "decode_sparse_attn: workspace of %zu bytes < %zu needed",
           workspace_bytes, need);
@@ -341,6 +376,8 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
                               uint32_t page_size, uint32_t layout, uint32_t flags,
                               void* stream) {
   REQUIRE(sel_pages, "sparse_decode_layer: sel_pages is required");
+  REQUIRE(max_pages <= aoakv::topk_max_pages(), "sparse_decode_layer: max_pages %u > %u",
+          max_pages, aoakv::topk_max_pages());
   aoakv::EstimateArgs ea{};
   if (int e = fill_estimate(ea, q, scores, score_stride, metadata_data, metadata_indptr,
                             metadata_indices, kv_indptr, kv_indices, kv_last_page_len,
@@ -354,14 +391,9 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
                           workspace_bytes, batch_size, max_pages, num_qo_heads, num_kv_heads,
                           head_dim, page_size, layout))
     return e;
-  ea.sel = sel_pages;
-  ea.sel_stride = sel_stride;
-  ea.token_budget = token_budget;
-  ea.token_budgets = token_budgets;
-  ea.counters = w.est_counters;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (int e = hip_status(aoakv::launch_estimate(ea, batch_size, max_pages, s),
-                         "sparse_decode_layer/estimate"))
+  if (int e = launch_estimate_topk(ea, w, sel_pages, sel_stride, token_budget, token_budgets,
+                                   batch_size, max_pages, page_size, flags, s))
     return e;
   return hip_status(aoakv::launch_decode(da, batch_size, s), "sparse_decode_layer/decode");
 }
@@ -376,6 +408,8 @@ int aoakv_estimate_topk(const void* q, const void* metadata_data, const int32_t*
                         uint32_t num_kv_heads, uint32_t head_dim, uint32_t page_size,
                         uint32_t layout, uint32_t flags, void* stream) {
   REQUIRE(sel_pages && workspace, "estimate_topk: sel_pages and workspace are required");
+  REQUIRE(max_pages <= aoakv::topk_max_pages(), "estimate_topk: max_pages %u > %u", max_pages,
+          aoakv::topk_max_pages());
   REQUIRE(sel_stride >= 3u, "estimate_topk: sel_stride %u < 3", sel_stride);
   aoakv::EstimateArgs ea{};
   if (int e = fill_estimate(ea, q, scores, score_stride, metadata_data, metadata_indptr,
@@ -388,14 +422,9 @@ int aoakv_estimate_topk(const void* q, const void* metadata_data, const int32_t*
   const size_t need = ws_layout(batch_size, num_qo_heads, num_kv_heads, max_sel, workspace, &w);
   REQUIRE(workspace_bytes >= need, "estimate_topk: workspace of %zu bytes < %zu needed",
           workspace_bytes, need);
-  ea.sel = sel_pages;
-  ea.sel_stride = sel_stride;
-  ea.token_budget = token_budget;
-  ea.token_budgets = token_budgets;
-  ea.counters = w.est_counters;
-  return hip_status(
-      aoakv::launch_estimate(ea, batch_size, max_pages, static_cast<hipStream_t>(stream)),
-      "estimate_topk");
+  return launch_estimate_topk(ea, w, sel_pages, sel_stride, token_budget, token_budgets,
+                              batch_size, max_pages, page_size, flags,
+                              static_cast<hipStream_t>(stream));
 }
 
 int aoakv_prefill_with_paged_kv_cache(const void* q, void* o, const void* kv_data,

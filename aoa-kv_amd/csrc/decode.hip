@@ -12,7 +12,10 @@
 // 16-lane rows; a row covers one 128-dim fp16 vector with 16-byte loads, so
 // one wave-wide load moves 1 KB.  Cross-workgroup steps (top-k after all of
 // a head's scores are written, the split-K merge) are done by the last
-// workgroup to arrive at a per-head counter, which it resets to zero.
+// workgroup to arrive at a per-head counter (arrive_last), with the data
+// handed over through agent-coherent stores and loads.  Loads that feed a
+// reduction are issued as a batch before any of them is consumed, so a
+// handoff costs one memory round trip, not one per element.
 #include "kernels.hpp"
 
 namespace aoakv {
@@ -20,63 +23,124 @@ namespace aoakv {
 constexpr int kThreads = 256;
 constexpr int kEstPagesPerWave = 32;                     // 8 steps x 4 rows
 constexpr int kEstPagesPerBlock = kEstPagesPerWave * 4;  // 128
-constexpr int kTopkMaxLds = 4096;                        // keys staged in LDS
 constexpr int kDecPagesPerWave = 2;
 constexpr int kDecPagesPerBlock = kDecPagesPerWave * 4;  // 8
 constexpr int kPartialStride = kHeadDim + 4;             // o[128], m, l, pad
+constexpr int kMergeMaxChunks = 1024;                    // decode chunks per head
+constexpr uint32_t kTopkMaxPages = 16384;
+
+// ======================================================================
+// block-wide helpers (256 threads = 4 waves)
+// ======================================================================
+
+__device__ inline uint32_t wave_incl_scan(uint32_t v) {
+  const uint32_t lane = __lane_id();
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const uint32_t t = __shfl_up(v, off);
+    if ((int)lane >= off) v += t;
+  }
+  return v;
+}
+
+// Exclusive prefix sum of v over the block (thread order); *total = sum.
+__device__ inline uint32_t block_excl_scan(uint32_t v, uint32_t* s4, uint32_t* total) {
+  const uint32_t lane = __lane_id(), wave = threadIdx.x / kWave;
+  const uint32_t incl = wave_incl_scan(v);
+  if (lane == kWave - 1) s4[wave] = incl;
+  __syncthreads();
+  uint32_t before = 0, tot = 0;
+#pragma unroll
+  for (uint32_t w = 0; w < 4; ++w) {
+    const uint32_t x = s4[w];
+    before += w < wave ? x : 0u;
+    tot += x;
+  }
+  __syncthreads();
+  *total = tot;
+  return before + incl - v;
+}
+
+__device__ inline float block_max(float v, float* s4) {
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  if (__lane_id() == 0) s4[threadIdx.x / kWave] = v;
+  __syncthreads();
+  v = fmaxf(fmaxf(s4[0], s4[1]), fmaxf(s4[2], s4[3]));
+  __syncthreads();
+  return v;
+}
+
+__device__ inline float block_sum(float v, float* s4) {
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  if (__lane_id() == 0) s4[threadIdx.x / kWave] = v;
+  __syncthreads();
+  v = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+  __syncthreads();
+  return v;
+}
 
 // ======================================================================
 // top-k selection for one (sequence, kv head), one 256-thread block
 // ======================================================================
 
 struct TopkShared {
-  uint32_t keys[kTopkMaxLds];
   uint32_t hist[256];
+  uint32_t s4[4];
   uint32_t red[8];
-  uint32_t bin, above;
-  uint32_t wsum[4][2];
+  uint32_t bin, above, count;
 };
-
-__device__ inline uint32_t wave_excl_count(bool flag, uint64_t& mask) {
-  mask = __ballot(flag);
-  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
-                                   __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
-}
 
 // Selects k of P pages from fp32 `scores` (filter_util.py:373-380): with
 // `fixed`, pages 0 and P-1 always; the rest by descending score, ties to the
 // lower page index.  Writes kv_ids[page] of the selected pages to out[] in
-// ascending page order.  Key order = float order (order_key).
-__device__ void topk_block(const float* __restrict__ scores, uint32_t P, uint32_t k, bool fixed,
+// ascending page order.
+//
+// Thread t owns pages [t*kpt, t*kpt + kpt), kpt = ceil(P/256) <= KPT, keys
+// held in registers.  The k-th largest free key is found by a radix select
+// over the key offset from the smallest free key, 8-bit digits from the top
+// set bit of the key range down (one head's scores span a narrow range, so
+// the first digit already spreads the histogram); it stops as soon as the
+// bucket holding the k-th key is taken whole.
+template <int KPT>
+__device__ __forceinline__ void topk_block(const float* __restrict__ scores, uint32_t P, uint32_t k, bool fixed,
                            const int32_t* __restrict__ kv_ids, int32_t* __restrict__ out,
                            TopkShared& sh) {
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = __lane_id();
   const uint32_t wave = tid / kWave;
-  const bool in_lds = P <= (uint32_t)kTopkMaxLds;
-
   if (k >= P) {  // everything selected
     for (uint32_t i = tid; i < P; i += kThreads) out[i] = kv_ids[i];
     return;
   }
-  auto forced = [&](uint32_t i) { return fixed && (i == 0u || i == P - 1u); };
-  auto key_at = [&](uint32_t i) -> uint32_t {
-    return in_lds ? sh.keys[i] : order_key(__builtin_nontemporal_load(scores + i));
-  };
+  const uint32_t kpt = (P + kThreads - 1) / kThreads;
+  const uint32_t i0 = tid * kpt;
 
-  // stage keys, min / max over the free (non-forced) pages
+  // all of this thread's scores are loaded before any is used
+  float sc[KPT];
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    const uint32_t i = i0 + j;
+    sc[j] = ((uint32_t)j < kpt && i < P) ? ld_agent(scores + i) : 0.f;
+  }
+  uint32_t key[KPT];
+  uint64_t free_mask = 0, valid_mask = 0;  // bit j: page i0+j exists / is not forced
   uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
-  for (uint32_t i = tid; i < P; i += kThreads) {
-    uint32_t key = order_key(scores[i]);
-    if (in_lds) sh.keys[i] = key;
-    if (!forced(i)) {
-      kmin = key < kmin ? key : kmin;
-      kmax = key > kmax ? key : kmax;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    const uint32_t i = i0 + j;
+    const bool valid = (uint32_t)j < kpt && i < P;
+    const bool forced = fixed && (i == 0u || i == P - 1u);
+    key[j] = order_key(sc[j]);
+    if (valid) valid_mask |= 1ull << j;
+    if (valid && !forced) {
+      free_mask |= 1ull << j;
+      kmin = key[j] < kmin ? key[j] : kmin;
+      kmax = key[j] > kmax ? key[j] : kmax;
     }
   }
   for (int off = 32; off > 0; off >>= 1) {
-    uint32_t a = __shfl_xor(kmin, off);
-    uint32_t b = __shfl_xor(kmax, off);
+    const uint32_t a = __shfl_xor(kmin, off);
+    const uint32_t b = __shfl_xor(kmax, off);
     kmin = a < kmin ? a : kmin;
     kmax = b > kmax ? b : kmax;
   }
@@ -87,6 +151,7 @@ __device__ void topk_block(const float* __restrict__ scores, uint32_t P, uint32_
   __syncthreads();
   kmin = sh.red[0];
   kmax = sh.red[4];
+#pragma unroll
   for (int w = 1; w < 4; ++w) {
     kmin = sh.red[w] < kmin ? sh.red[w] : kmin;
     kmax = sh.red[4 + w] > kmax ? sh.red[4 + w] : kmax;
@@ -94,21 +159,20 @@ __device__ void topk_block(const float* __restrict__ scores, uint32_t P, uint32_
   const uint32_t nforced = fixed ? (P == 1u ? 1u : 2u) : 0u;
   uint32_t kr = k - nforced;  // >= 1 because k >= 3 whenever k < P
 
-  // radix select of the kr-th largest free key, digits of the key offset
-  // (key - kmin) from its top set bit down (the offsets of one head's scores
-  // span a narrow range, so the first digit already spreads the histogram)
   const uint32_t range = kmax - kmin;
   uint64_t prefix = 0;
   int hi = range == 0u ? 0 : 32 - __builtin_clz(range);
+  bool take_bucket = false;  // the final bucket is taken whole
   while (hi > 0) {
     const int w = hi < 8 ? hi : 8;
-    const int sh_ = hi - w;
-    for (uint32_t i = tid; i < 256u; i += kThreads) sh.hist[i] = 0u;
+    const int sft = hi - w;
+    sh.hist[tid] = 0u;
     __syncthreads();
-    for (uint32_t i = tid; i < P; i += kThreads) {
-      if (forced(i)) continue;
-      uint64_t rel = (uint64_t)(key_at(i) - kmin);
-      if ((rel >> hi) == (prefix >> hi)) atomicAdd(&sh.hist[(uint32_t)(rel >> sh_) & ((1u << w) - 1u)], 1u);
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const uint64_t rel = (uint64_t)(key[j] - kmin);
+      if (((free_mask >> j) & 1ull) && (rel >> hi) == (prefix >> hi))
+        atomicAdd(&sh.hist[(uint32_t)(rel >> sft) & ((1u << w) - 1u)], 1u);
     }
     __syncthreads();
     if (wave == 0) {
@@ -119,128 +183,146 @@ __device__ void topk_block(const float* __restrict__ scores, uint32_t P, uint32_
         c[j] = sh.hist[255u - 4u * lane - j];
         s4 += c[j];
       }
-      uint32_t incl = s4;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        uint32_t t = __shfl_up(incl, off);
-        if ((int)lane >= off) incl += t;
-      }
-      uint32_t excl = incl - s4;
+      const uint32_t incl = wave_incl_scan(s4);
+      const uint32_t excl = incl - s4;
       if (excl < kr && kr <= incl) {
-        uint32_t cc = excl;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if (cc + c[j] >= kr) {
-            sh.bin = 255u - 4u * lane - j;
-            sh.above = cc;
-            break;
-          }
-          cc += c[j];
-        }
+        // first of this lane's 4 bins whose running count reaches kr
+        const uint32_t c0 = excl + c[0], c1 = c0 + c[1], c2 = c1 + c[2];
+        const uint32_t j = kr <= c0 ? 0u : kr <= c1 ? 1u : kr <= c2 ? 2u : 3u;
+        sh.bin = 255u - 4u * lane - j;
+        sh.above = j == 0u ? excl : j == 1u ? c0 : j == 2u ? c1 : c2;
+        sh.count = j == 0u ? c[0] : j == 1u ? c[1] : j == 2u ? c[2] : c[3];
       }
     }
     __syncthreads();
-    prefix |= (uint64_t)sh.bin << sh_;
+    prefix |= (uint64_t)sh.bin << sft;
     kr -= sh.above;
-    hi = sh_;
-    __syncthreads();
-  }
-  const uint32_t T = kmin + (uint32_t)prefix;  // key of the k-th free page
-  const uint32_t take_eq = kr;                 // pages with key == T to take
-
-  // compaction in ascending page order, 256 pages per round
-  uint32_t base_sel = 0, base_eq = 0;
-  for (uint32_t r0 = 0; r0 < P; r0 += kThreads) {
-    const uint32_t i = r0 + tid;
-    bool valid = i < P;
-    uint32_t key = valid ? key_at(i) : 0u;
-    bool f = valid && forced(i);
-    bool eq = valid && !f && key == T;
-    bool gt = valid && !f && key > T;
-    uint64_t m_eq, m_sel;
-    uint32_t eq_rank = wave_excl_count(eq, m_eq);
-    if (lane == 0) sh.wsum[wave][0] = (uint32_t)__popcll(m_eq);
-    __syncthreads();
-    uint32_t eq_before = base_eq;
-    for (uint32_t w = 0; w < wave; ++w) eq_before += sh.wsum[w][0];
-    bool take = f || gt || (eq && eq_before + eq_rank < take_eq);
-    uint32_t sel_rank = wave_excl_count(take, m_sel);
-    if (lane == 0) sh.wsum[wave][1] = (uint32_t)__popcll(m_sel);
-    __syncthreads();
-    uint32_t sel_before = base_sel;
-    for (uint32_t w = 0; w < wave; ++w) sel_before += sh.wsum[w][1];
-    if (take) out[sel_before + sel_rank] = kv_ids[i];
-    for (uint32_t w = 0; w < 4; ++w) {
-      base_eq += sh.wsum[w][0];
-      base_sel += sh.wsum[w][1];
+    hi = sft;
+    if (sh.count == kr) {  // uniform: every key of the bucket is selected
+      take_bucket = true;
+      break;
     }
-    __syncthreads();
   }
+  // selection classes at the final resolution `hi`:
+  //   above:  (rel >> hi) >  (prefix >> hi)  -- selected
+  //   bucket: (rel >> hi) == (prefix >> hi)  -- kr of them selected: all when
+  //           take_bucket, else (hi == 0, equal keys) the lowest pages first
+  const uint64_t thr = prefix >> hi;
+  uint32_t n_eq = 0;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j)
+    if ((free_mask >> j) & 1ull) n_eq += ((uint64_t)(key[j] - kmin) >> hi) == thr ? 1u : 0u;
+  uint32_t tot;
+  const uint32_t eq_before = block_excl_scan(n_eq, sh.s4, &tot);
+  uint64_t take_mask = 0;
+  uint32_t eq_seen = eq_before;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    if (!((valid_mask >> j) & 1ull)) continue;
+    bool take;
+    if (!((free_mask >> j) & 1ull)) {
+      take = true;  // forced page
+    } else {
+      const uint64_t r = (uint64_t)(key[j] - kmin) >> hi;
+      if (r > thr) {
+        take = true;
+      } else if (r == thr) {
+        take = take_bucket || eq_seen < kr;
+        ++eq_seen;
+      } else {
+        take = false;
+      }
+    }
+    if (take) take_mask |= 1ull << j;
+  }
+  const uint32_t sel_before = block_excl_scan((uint32_t)__builtin_popcountll(take_mask), sh.s4, &tot);
+  uint32_t pos = sel_before;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j)
+    if ((take_mask >> j) & 1ull) out[pos++] = kv_ids[i0 + j];
 }
+
+// Pages per head the fused estimate + top-k kernel selects from (16 keys per
+// thread keep its register count at the scoring kernel's); longer sequences
+// use the standalone top-k kernel.
+constexpr uint32_t kFusedTopkMaxPages = 16u * kThreads;
 
 // ======================================================================
 // page scores (+ optional fused top-k)
 // ======================================================================
 
-
+// Grid (page chunks of 128, kv heads, batch); a wave scores 32 consecutive
+// pages = two metadata pages (page_size 16), so its metadata page indices
+// are two scalar loads.
 template <int GROUP>
 __global__ __launch_bounds__(kThreads) void estimate_kernel(EstimateArgs a) {
   __shared__ TopkShared sh;
+  __shared__ float s_sc[kEstPagesPerBlock];
   __shared__ uint32_t s_last;
   const uint32_t lane = __lane_id();
-  const uint32_t wave = threadIdx.x / kWave;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t row = lane / kLanesPerRow;
   const uint32_t l16 = lane % kLanesPerRow;
   const uint32_t b = blockIdx.z, h = blockIdx.y, chunk = blockIdx.x;
   const uint32_t pbeg = (uint32_t)a.kv_indptr[b];
   uint32_t P = (uint32_t)a.kv_indptr[b + 1] - pbeg;
   if (P > a.score_stride) P = a.score_stride;  // never write past a score row
+  if (P > kFusedTopkMaxPages && a.sel != nullptr) P = kFusedTopkMaxPages;
   if (chunk * kEstPagesPerBlock >= P) return;  // uniform per block
-  const uint32_t S = a.S;
   const uint32_t mbeg = (uint32_t)a.meta_indptr[b];
   const uint32_t d0 = l16 * kVec;
   const bool value_aware = (a.flags & 1u) != 0u;
 
+  const uint32_t page0 = chunk * kEstPagesPerBlock + wave * kEstPagesPerWave;
+  const bool wave_live = page0 < P;
+  uint32_t mp0 = 0, mp1 = 0;
+  if (wave_live) {
+    mp0 = (uint32_t)a.meta_indices[mbeg + page0 / kPageSize];
+    mp1 = page0 + kPageSize < P ? (uint32_t)a.meta_indices[mbeg + page0 / kPageSize + 1] : mp0;
+  }
+  // lane j < 32 fetches the value statistic of page page0 + j
+  float lvn_lane = 0.f;
+  if (value_aware && lane < (uint32_t)kEstPagesPerWave && page0 + lane < P)
+    lvn_lane = (float)a.v_log_norm[(size_t)(uint32_t)a.kv_indices[pbeg + page0 + lane] * a.Hkv + h];
+
   float qf[GROUP][kVec];
 #pragma unroll
   for (int g = 0; g < GROUP; ++g) {
-    H8 qq = ld16(a.q + ((size_t)b * a.Hq + h * GROUP + g) * kHeadDim + d0);
+    const H8 qq = ld16(a.q + ((size_t)b * a.Hq + h * GROUP + g) * kHeadDim + d0);
 #pragma unroll
     for (int j = 0; j < kVec; ++j) qf[g][j] = (float)qq.v[j];
   }
 
-  const uint32_t page0 = chunk * kEstPagesPerBlock + wave * kEstPagesPerWave;
   constexpr int kSteps = kEstPagesPerWave / 4;
   H8 kmx[kSteps], kmn[kSteps];
-  f16 lvn[kSteps];
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
     const uint32_t p = page0 + s * 4 + row;
     if (p < P) {
-      const uint32_t mp = (uint32_t)a.meta_indices[mbeg + p / S];
-      const size_t off = elem_off(a.g, mp, 0, h, p % S) + d0;
+      const uint32_t mp = s < kSteps / 2 ? mp0 : mp1;
+      const size_t off = elem_off(a.g, mp, 0, h, (s * 4 + row) % kPageSize) + d0;
       kmx[s] = ld16(a.meta + off);
       kmn[s] = ld16(a.meta + off + a.g.kv);
-      if (value_aware)
-        lvn[s] = a.v_log_norm[(size_t)(uint32_t)a.kv_indices[pbeg + p] * a.Hkv + h];
+    } else {
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) kmx[s].v[j] = kmn[s].v[j] = (f16)0.f;
     }
   }
-  float* out = a.scores + ((size_t)b * a.Hkv + h) * a.score_stride;
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
-    const uint32_t p = page0 + s * 4 + row;
     float x[GROUP];
 #pragma unroll
     for (int g = 0; g < GROUP; ++g) {
       float acc = 0.f;
 #pragma unroll
       for (int j = 0; j < kVec; ++j) {
-        float u = qf[g][j] * (float)kmx[s].v[j];
-        float w = qf[g][j] * (float)kmn[s].v[j];
+        const float u = qf[g][j] * (float)kmx[s].v[j];
+        const float w = qf[g][j] * (float)kmn[s].v[j];
         acc = acc + fmaxf(u, w);
       }
       x[g] = row_sum16(acc);
     }
+    const float lvn = __shfl(lvn_lane, s * 4 + (int)row);
     float score;
     if (value_aware) {
       // 2 * (bound / sqrt(d)), logsumexp over the group, + 2 * log-norm
@@ -257,36 +339,32 @@ __global__ __launch_bounds__(kThreads) void estimate_kernel(EstimateArgs a) {
         for (int g = 0; g < GROUP; ++g) se = se + expf(x[g] - m);
         lse = logf(se) + m;
       }
-      score = lse + 2.0f * (float)lvn[s];
+      score = lse + 2.0f * lvn;
     } else {
       score = x[0];
 #pragma unroll
       for (int g = 1; g < GROUP; ++g) score = score + x[g];
     }
-    if (p < P && l16 == 0u) out[p] = score;
+    if (l16 == 0u) s_sc[wave * kEstPagesPerWave + s * 4 + row] = score;
+  }
+  __syncthreads();
+  float* out = a.scores + ((size_t)b * a.Hkv + h) * a.score_stride;
+  {
+    const uint32_t p = chunk * kEstPagesPerBlock + threadIdx.x;
+    if (threadIdx.x < (uint32_t)kEstPagesPerBlock && p < P) st_agent(out + p, s_sc[threadIdx.x]);
   }
 
   if (a.sel == nullptr) return;
   // ---- fused top-k: the last block of this (sequence, head) selects
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t nch = (P + kEstPagesPerBlock - 1) / kEstPagesPerBlock;
-    const uint32_t prev = atomicAdd(&a.counters[b * a.Hkv + h], 1u);
-    s_last = prev == nch - 1u ? 1u : 0u;
-  }
-  __syncthreads();
-  if (s_last == 0u) return;
-  __threadfence();
-  const uint32_t L = (P - 1u) * S + (uint32_t)a.kv_last_page_len[b];
+  const uint32_t nch = (P + kEstPagesPerBlock - 1) / kEstPagesPerBlock;
+  if (!arrive_last(&a.counters[b * a.Hkv + h], nch, &s_last)) return;
+  const uint32_t L = (P - 1u) * kPageSize + (uint32_t)a.kv_last_page_len[b];
   const uint32_t budget = a.token_budgets ? (uint32_t)a.token_budgets[b] : a.token_budget;
-  uint32_t k = num_selected_pages(L, budget, S, P);
+  uint32_t k = num_selected_pages(L, budget, kPageSize, P);
   if (k > a.sel_stride) k = a.sel_stride;  // never write past a selection row
-  topk_block(out, P, k, (a.flags & 2u) != 0u, a.kv_indices + pbeg,
-             a.sel + ((size_t)b * a.Hkv + h) * a.sel_stride, sh);
-  if (threadIdx.x == 0) a.counters[b * a.Hkv + h] = 0u;
+  topk_block<16>(out, P, k, (a.flags & 2u) != 0u, a.kv_indices + pbeg,
+                 a.sel + ((size_t)b * a.Hkv + h) * a.sel_stride, sh);
 }
-
 
 __global__ __launch_bounds__(kThreads) void topk_kernel(TopkArgs a) {
   __shared__ TopkShared sh;
@@ -295,30 +373,37 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopkArgs a) {
   uint32_t P = (uint32_t)a.kv_indptr[b + 1] - pbeg;
   if (P == 0u) return;
   if (P > a.score_stride) P = a.score_stride;
+  if (P > kTopkMaxPages) P = kTopkMaxPages;
   const uint32_t L = (P - 1u) * a.S + (uint32_t)a.kv_last_page_len[b];
   const uint32_t budget = a.token_budgets ? (uint32_t)a.token_budgets[b] : a.token_budget;
   uint32_t k = num_selected_pages(L, budget, a.S, P);
   if (k > a.sel_stride) k = a.sel_stride;
-  topk_block(a.scores + ((size_t)b * a.Hkv + h) * a.score_stride, P, k, (a.flags & 2u) != 0u,
-             a.kv_indices + pbeg, a.sel + ((size_t)b * a.Hkv + h) * a.sel_stride, sh);
+  const float* row = a.scores + ((size_t)b * a.Hkv + h) * a.score_stride;
+  int32_t* out = a.sel + ((size_t)b * a.Hkv + h) * a.sel_stride;
+  if (P <= kFusedTopkMaxPages)
+    topk_block<16>(row, P, k, (a.flags & 2u) != 0u, a.kv_indices + pbeg, out, sh);
+  else
+    topk_block<kTopkMaxPages / kThreads>(row, P, k, (a.flags & 2u) != 0u, a.kv_indices + pbeg,
+                                          out, sh);
 }
 
 // ======================================================================
 // sparse decode attention, split-K over pages with a fused merge
 // ======================================================================
 
-
 __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
   __shared__ float s_o[4][kHeadDim];
   __shared__ float s_ml[4][2];
+  __shared__ float s_m[kMergeMaxChunks], s_l[kMergeMaxChunks];
+  __shared__ float s4[4];
   __shared__ uint32_t s_last;
   const uint32_t lane = __lane_id();
-  const uint32_t wave = threadIdx.x / kWave;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t row = lane / kLanesPerRow;
   const uint32_t l16 = lane % kLanesPerRow;
   const uint32_t b = blockIdx.z, hq = blockIdx.y, chunk = blockIdx.x;
   const uint32_t hkv = hq / (a.Hq / a.Hkv);
-  const uint32_t S = a.S;
+  const uint32_t S = kPageSize;
   const uint32_t pbeg = (uint32_t)a.kv_indptr[b];
   const uint32_t P = (uint32_t)a.kv_indptr[b + 1] - pbeg;
   const uint32_t lpl = (uint32_t)a.kv_last_page_len[b];
@@ -330,38 +415,50 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
     if (npages > a.sel_stride) npages = a.sel_stride;
   }
   // the grid holds max_chunks blocks per head; never index partials past it
-  if (npages > a.max_chunks * kDecPagesPerBlock) npages = a.max_chunks * kDecPagesPerBlock;
+  const uint32_t cap =
+      a.max_chunks < (uint32_t)kMergeMaxChunks ? a.max_chunks : (uint32_t)kMergeMaxChunks;
+  if (npages > cap * kDecPagesPerBlock) npages = cap * kDecPagesPerBlock;
   const uint32_t nch = (npages + kDecPagesPerBlock - 1) / kDecPagesPerBlock;
   if (chunk >= nch) return;  // uniform per block
   const uint32_t last_phys = (uint32_t)a.kv_indices[pbeg + P - 1u];
   const uint32_t d0 = l16 * kVec;
   const size_t bh = (size_t)b * a.Hq + hq;
 
-  float qf[kVec];
-  {
-    H8 qq = ld16(a.q + bh * kHeadDim + d0);
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) qf[j] = (float)qq.v[j];
-  }
-
-  // ---- issue all loads of this wave's pages
-  H8 kk[kDecPagesPerWave][4], vv[kDecPagesPerWave][4];
-  uint32_t ntok[kDecPagesPerWave];
+  // ---- page ids of this wave's pages, then all their K/V loads
+  uint32_t phys[kDecPagesPerWave], ntok[kDecPagesPerWave];
 #pragma unroll
   for (int s = 0; s < kDecPagesPerWave; ++s) {
     const uint32_t idx = chunk * kDecPagesPerBlock + wave * kDecPagesPerWave + s;
     ntok[s] = 0u;
+    phys[s] = 0u;
     if (idx < npages) {
-      const uint32_t phys = a.sel ? (uint32_t)a.sel[((size_t)b * a.Hkv + hkv) * a.sel_stride + idx]
-                                  : (uint32_t)a.kv_indices[pbeg + idx];
-      ntok[s] = phys == last_phys ? lpl : S;
-      const size_t kbase = elem_off(a.g, phys, 0, hkv, 0) + d0;
+      phys[s] = a.sel ? (uint32_t)a.sel[((size_t)b * a.Hkv + hkv) * a.sel_stride + idx]
+                      : (uint32_t)a.kv_indices[pbeg + idx];
+      ntok[s] = phys[s] == last_phys ? lpl : S;
+    }
+  }
+  float qf[kVec];
+  {
+    const H8 qq = ld16(a.q + bh * kHeadDim + d0);
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) qf[j] = (float)qq.v[j];
+  }
+  H8 kk[kDecPagesPerWave][4], vv[kDecPagesPerWave][4];
+#pragma unroll
+  for (int s = 0; s < kDecPagesPerWave; ++s) {
+    if (ntok[s] != 0u) {
+      const size_t kbase = elem_off(a.g, phys[s], 0, hkv, 0) + d0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const uint32_t t = i * 4 + row;
         kk[s][i] = ld16(a.kv + kbase + (size_t)t * a.g.tok);
         vv[s][i] = ld16(a.kv + kbase + a.g.kv + (size_t)t * a.g.tok);
       }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < kVec; ++j) kk[s][i].v[j] = vv[s][i].v[j] = (f16)0.f;
     }
   }
 
@@ -403,7 +500,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
 #pragma unroll
   for (int j = 0; j < kVec; ++j) o[j] = cross_row_sum(o[j]);
 
-  // ---- combine the 4 waves of the block in LDS
+  // ---- combine the 4 waves of the block in LDS, store the chunk's (o, m, l)
   if (row == 0u) {
 #pragma unroll
     for (int j = 0; j < kVec; ++j) s_o[wave][d0 + j] = o[j];
@@ -414,48 +511,60 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
   }
   __syncthreads();
   float* part = a.partial + (bh * a.max_chunks + chunk) * kPartialStride;
-  if (threadIdx.x < (uint32_t)kHeadDim) {
+  if (threadIdx.x < (uint32_t)kHeadDim + 2u) {
     const uint32_t d = threadIdx.x;
-    float M = fmaxf(fmaxf(s_ml[0][0], s_ml[1][0]), fmaxf(s_ml[2][0], s_ml[3][0]));
-    float acc = 0.f, l = 0.f;
+    const float M = fmaxf(fmaxf(s_ml[0][0], s_ml[1][0]), fmaxf(s_ml[2][0], s_ml[3][0]));
+    float acc = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       const float sc = s_ml[w][0] == -INFINITY ? 0.f : __expf(s_ml[w][0] - M);
-      acc = acc + sc * s_o[w][d];
-      l = l + sc * s_ml[w][1];
+      const float val = d < (uint32_t)kHeadDim ? s_o[w][d] : s_ml[w][1];
+      acc = acc + sc * val;
     }
-    part[d] = acc;
-    if (d == 0u) {
-      part[kHeadDim] = M;
-      part[kHeadDim + 1] = l;
-    }
+    // slots 0..127: o; slot 128: m; slot 129: l
+    st_agent(part + d, d == (uint32_t)kHeadDim ? M : acc);
   }
 
   // ---- the last block of this (sequence, head) merges the chunks
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t prev = atomicAdd(&a.counters[bh], 1u);
-    s_last = prev == nch - 1u ? 1u : 0u;
+  if (!arrive_last(&a.counters[bh], nch, &s_last)) return;
+  const float* base = a.partial + bh * a.max_chunks * kPartialStride;
+  // (m, l) of every chunk, loaded together
+  float mc = -INFINITY;
+  for (uint32_t c = threadIdx.x; c < nch; c += kThreads) {
+    const float mm = ld_agent(base + c * kPartialStride + kHeadDim);
+    const float ll = ld_agent(base + c * kPartialStride + kHeadDim + 1);
+    s_m[c] = mm;
+    s_l[c] = ll;
+    mc = fmaxf(mc, mm);
   }
-  __syncthreads();
-  if (s_last == 0u) return;
-  __threadfence();
-  if (threadIdx.x < (uint32_t)kHeadDim) {
-    const uint32_t d = threadIdx.x;
-    const float* base = a.partial + bh * a.max_chunks * kPartialStride;
-    float M = -INFINITY;
-    for (uint32_t c = 0; c < nch; ++c) M = fmaxf(M, base[c * kPartialStride + kHeadDim]);
-    float acc = 0.f, l = 0.f;
-    for (uint32_t c = 0; c < nch; ++c) {
-      const float* pc = base + c * kPartialStride;
-      const float sc = __expf(pc[kHeadDim] - M);
-      acc = acc + sc * pc[d];
-      l = l + sc * pc[kHeadDim + 1];
+  const float M = block_max(mc, s4);
+  float lpart = 0.f;
+  for (uint32_t c = threadIdx.x; c < nch; c += kThreads) {
+    const float w = __expf(s_m[c] - M);
+    s_m[c] = w;  // becomes the chunk weight
+    lpart = lpart + w * s_l[c];
+  }
+  const float Lsum = block_sum(lpart, s4);  // ends with a barrier: weights visible
+  // o[d] = sum_c w_c o_c[d]: thread t sums dim t%128 over the chunks of
+  // parity t/128, eight loads in flight at a time
+  const uint32_t d = threadIdx.x % kHeadDim, half = threadIdx.x / kHeadDim;
+  float acc = 0.f;
+  for (uint32_t c0 = half; c0 < nch; c0 += 16u) {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t c = c0 + 2u * i;
+      v[i] = c < nch ? ld_agent(base + c * kPartialStride + d) : 0.f;
     }
-    a.o[bh * kHeadDim + d] = r16(acc / l);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t c = c0 + 2u * i;
+      if (c < nch) acc = acc + s_m[c] * v[i];
+    }
   }
-  if (threadIdx.x == 0) a.counters[bh] = 0u;
+  if (half == 1u) s_o[0][d] = acc;
+  __syncthreads();
+  if (half == 0u) a.o[bh * kHeadDim + d] = r16((acc + s_o[0][d]) / Lsum);
 }
 
 __global__ void fill_u32_kernel(uint32_t* p, size_t n, uint32_t v) {
@@ -499,5 +608,8 @@ uint32_t decode_chunks(uint32_t max_sel_pages) {
   return (max_sel_pages + kDecPagesPerBlock - 1) / kDecPagesPerBlock;
 }
 uint32_t partial_stride() { return kPartialStride; }
+uint32_t decode_max_chunks() { return kMergeMaxChunks; }
+uint32_t topk_max_pages() { return kTopkMaxPages; }
+uint32_t fused_topk_max_pages() { return kFusedTopkMaxPages; }
 
 }  // namespace aoakv

@@ -155,6 +155,42 @@ __device__ inline f16 log_norm_row(const H8& vbar, uint32_t lane16) {
   return r16((float)ln);
 }
 
+// ---------------------------------------------------------------- cross-workgroup handoff
+// gfx950 has one L2 per XCD and the L2s are not coherent with each other.
+// An agent-scope __threadfence() therefore writes back and invalidates the
+// whole L2 -- far too slow to run in every workgroup.  Data handed from one
+// workgroup to another instead travels through agent-coherent accesses
+// (relaxed agent-scope atomic loads / stores, `sc1`), which go to the
+// memory-side coherence point, and the handoff is ordered by waiting for the
+// stores to complete before the arrival counter is incremented (RMW atomics
+// are performed at the coherence point).
+
+__device__ inline void st_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float ld_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Every workgroup of a group of n calls this once after its st_agent()
+// stores; it returns true (in all threads) in the workgroup that arrives
+// last, which may then ld_agent() everything the others stored.  The last
+// workgroup resets the counter to zero for the next launch.
+__device__ inline bool arrive_last(uint32_t* counter, uint32_t n, uint32_t* s_flag) {
+  // the vector-memory counter reaches zero only when this wave's stores are
+  // complete; the "memory" clobber keeps the compiler from moving them
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev =
+        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_flag = prev == n - 1u ? 1u : 0u;
+    if (prev == n - 1u) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  return *s_flag != 0u;
+}
+
 // Map an fp32 score to a uint32 key with the same order (larger float ->
 // larger key).  -0.0 and +0.0 map to adjacent keys (torch.topk treats them
 // as equal; scores of exactly zero with both signs do not arise).

@@ -95,5 +95,8 @@ hipError_t launch_decode(const DecodeArgs& a, uint32_t batch, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s);
 uint32_t decode_chunks(uint32_t max_sel_pages);
 uint32_t partial_stride();
+uint32_t decode_max_chunks();  // split-K chunks per head the merge holds
+uint32_t topk_max_pages();     // pages per (sequence, head) top-k supports
+uint32_t fused_topk_max_pages();  // ... and the fused estimate + top-k kernel
 
 }  // namespace aoakv

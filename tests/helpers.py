@@ -39,7 +39,7 @@ def page_token(buf, layout, phys, kv, e):
 def read_kv(buf, layout, pages, L):
     """Gather K and V of one sequence: returns (K, V) numpy (1, H, L, D)."""
     b = buf.cpu()
-    S = b.shape[3] if layout == NHD else b.shape[4]
+    S = b.shape[2] if layout == NHD else b.shape[3]
     ks, vs = [], []
     for t in range(L):
         p, e = divmod(t, S)
@@ -53,7 +53,7 @@ def read_kv(buf, layout, pages, L):
 def read_filters(meta, layout, meta_pages, P):
     """(1, H, P, 2, D) numpy page filters from a metadata cache."""
     m = meta.cpu()
-    S = m.shape[3] if layout == NHD else m.shape[4]
+    S = m.shape[2] if layout == NHD else m.shape[3]
     out = []
     for p in range(P):
         mp, e = meta_pages[p // S], p % S

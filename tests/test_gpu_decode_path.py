@@ -114,19 +114,27 @@ def test_decode_append_trace_bit_exact(layout):
             check_metadata(ctrl, st)
 
 
-def test_chunked_prefill_append_matches_token_by_token():
-    """A bulk append onto a page that already holds tokens continues the
-    running mean token by token (same result as single-token appends)."""
-    _say("[chunked-append]")
+@pytest.mark.parametrize("layout", [NHD, HND])
+def test_chunked_prefill_append(layout):
+    """A second bulk append: the page already holding tokens continues the
+    running mean token by token (update_mean_filter); every page the chunk
+    opens gets the prefill page mean (compute_page_v_mean), as a prefill of
+    those tokens would."""
+    _say(f"[chunked-append] layout={layout}")
     H, L0, N = 4, 21, 30
     K = randn16(5, (1, H, L0 + N, D))
     V = randn16(6, (1, H, L0 + N, D))
-    ctrl = make_ctrl(H, 128, HND)
+    ctrl = make_ctrl(H, 128, layout, shuffle=2)
     prefill(ctrl, K[:, :, :L0], V[:, :, :L0])
     prefill(ctrl, K[:, :, L0:], V[:, :, L0:])
     st = sim.SimLayerState(K[:, :, :L0], V[:, :, :L0])
-    for t in range(L0, L0 + N):
+    cont = S - L0 % S                    # tokens that complete the partial page
+    for t in range(L0, L0 + cont):
         st.append(K[:, :, t:t + 1], V[:, :, t:t + 1])
+    fresh = sim.SimLayerState(K[:, :, L0 + cont:], V[:, :, L0 + cont:])
+    st.page_filters = np.concatenate([st.page_filters, fresh.page_filters], axis=2)
+    st.v_mean = np.concatenate([st.v_mean, fresh.v_mean], axis=2)
+    st.K, st.V, st.kv_len = K, V, L0 + N
     check_metadata(ctrl, st)
 
 
