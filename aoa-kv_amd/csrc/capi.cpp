@@ -432,10 +432,30 @@ int aoakv_prefill_with_paged_kv_cache(const void* q, void* o, const void* kv_dat
                                       uint32_t kv_last_page_len, uint32_t qo_len,
                                       uint32_t causal, uint32_t num_heads, uint32_t head_dim,
                                       uint32_t page_size, uint32_t layout, void* stream) {
-  (void)q; (void)o; (void)kv_data; (void)kv_indices; (void)num_kv_pages;
-  (void)kv_last_page_len; (void)qo_len; (void)causal; (void)num_heads; (void)head_dim;
-  (void)page_size; (void)layout; (void)stream;
-  return fail(AOAKV_ERR_UNSUPPORTED, "prefill_with_paged_kv_cache: not built yet");
+  if (int e = check_shape(head_dim, page_size, layout, num_heads)) return e;
+  REQUIRE(q && o && kv_data && kv_indices, "prefill_with_paged_kv_cache: null pointer argument");
+  REQUIRE(num_kv_pages >= 1u, "prefill_with_paged_kv_cache: num_kv_pages must be >= 1");
+  REQUIRE(kv_last_page_len >= 1u && kv_last_page_len <= page_size,
+          "prefill_with_paged_kv_cache: kv_last_page_len %u not in [1, %u]", kv_last_page_len,
+          page_size);
+  const uint64_t L = (uint64_t)(num_kv_pages - 1u) * page_size + kv_last_page_len;
+  REQUIRE(qo_len >= 1u && qo_len <= L,
+          "prefill_with_paged_kv_cache: qo_len %u not in [1, %llu]", qo_len,
+          (unsigned long long)L);
+  REQUIRE(L < (1ull << 31), "prefill_with_paged_kv_cache: sequence too long");
+  aoakv::PrefillArgs a{};
+  a.q = static_cast<const aoakv::f16*>(q);
+  a.o = static_cast<aoakv::f16*>(o);
+  a.kv = static_cast<const aoakv::f16*>(kv_data);
+  a.kv_indices = kv_indices;
+  a.H = num_heads;
+  a.L = (uint32_t)L;
+  a.Lq = qo_len;
+  a.causal = causal ? 1u : 0u;
+  a.sm_scale = 1.0f / aoakv::kSqrtHeadDim;
+  a.g = aoakv::make_geom(layout, num_heads, page_size, head_dim);
+  return hip_status(aoakv::launch_prefill(a, static_cast<hipStream_t>(stream)),
+                    "prefill_with_paged_kv_cache");
 }
 
 }  // extern "C"

@@ -86,6 +86,16 @@ struct DecodeArgs {
   PageGeom g;
 };
 
+struct PrefillArgs {
+  const f16* q;  // [Lq, H, D]
+  f16* o;        // [Lq, H, D]
+  const f16* kv;
+  const int32_t* kv_indices;
+  uint32_t H, L, Lq, causal;
+  float sm_scale;
+  PageGeom g;
+};
+
 hipError_t launch_append_prefill(const AppendPrefillArgs& a, hipStream_t s);
 hipError_t launch_append_decode(const AppendDecodeArgs& a, uint32_t batch, hipStream_t s);
 hipError_t launch_estimate(const EstimateArgs& a, uint32_t batch, uint32_t max_pages,
@@ -93,6 +103,7 @@ hipError_t launch_estimate(const EstimateArgs& a, uint32_t batch, uint32_t max_p
 hipError_t launch_topk(const TopkArgs& a, uint32_t batch, hipStream_t s);
 hipError_t launch_decode(const DecodeArgs& a, uint32_t batch, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s);
+hipError_t launch_prefill(const PrefillArgs& a, hipStream_t s);
 uint32_t decode_chunks(uint32_t max_sel_pages);
 uint32_t partial_stride();
 uint32_t decode_max_chunks();  // split-K chunks per head the merge holds

@@ -134,6 +134,107 @@ def decode_appends(dev, layout, n_app=512):
     return e0.elapsed_time(e1) * 1e3 / n_app
 
 
+def prefill_bench(dev, layout, L, reps=5):
+    """Config 4: causal paged prefill, 32 heads x 128, q/K/V ~ N(0, 0.5^2).
+    FLOPs as the reference's nvbench counts them (bench_prefill.cu:109-111):
+    L * (2L - L) * 2 * H * D."""
+    import torch
+    from aoakv import ops
+    from aoakv.utils import InferenceController, append_kv
+    c = InferenceController(1, H, D, S, 64, L + S, torch.float16, dev, layout=layout)
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = (torch.randn((L, H, D), generator=g, device=dev) * 0.5).half()
+    k = (torch.randn((L, H, D), generator=g, device=dev) * 0.5).half()
+    v = (torch.randn((L, H, D), generator=g, device=dev) * 0.5).half()
+    c.prepare_metadata(L)
+    c.begin_forward(L)
+    append_kv(k, v, c, 0)
+    o = torch.empty_like(q)
+    args = (q, c.kv_cache.buf_layer(0), c.kv_indices_with_last, len(c.kv_cache.indicies),
+            c.kv_cache.last_page_len, layout)
+    ops.prefill_with_paged_kv_cache(*args, o=o)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        ops.prefill_with_paged_kv_cache(*args, o=o)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    flops = L * (2 * L - L) * 2 * H * D
+    return us, flops / (us * 1e-6) / 1e12
+
+
+def ragged_batch_bench(dev, layout, reps=20):
+    """Config 5: batch 16, L_i ~ U[8192, 65536] (seeded), budget min(2048, L/8),
+    keys with 4 channels x8, values of 10% of the pages x4.  One fused layer
+    call for the whole batch; algorithmic bytes summed per sequence."""
+    import numpy as np
+    import torch
+    from aoakv import ops
+    Bn = 16
+    gen = torch.Generator().manual_seed(5)
+    Ls = torch.randint(8192, 65537, (Bn,), generator=gen).tolist()
+    budgets = [min(2048, Lb // 8) for Lb in Ls]
+    Ps = [(Lb + S - 1) // S for Lb in Ls]
+    Pms = [(Pb + S - 1) // S for Pb in Ps]
+    tot, totm = sum(Ps), sum(Pms)
+    shape = (tot, 2, H, S, D) if layout == ops.HND else (tot, 2, S, H, D)
+    mshape = (totm, 2, H, S, D) if layout == ops.HND else (totm, 2, S, H, D)
+    kv = torch.empty(shape, dtype=torch.float16, device=dev)
+    meta = torch.empty(mshape, dtype=torch.float16, device=dev)
+    lvn = torch.empty((tot, H), dtype=torch.float16, device=dev)
+    vmean = torch.empty((tot, H, D), dtype=torch.float16, device=dev)
+    perm = torch.randperm(tot, generator=gen).to(torch.int32)
+    indptr = [0]
+    mindptr = [0]
+    for Pb, Pm in zip(Ps, Pms):
+        indptr.append(indptr[-1] + Pb)
+        mindptr.append(mindptr[-1] + Pm)
+    g = torch.Generator(device=dev).manual_seed(6)
+    for b, Lb in enumerate(Ls):
+        kk = torch.randn((Lb, H, D), generator=g, device=dev)
+        ch = torch.randperm(D, generator=gen)[:4].to(dev)
+        kk[:, :, ch] *= 8.0
+        vv = torch.randn((Lb, H, D), generator=g, device=dev)
+        pages4 = torch.rand(Ps[b], generator=gen) < 0.1
+        tok4 = pages4.repeat_interleave(S)[:Lb].to(dev)
+        vv[tok4] *= 4.0
+        idx_b = perm[indptr[b]:indptr[b + 1]].to(dev)
+        midx_b = torch.arange(mindptr[b], mindptr[b + 1], dtype=torch.int32, device=dev)
+        ops.append_kv_cache_prefill(kk.half(), vv.half(), kv, idx_b, Ps[b], (Lb - 1) % S + 1,
+                                    meta, midx_b, lvn, vmean, layout)
+        del kk, vv
+    t = lambda x: torch.tensor(x, dtype=torch.int32, device=dev)
+    kv_indptr, m_indptr = t(indptr), t(mindptr)
+    kv_indices, m_indices = perm.to(dev), torch.arange(totm, dtype=torch.int32, device=dev)
+    lpl = t([(Lb - 1) % S + 1 for Lb in Ls])
+    tb = t(budgets)
+    ks = [min(max(3, min(Lb, bb) // S), Pb) for Lb, bb, Pb in zip(Ls, budgets, Ps)]
+    maxP, kmax = max(Ps), max(ks)
+    q = torch.randn((Bn, H, D), generator=g, device=dev).half()
+    o = torch.empty_like(q)
+    scores = torch.empty((Bn, H, maxP), dtype=torch.float32, device=dev)
+    sel = torch.empty((Bn, H, kmax), dtype=torch.int32, device=dev)
+    ws = ops.decode_workspace(Bn, H, H, kmax, dev)
+    call = lambda: ops.sparse_decode_layer(q, o, kv, kv_indptr, kv_indices, lpl, meta, m_indptr,
+                                           m_indices, lvn, scores, sel, 0, ws, maxP, layout,
+                                           token_budgets=tb)
+    call()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        call()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    nbytes = sum(H * Pb * (2 * D * 2 + 2) + H * kb * S * D * 2 * 2 + 2 * H * kb * 4 + 3 * H * D * 2
+                 for Pb, kb in zip(Ps, ks))
+    return {"us_per_batch_layer": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "bytes": int(nbytes), "contexts": Ls, "pages_selected": ks}
+
+
 def cpu_baseline(k0, v0, q0, reps):
     """The oracle's sparse decode of one config-2 layer on the host cores:
     page scores of all 2048 pages, top-k mask, masked attention over all
@@ -285,6 +386,13 @@ def main():
         extra["bulk_append_32k_GBps"] = round(app_bytes / (np.median(app) * 1e-6) / 1e9, 1)
         extra["bulk_append_bytes"] = app_bytes
         extra["decode_append_us"] = round(decode_appends(dev, layout), 3)
+        for Lp in (8192, 16384):
+            us, tf = prefill_bench(dev, layout, Lp)
+            extra[f"prefill_{Lp // 1024}k_us"] = round(us, 1)
+            extra[f"prefill_{Lp // 1024}k_TFLOPs"] = round(tf, 1)
+            extra[f"prefill_{Lp // 1024}k_mfma_frac"] = round(tf / 2500.0, 4)
+        log("[bench] config 5 (ragged batch) ...")
+        extra["config5_ragged_batch16"] = ragged_batch_bench(dev, layout)
 
     dom_us, dom_bytes, dom_name = (us_est, EST_BYTES, "estimate_kernel (score + fused top-k)") \
         if us_est >= us_dec else (us_dec, DEC_BYTES, "decode_kernel (split-K sparse attention)")

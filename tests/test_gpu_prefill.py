@@ -1,0 +1,106 @@
+"""GPU parity of the MFMA causal paged prefill (aoakv_prefill_with_paged_kv_cache)
+against the oracle's fp64 textbook causal attention (oracle.sim.causal_prefill_rows,
+after quest/tests/test_prefill_attention.py:17-44 and cpu_reference.h:56-159).
+
+Bar: max |o - ref| <= 2e-3 (fp16 output, fp32 accumulation).  Inputs
+q, K, V ~ N(0, 0.5^2) as in BASELINE config 4.
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import HND, NHD, randn16
+from oracle import sim
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+D, S = 128, 16
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _aoakv():
+    import aoakv  # noqa: F401
+    yield
+
+
+def _say(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def _run(L, Lq, H, layout, seed, causal=True, shuffle=None, via_utils=False):
+    from aoakv import ops
+    from aoakv.utils import InferenceController, append_kv, prefill_forward
+    q = randn16(seed, (Lq, H, D), 0.5)
+    k = randn16(seed + 1, (L, H, D), 0.5)
+    v = randn16(seed + 2, (L, H, D), 0.5)
+    c = InferenceController(1, H, D, S, 64, L + S, torch.float16, DEV, layout=layout,
+                            shuffle_seed=shuffle)
+    c.prepare_metadata(L)
+    c.begin_forward(L)
+    append_kv(torch.from_numpy(k).to(DEV), torch.from_numpy(v).to(DEV), c, 0)
+    qd = torch.from_numpy(q).to(DEV)
+    if via_utils:
+        assert Lq == L and causal
+        o = prefill_forward(qd, c, 0)
+    else:
+        o = ops.prefill_with_paged_kv_cache(qd, c.kv_cache.buf_layer(0), c.kv_indices_with_last,
+                                            len(c.kv_cache.indicies), c.kv_cache.last_page_len,
+                                            layout, causal=causal)
+    torch.cuda.synchronize()
+    return q, k, v, o.cpu().numpy()
+
+
+def _ref_rows(q, k, v, rows, causal):
+    if causal:
+        return sim.causal_prefill_rows(q, k, v, rows)
+    res = []  # non-causal: every query sees every key
+    for r in rows:
+        s = np.einsum("hd,lhd->hl", q[r].astype(np.float64), k.astype(np.float64)) / np.sqrt(D)
+        s -= s.max(-1, keepdims=True)
+        p = np.exp(s)
+        p /= p.sum(-1, keepdims=True)
+        res.append(np.einsum("hl,lhd->hd", p, v.astype(np.float64)))
+    return np.stack(res).astype(np.float32)
+
+
+@pytest.mark.parametrize("layout", [NHD, HND])
+@pytest.mark.parametrize("L,Lq", [(1, 1), (15, 15), (16, 16), (17, 17), (100, 100), (300, 300),
+                                  (300, 40), (777, 129), (1000, 1000)])
+def test_prefill_matches_causal_attention(layout, L, Lq):
+    _say(f"[prefill] layout={layout} L={L} Lq={Lq}")
+    H = 4
+    q, k, v, o = _run(L, Lq, H, layout, seed=L + Lq, shuffle=L)
+    ref = _ref_rows(q, k, v, np.arange(Lq), True)
+    err = np.abs(o.astype(np.float32) - ref).max()
+    assert err <= 2e-3, err
+
+
+def test_prefill_non_causal():
+    _say("[prefill] non-causal")
+    q, k, v, o = _run(200, 64, 2, HND, seed=5, causal=False)
+    ref = _ref_rows(q, k, v, np.arange(64), False)
+    assert np.abs(o.astype(np.float32) - ref).max() <= 2e-3
+
+
+def test_prefill_forward_via_controller():
+    _say("[prefill] utils.prefill_forward")
+    q, k, v, o = _run(333, 333, 8, HND, seed=9, shuffle=2, via_utils=True)
+    ref = _ref_rows(q, k, v, np.arange(333), True)
+    assert np.abs(o.astype(np.float32) - ref).max() <= 2e-3
+
+
+@pytest.mark.parametrize("layout", [NHD, HND])
+def test_prefill_config4_8k_sampled_rows(layout):
+    """BASELINE config 4 shape (32 heads, 8192 tokens); rows sampled across the
+    causal range, including tile and page boundaries."""
+    _say(f"[prefill] config-4 8k layout={layout}")
+    L = 8192
+    q, k, v, o = _run(L, L, 32, layout, seed=0, shuffle=4)
+    rows = np.array([0, 1, 15, 16, 63, 64, 127, 128, 129, 1000, 4095, 4096, 6000, 8126, 8190, 8191])
+    ref = _ref_rows(q, k, v, rows, True)
+    err = np.abs(o[rows].astype(np.float32) - ref).max()
+    _say(f"   max err {err:.2e}")
+    assert err <= 2e-3
+    assert np.isfinite(o.astype(np.float32)).all()
