@@ -62,25 +62,35 @@ int check_group(uint32_t hq, uint32_t hkv) {
 }
 
 struct Workspace {
+  uint32_t* ctl;  // [0] ticket counter, [1] finished blocks, [2] error flag
   uint32_t* est_counters;
   uint32_t* dec_counters;
+  uint32_t* ready;
   float* partial;
   size_t bytes;
 };
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-// [est counters: B*Hkv u32][dec counters: B*Hq u32][partials: B*Hq*chunks*stride f32]
+// [ctl: 64 u32][est counters: B*Hkv][dec counters: B*Hq][ready: B*Hkv]
+// [partials: B*Hq*chunks*stride f32]; every region 256-byte aligned.  The
+// control words sit at offset 0 so a caller can read the error flag
+// (word 2) without knowing the shapes.
 size_t ws_layout(uint32_t B, uint32_t hq, uint32_t hkv, uint32_t max_sel_pages, void* base,
                  Workspace* w) {
-  size_t off_dec = round_up((size_t)B * hkv * 4u, 256);
-  size_t off_part = off_dec + round_up((size_t)B * hq * 4u, 256);
-  size_t part = (size_t)B * hq * aoakv::decode_chunks(max_sel_pages) * aoakv::partial_stride() * 4u;
-  size_t total = off_part + round_up(part, 256);
+  const size_t off_est = 256;
+  const size_t off_dec = off_est + round_up((size_t)B * hkv * 4u, 256);
+  const size_t off_rdy = off_dec + round_up((size_t)B * hq * 4u, 256);
+  const size_t off_part = off_rdy + round_up((size_t)B * hkv * 4u, 256);
+  const size_t part =
+      (size_t)B * hq * aoakv::decode_chunks(max_sel_pages) * aoakv::partial_stride() * 4u;
+  const size_t total = off_part + round_up(part, 256);
   if (w) {
     char* c = static_cast<char*>(base);
-    w->est_counters = reinterpret_cast<uint32_t*>(c);
+    w->ctl = reinterpret_cast<uint32_t*>(c);
+    w->est_counters = reinterpret_cast<uint32_t*>(c + off_est);
     w->dec_counters = reinterpret_cast<uint32_t*>(c + off_dec);
+    w->ready = reinterpret_cast<uint32_t*>(c + off_rdy);
     w->partial = reinterpret_cast<float*>(c + off_part);
     w->bytes = total;
   }
@@ -231,6 +241,7 @@ static int fill_estimate(aoakv::EstimateArgs& a, const void* q, float* scores,
   a.Hkv = num_kv_heads;
   a.S = page_size;
   a.flags = flags;
+  a.max_pages = max_pages;
   a.g = aoakv::make_geom(layout, num_kv_heads, page_size, head_dim);
   return AOAKV_OK;
 }
@@ -392,6 +403,24 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
                           head_dim, page_size, layout))
     return e;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (max_pages <= aoakv::fused_topk_max_pages()) {
+    // one launch: scoring, top-k and decode items of every head
+    aoakv::LayerArgs la{};
+    la.e = ea;
+    la.e.sel = sel_pages;
+    la.e.sel_stride = sel_stride;
+    la.e.token_budget = token_budget;
+    la.e.token_budgets = token_budgets;
+    la.e.counters = w.est_counters;
+    la.d = da;
+    la.est_chunks = aoakv::est_chunks(max_pages);
+    la.n_est = batch_size * num_kv_heads * la.est_chunks;
+    la.n_dec = batch_size * num_qo_heads * da.max_chunks;
+    la.n_ready = batch_size * num_kv_heads;
+    la.ready = w.ready;
+    la.ctl = w.ctl;
+    return hip_status(aoakv::launch_layer(la, s), "sparse_decode_layer");
+  }
   if (int e = launch_estimate_topk(ea, w, sel_pages, sel_stride, token_budget, token_budgets,
                                    batch_size, max_pages, page_size, flags, s))
     return e;

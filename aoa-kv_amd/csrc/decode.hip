@@ -109,7 +109,7 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
   const uint32_t lane = __lane_id();
   const uint32_t wave = tid / kWave;
   if (k >= P) {  // everything selected
-    for (uint32_t i = tid; i < P; i += kThreads) out[i] = kv_ids[i];
+    for (uint32_t i = tid; i < P; i += kThreads) st_agent_i32(out + i, kv_ids[i]);
     return;
   }
   const uint32_t kpt = (P + kThreads - 1) / kThreads;
@@ -239,7 +239,7 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
   uint32_t pos = sel_before;
 #pragma unroll
   for (int j = 0; j < KPT; ++j)
-    if ((take_mask >> j) & 1ull) out[pos++] = kv_ids[i0 + j];
+    if ((take_mask >> j) & 1ull) st_agent_i32(out + pos++, kv_ids[i0 + j]);
 }
 
 // Pages per head the fused estimate + top-k kernel selects from (16 keys per
@@ -254,21 +254,30 @@ constexpr uint32_t kFusedTopkMaxPages = 16u * kThreads;
 // Grid (page chunks of 128, kv heads, batch); a wave scores 32 consecutive
 // pages = two metadata pages (page_size 16), so its metadata page indices
 // are two scalar loads.
+struct EstShared {
+  TopkShared tk;
+  float sc[kEstPagesPerBlock];
+  uint32_t last;
+};
+
+// Scores pages [128*chunk, 128*chunk + 128) of (sequence b, kv head h); with
+// a.sel set, the last block of the head also selects its pages.  Returns
+// true in the block that wrote the head's selection.
 template <int GROUP>
-__global__ __launch_bounds__(kThreads) void estimate_kernel(EstimateArgs a) {
-  __shared__ TopkShared sh;
-  __shared__ float s_sc[kEstPagesPerBlock];
-  __shared__ uint32_t s_last;
+__device__ __forceinline__ bool estimate_item(const EstimateArgs& a, uint32_t b, uint32_t h,
+                                              uint32_t chunk, EstShared& sm) {
+  TopkShared& sh = sm.tk;
+  float* s_sc = sm.sc;
   const uint32_t lane = __lane_id();
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t row = lane / kLanesPerRow;
   const uint32_t l16 = lane % kLanesPerRow;
-  const uint32_t b = blockIdx.z, h = blockIdx.y, chunk = blockIdx.x;
   const uint32_t pbeg = (uint32_t)a.kv_indptr[b];
   uint32_t P = (uint32_t)a.kv_indptr[b + 1] - pbeg;
   if (P > a.score_stride) P = a.score_stride;  // never write past a score row
+  if (P > a.max_pages) P = a.max_pages;        // the grid covers max_pages per head
   if (P > kFusedTopkMaxPages && a.sel != nullptr) P = kFusedTopkMaxPages;
-  if (chunk * kEstPagesPerBlock >= P) return;  // uniform per block
+  if (chunk * kEstPagesPerBlock >= P) return false;  // uniform per block
   const uint32_t mbeg = (uint32_t)a.meta_indptr[b];
   const uint32_t d0 = l16 * kVec;
   const bool value_aware = (a.flags & 1u) != 0u;
@@ -354,16 +363,23 @@ __global__ __launch_bounds__(kThreads) void estimate_kernel(EstimateArgs a) {
     if (threadIdx.x < (uint32_t)kEstPagesPerBlock && p < P) st_agent(out + p, s_sc[threadIdx.x]);
   }
 
-  if (a.sel == nullptr) return;
+  if (a.sel == nullptr) return false;
   // ---- fused top-k: the last block of this (sequence, head) selects
   const uint32_t nch = (P + kEstPagesPerBlock - 1) / kEstPagesPerBlock;
-  if (!arrive_last(&a.counters[b * a.Hkv + h], nch, &s_last)) return;
+  if (!arrive_last(&a.counters[b * a.Hkv + h], nch, &sm.last)) return false;
   const uint32_t L = (P - 1u) * kPageSize + (uint32_t)a.kv_last_page_len[b];
   const uint32_t budget = a.token_budgets ? (uint32_t)a.token_budgets[b] : a.token_budget;
   uint32_t k = num_selected_pages(L, budget, kPageSize, P);
   if (k > a.sel_stride) k = a.sel_stride;  // never write past a selection row
   topk_block<16>(out, P, k, (a.flags & 2u) != 0u, a.kv_indices + pbeg,
                  a.sel + ((size_t)b * a.Hkv + h) * a.sel_stride, sh);
+  return true;
+}
+
+template <int GROUP>
+__global__ __launch_bounds__(kThreads) void estimate_kernel(EstimateArgs a) {
+  __shared__ EstShared sm;
+  estimate_item<GROUP>(a, blockIdx.z, blockIdx.y, blockIdx.x, sm);
 }
 
 __global__ __launch_bounds__(kThreads) void topk_kernel(TopkArgs a) {
@@ -391,17 +407,34 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopkArgs a) {
 // sparse decode attention, split-K over pages with a fused merge
 // ======================================================================
 
-__global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
-  __shared__ float s_o[4][kHeadDim];
-  __shared__ float s_ml[4][2];
-  __shared__ float s_m[kMergeMaxChunks], s_l[kMergeMaxChunks];
-  __shared__ float s4[4];
-  __shared__ uint32_t s_last;
+struct DecShared {
+  float o[4][kHeadDim];
+  float ml[4][2];
+  float m[kMergeMaxChunks], l[kMergeMaxChunks];
+  float s4[4];
+  uint32_t last, ok;
+};
+
+// Bound on polls of a ready flag before a decode item gives up (it then
+// flags an error and skips its pages, so every wave still exits).
+constexpr uint32_t kSpinLimit = 1u << 18;
+
+// Attends pages [8*chunk, 8*chunk + 8) of the selection of (sequence b,
+// query head hq) and, in the last block of the head, merges the chunks.
+// With `ready` set, waits first for the head's selection to be published
+// in this launch (ready[b * Hkv + hkv] != 0).
+__device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uint32_t hq,
+                                            uint32_t chunk, DecShared& sm, const uint32_t* ready,
+                                            uint32_t* error) {
+  float (*s_o)[kHeadDim] = sm.o;
+  float (*s_ml)[2] = sm.ml;
+  float* s_m = sm.m;
+  float* s_l = sm.l;
+  float* s4 = sm.s4;
   const uint32_t lane = __lane_id();
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t row = lane / kLanesPerRow;
   const uint32_t l16 = lane % kLanesPerRow;
-  const uint32_t b = blockIdx.z, hq = blockIdx.y, chunk = blockIdx.x;
   const uint32_t hkv = hq / (a.Hq / a.Hkv);
   const uint32_t S = kPageSize;
   const uint32_t pbeg = (uint32_t)a.kv_indptr[b];
@@ -420,6 +453,22 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
   if (npages > cap * kDecPagesPerBlock) npages = cap * kDecPagesPerBlock;
   const uint32_t nch = (npages + kDecPagesPerBlock - 1) / kDecPagesPerBlock;
   if (chunk >= nch) return;  // uniform per block
+  if (ready != nullptr && a.sel != nullptr) {
+    if (threadIdx.x == 0) {
+      uint32_t ok = 1u, it = 0u;
+      while (ld_agent_u32(ready + b * a.Hkv + hkv) == 0u) {
+        __builtin_amdgcn_s_sleep(2);
+        if (++it > kSpinLimit) {
+          atomicOr(error, 1u);
+          ok = 0u;
+          break;
+        }
+      }
+      sm.ok = ok;
+    }
+    __syncthreads();
+    if (sm.ok == 0u) return;
+  }
   const uint32_t last_phys = (uint32_t)a.kv_indices[pbeg + P - 1u];
   const uint32_t d0 = l16 * kVec;
   const size_t bh = (size_t)b * a.Hq + hq;
@@ -432,7 +481,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
     ntok[s] = 0u;
     phys[s] = 0u;
     if (idx < npages) {
-      phys[s] = a.sel ? (uint32_t)a.sel[((size_t)b * a.Hkv + hkv) * a.sel_stride + idx]
+      phys[s] = a.sel ? ld_agent_u32(reinterpret_cast<const uint32_t*>(a.sel) +
+                                     ((size_t)b * a.Hkv + hkv) * a.sel_stride + idx)
                       : (uint32_t)a.kv_indices[pbeg + idx];
       ntok[s] = phys[s] == last_phys ? lpl : S;
     }
@@ -526,7 +576,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
   }
 
   // ---- the last block of this (sequence, head) merges the chunks
-  if (!arrive_last(&a.counters[bh], nch, &s_last)) return;
+  if (!arrive_last(&a.counters[bh], nch, &sm.last)) return;
   const float* base = a.partial + bh * a.max_chunks * kPartialStride;
   // (m, l) of every chunk, loaded together
   float mc = -INFINITY;
@@ -567,6 +617,69 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
   if (half == 0u) a.o[bh * kHeadDim + d] = r16((acc + s_o[0][d]) / Lsum);
 }
 
+__global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
+  __shared__ DecShared sm;
+  decode_item(a, blockIdx.z, blockIdx.y, blockIdx.x, sm, nullptr, nullptr);
+}
+
+// ======================================================================
+// one launch per decode layer
+// ======================================================================
+//
+// Workgroups take tickets from an atomic counter in the order they start.
+// Tickets [0, n_est) are scoring items ordered head by head (the last item
+// of a head also runs its top-k and publishes a ready flag); tickets
+// [n_est, n_est + n_dec) are decode items, also head by head, which wait for
+// their head's flag.  A decode item only ever waits on items with smaller
+// tickets, i.e. on workgroups that have already started, and those never
+// wait, so the wait always ends (and is bounded by kSpinLimit regardless).
+// The last workgroup to finish resets the ticket counter and the flags.
+template <int GROUP>
+__global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
+  __shared__ union {
+    EstShared e;
+    DecShared d;
+  } sm;
+  __shared__ uint32_t s_ticket, s_fin;
+  if (threadIdx.x == 0)
+    s_ticket = __hip_atomic_fetch_add(la.ctl + 0, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const uint32_t t = s_ticket;
+  if (t < la.n_est) {
+    const uint32_t bh = t / la.est_chunks, chunk = t % la.est_chunks;
+    const uint32_t b = bh / la.e.Hkv, h = bh % la.e.Hkv;
+    if (estimate_item<GROUP>(la.e, b, h, chunk, sm.e)) {
+      // the head's selection is written: publish it
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (threadIdx.x == 0)
+        __hip_atomic_store(la.ready + b * la.e.Hkv + h, 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+  } else if (t < la.n_est + la.n_dec) {
+    const uint32_t u = t - la.n_est;
+    const uint32_t bh = u / la.d.max_chunks, chunk = u % la.d.max_chunks;
+    const uint32_t b = bh / la.d.Hq, hq = bh % la.d.Hq;
+    decode_item(la.d, b, hq, chunk, sm.d, la.ready, la.ctl + 2);
+  }
+  // ---- the last workgroup to finish resets the launch state
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev =
+        __hip_atomic_fetch_add(la.ctl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_fin = prev == gridDim.x - 1u ? 1u : 0u;
+  }
+  __syncthreads();
+  if (s_fin != 0u) {
+    for (uint32_t i = threadIdx.x; i < la.n_ready; i += kThreads)
+      __hip_atomic_store(la.ready + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) {
+      __hip_atomic_store(la.ctl + 0, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(la.ctl + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
 __global__ void fill_u32_kernel(uint32_t* p, size_t n, uint32_t v) {
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
@@ -585,6 +698,22 @@ hipError_t launch_estimate(const EstimateArgs& a, uint32_t batch, uint32_t max_p
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+hipError_t launch_layer(const LayerArgs& la, hipStream_t s) {
+  const uint32_t grid = la.n_est + la.n_dec;
+  switch (la.e.Hq / la.e.Hkv) {
+    case 1: hipLaunchKernelGGL(layer_kernel<1>, dim3(grid), dim3(kThreads), 0, s, la); break;
+    case 2: hipLaunchKernelGGL(layer_kernel<2>, dim3(grid), dim3(kThreads), 0, s, la); break;
+    case 4: hipLaunchKernelGGL(layer_kernel<4>, dim3(grid), dim3(kThreads), 0, s, la); break;
+    case 8: hipLaunchKernelGGL(layer_kernel<8>, dim3(grid), dim3(kThreads), 0, s, la); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+uint32_t est_chunks(uint32_t max_pages) {
+  return (max_pages + kEstPagesPerBlock - 1) / kEstPagesPerBlock;
 }
 
 hipError_t launch_topk(const TopkArgs& a, uint32_t batch, hipStream_t s) {

@@ -47,6 +47,7 @@ struct EstimateArgs {
   const int32_t* kv_last_page_len;
   const f16* v_log_norm;  // [max_pages, Hkv]
   uint32_t Hq, Hkv, S, flags;
+  uint32_t max_pages;  // pages the grid covers per (sequence, head)
   PageGeom g;
   // fused top-k (sel == nullptr: scores only)
   int32_t* sel;
@@ -96,11 +97,25 @@ struct PrefillArgs {
   PageGeom g;
 };
 
+// One decode layer in one launch (see layer_kernel in decode.hip).
+struct LayerArgs {
+  EstimateArgs e;      // with sel / counters of the fused top-k
+  DecodeArgs d;
+  uint32_t n_est;      // scoring items: B * Hkv * est_chunks
+  uint32_t est_chunks; // 128-page chunks per (sequence, head) item row
+  uint32_t n_dec;      // decode items: B * Hq * d.max_chunks
+  uint32_t n_ready;    // B * Hkv
+  uint32_t* ready;     // [B * Hkv] selection published in this launch
+  uint32_t* ctl;       // [0] ticket counter, [1] finished blocks, [2] error flag
+};
+
 hipError_t launch_append_prefill(const AppendPrefillArgs& a, hipStream_t s);
 hipError_t launch_append_decode(const AppendDecodeArgs& a, uint32_t batch, hipStream_t s);
 hipError_t launch_estimate(const EstimateArgs& a, uint32_t batch, uint32_t max_pages,
                            hipStream_t s);
 hipError_t launch_topk(const TopkArgs& a, uint32_t batch, hipStream_t s);
+hipError_t launch_layer(const LayerArgs& la, hipStream_t s);
+uint32_t est_chunks(uint32_t max_pages);
 hipError_t launch_decode(const DecodeArgs& a, uint32_t batch, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s);
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t s);
