@@ -16,6 +16,7 @@ AOAKV_ERR_HIP = 3
 
 FLAG_VALUE_AWARE = 1
 FLAG_FIXED = 2
+FLAG_SINGLE_LAUNCH = 4
 
 _u32 = ctypes.c_uint32
 _p = ctypes.c_void_p

@@ -11,7 +11,7 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._lib import FLAG_FIXED, FLAG_VALUE_AWARE  # noqa: F401  (re-exported)
+from ._lib import FLAG_FIXED, FLAG_SINGLE_LAUNCH, FLAG_VALUE_AWARE  # noqa: F401  (re-exported)
 
 NHD = 0
 HND = 1

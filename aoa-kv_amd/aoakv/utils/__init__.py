@@ -109,9 +109,10 @@ def decode_sparse_attn(q: torch.Tensor, iController: InferenceController, layer_
     return o.view_as(q)
 
 
-def decode_layer(q: torch.Tensor, iController: InferenceController, layer_idx: int
-                 ) -> torch.Tensor:
-    """estimate + top-k + sparse decode in two launches (fused entry point)."""
+def decode_layer(q: torch.Tensor, iController: InferenceController, layer_idx: int,
+                 single_launch: bool = False) -> torch.Tensor:
+    """estimate + top-k + sparse decode in two launches (or one, with
+    ``single_launch``)."""
     c = iController
     q3 = q.view(1, c.num_heads, c.head_dim)
     o = torch.empty_like(q3)
@@ -120,5 +121,5 @@ def decode_layer(q: torch.Tensor, iController: InferenceController, layer_idx: i
         c.kv_last_page_len_t, c.metadata_cache.buf_layer(layer_idx),
         c.metadata_indptr_for_append, c.metadata_indices, c.v_log_norm_layer(layer_idx),
         c.scores, c._sel, c.token_budget, c.workspace, len(c.kv_cache.indicies), c.layout,
-        c.flags)
+        c.flags | (ops.FLAG_SINGLE_LAUNCH if single_launch else 0))
     return o.view_as(q)

@@ -226,7 +226,7 @@ static int fill_estimate(aoakv::EstimateArgs& a, const void* q, float* scores,
           batch_size);
   REQUIRE(max_pages >= 1u && score_stride >= max_pages,
           "estimate_attn_score: score_stride %u < max_pages %u", score_stride, max_pages);
-  REQUIRE((flags & ~3u) == 0u, "estimate_attn_score: unknown flags 0x%x", flags);
+  REQUIRE((flags & ~7u) == 0u, "estimate_attn_score: unknown flags 0x%x", flags);
   a.q = static_cast<const aoakv::f16*>(q);
   a.scores = scores;
   a.score_stride = score_stride;
@@ -403,7 +403,8 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
                           head_dim, page_size, layout))
     return e;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (max_pages <= aoakv::fused_topk_max_pages()) {
+  ea.flags &= 3u;
+  if ((flags & AOAKV_FLAG_SINGLE_LAUNCH) && max_pages <= aoakv::fused_topk_max_pages()) {
     // one launch: scoring, top-k and decode items of every head
     aoakv::LayerArgs la{};
     la.e = ea;

@@ -33,14 +33,33 @@ constexpr uint32_t kTopkMaxPages = 16384;
 // block-wide helpers (256 threads = 4 waves)
 // ======================================================================
 
+// Inclusive prefix sum over the 64 lanes of a wave: DPP row_shr steps inside
+// each 16-lane row, then the totals of the rows below through readlane.
 __device__ inline uint32_t wave_incl_scan(uint32_t v) {
-  const uint32_t lane = __lane_id();
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const uint32_t t = __shfl_up(v, off);
-    if ((int)lane >= off) v += t;
-  }
-  return v;
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 15);
+  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 31);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 47);
+  const uint32_t row = __lane_id() / kLanesPerRow;
+  return v + (row > 0u ? r0 : 0u) + (row > 1u ? r1 : 0u) + (row > 2u ? r2 : 0u);
+}
+
+// min / max of a uint32 over the wave (DPP inside rows, readlane across)
+template <bool MAX>
+__device__ inline uint32_t wave_reduce_u32(uint32_t v) {
+  auto op = [](uint32_t x, uint32_t y) { return MAX ? (x > y ? x : y) : (x < y ? x : y); };
+  v = op(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kQuadSwap1, 0xf, 0xf, true));
+  v = op(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kQuadSwap2, 0xf, 0xf, true));
+  v = op(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kRowHalfMirror, 0xf, 0xf, true));
+  v = op(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kRowMirror, 0xf, 0xf, true));
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+  const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+  const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return op(op(a, b), op(c, d));
 }
 
 // Exclusive prefix sum of v over the block (thread order); *total = sum.
@@ -114,13 +133,17 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
   }
   const uint32_t kpt = (P + kThreads - 1) / kThreads;
   const uint32_t i0 = tid * kpt;
+  sh.hist[tid] = 0u;  // first pass histogram (visible after the barrier below)
 
-  // all of this thread's scores are loaded before any is used
+  // all of this thread's scores and page ids are loaded before any is used
   float sc[KPT];
+  int32_t id[KPT];
 #pragma unroll
   for (int j = 0; j < KPT; ++j) {
     const uint32_t i = i0 + j;
-    sc[j] = ((uint32_t)j < kpt && i < P) ? ld_agent(scores + i) : 0.f;
+    const bool valid = (uint32_t)j < kpt && i < P;
+    sc[j] = valid ? ld_agent(scores + i) : 0.f;
+    id[j] = valid ? kv_ids[i] : 0;
   }
   uint32_t key[KPT];
   uint64_t free_mask = 0, valid_mask = 0;  // bit j: page i0+j exists / is not forced
@@ -138,12 +161,8 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
       kmax = key[j] > kmax ? key[j] : kmax;
     }
   }
-  for (int off = 32; off > 0; off >>= 1) {
-    const uint32_t a = __shfl_xor(kmin, off);
-    const uint32_t b = __shfl_xor(kmax, off);
-    kmin = a < kmin ? a : kmin;
-    kmax = b > kmax ? b : kmax;
-  }
+  kmin = wave_reduce_u32<false>(kmin);
+  kmax = wave_reduce_u32<true>(kmax);
   if (lane == 0) {
     sh.red[wave] = kmin;
     sh.red[4 + wave] = kmax;
@@ -163,11 +182,15 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
   uint64_t prefix = 0;
   int hi = range == 0u ? 0 : 32 - __builtin_clz(range);
   bool take_bucket = false;  // the final bucket is taken whole
+  bool first = true;
   while (hi > 0) {
     const int w = hi < 8 ? hi : 8;
     const int sft = hi - w;
-    sh.hist[tid] = 0u;
-    __syncthreads();
+    if (!first) {
+      sh.hist[tid] = 0u;
+      __syncthreads();
+    }
+    first = false;
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
       const uint64_t rel = (uint64_t)(key[j] - kmin);
@@ -177,12 +200,10 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
     __syncthreads();
     if (wave == 0) {
       // lane L holds bins 255-4L .. 252-4L (descending)
-      uint32_t c[4], s4 = 0;
+      uint32_t c[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        c[j] = sh.hist[255u - 4u * lane - j];
-        s4 += c[j];
-      }
+      for (int j = 0; j < 4; ++j) c[j] = sh.hist[255u - 4u * lane - j];
+      const uint32_t s4 = (c[0] + c[1]) + (c[2] + c[3]);
       const uint32_t incl = wave_incl_scan(s4);
       const uint32_t excl = incl - s4;
       if (excl < kr && kr <= incl) {
@@ -208,14 +229,16 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
   //   bucket: (rel >> hi) == (prefix >> hi)  -- kr of them selected: all when
   //           take_bucket, else (hi == 0, equal keys) the lowest pages first
   const uint64_t thr = prefix >> hi;
-  uint32_t n_eq = 0;
-#pragma unroll
-  for (int j = 0; j < KPT; ++j)
-    if ((free_mask >> j) & 1ull) n_eq += ((uint64_t)(key[j] - kmin) >> hi) == thr ? 1u : 0u;
   uint32_t tot;
-  const uint32_t eq_before = block_excl_scan(n_eq, sh.s4, &tot);
+  uint32_t eq_seen = 0;
+  if (!take_bucket) {  // ties: rank the equal keys by page index
+    uint32_t n_eq = 0;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j)
+      if ((free_mask >> j) & 1ull) n_eq += ((uint64_t)(key[j] - kmin) >> hi) == thr ? 1u : 0u;
+    eq_seen = block_excl_scan(n_eq, sh.s4, &tot);
+  }
   uint64_t take_mask = 0;
-  uint32_t eq_seen = eq_before;
 #pragma unroll
   for (int j = 0; j < KPT; ++j) {
     if (!((valid_mask >> j) & 1ull)) continue;
@@ -239,7 +262,7 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
   uint32_t pos = sel_before;
 #pragma unroll
   for (int j = 0; j < KPT; ++j)
-    if ((take_mask >> j) & 1ull) st_agent_i32(out + pos++, kv_ids[i0 + j]);
+    if ((take_mask >> j) & 1ull) st_agent_i32(out + pos++, id[j]);
 }
 
 // Pages per head the fused estimate + top-k kernel selects from (16 keys per

@@ -364,6 +364,14 @@ def main():
 
     log(f"[bench] timing {steps} layers (graph replay) ...")
     us_layer = time_graph(g_layer, steps)
+    def layer1(l):
+        ops.sparse_decode_layer(q[l], o[l], kv[l], indptr, idx[l], lpl, meta[l], mindptr, midx,
+                                lvn[l], scores[l], sel[l], BUDGET, ws, P, layout,
+                                flags | ops.FLAG_SINGLE_LAUNCH)
+
+    g_one = capture(layer1)
+    time_graph(g_one, warm)
+    us_one = time_graph(g_one, steps)
     g_est, g_dec = capture(est), capture(dec)
     time_graph(g_est, warm)
     time_graph(g_dec, warm)
@@ -415,6 +423,7 @@ def main():
         "layer_bytes": LAYER_BYTES,
         "layer_hbm_frac": round(LAYER_BYTES / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "per_kernel_us": {"estimate_topk": round(us_est, 3), "decode": round(us_dec, 3)},
+        "single_launch_us_per_layer": round(us_one, 3),
         "graph_replay_exact": replay_exact,
         "roofline": roof,
     }

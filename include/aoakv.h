@@ -67,6 +67,9 @@ extern "C" {
 /* flags for scoring / selection */
 #define AOAKV_FLAG_VALUE_AWARE 1u /* AOA-KV score (else plain Quest bound)   */
 #define AOAKV_FLAG_FIXED 2u       /* force first and last page (sim `fixed`) */
+/* aoakv_sparse_decode_layer only: run scoring, top-k and decode in ONE launch
+ * (ticketed work items, per-head ready flags) instead of two launches. */
+#define AOAKV_FLAG_SINGLE_LAUNCH 4u
 
 /* Thread-local description of the last failure ("" when none). */
 const char* aoakv_last_error(void);

@@ -266,10 +266,16 @@ def test_full_decode_step_matches_simulation(layout, L):
         mask = sim.pages_to_token_mask(sel_logical[None, :, None], S, L)
         ref2 = sim.masked_decode_attention(q, st.K, st.V, mask)[0, :, 0].astype(np.float32)
         assert np.abs(o.astype(np.float32) - ref2).max() <= 2e-3
-    # the fused layer entry point gives the same bits as the three calls
+    # the fused layer entry points (two launches, and one launch) give the
+    # same bits as the three calls
     o2 = decode_layer(qd, ctrl, 0).cpu().numpy()[0]
     assert np.array_equal(bits(o2), bits(o))
     assert np.array_equal(ctrl.topk_dindices_buffer.cpu().numpy()[0], sel.cpu().numpy())
+    ctrl.topk_dindices_buffer.fill_(-1)
+    o3 = decode_layer(qd, ctrl, 0, single_launch=True).cpu().numpy()[0]
+    assert np.array_equal(bits(o3), bits(o))
+    assert np.array_equal(ctrl.topk_dindices_buffer.cpu().numpy()[0], sel.cpu().numpy())
+    assert int(ctrl.workspace[8:12].view(torch.int32).item()) == 0, "spin-wait error flag set"
 
 
 @pytest.mark.parametrize("layout", [NHD, HND])
