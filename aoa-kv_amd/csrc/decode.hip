@@ -18,6 +18,8 @@
 // handoff costs one memory round trip, not one per element.
 #include "kernels.hpp"
 
+#include <type_traits>
+
 namespace aoakv {
 
 constexpr int kThreads = 256;
@@ -62,68 +64,102 @@ __device__ inline uint32_t wave_reduce_u32(uint32_t v) {
   return op(op(a, b), op(c, d));
 }
 
-// Exclusive prefix sum of v over the block (thread order); *total = sum.
-__device__ inline uint32_t block_excl_scan(uint32_t v, uint32_t* s4, uint32_t* total) {
-  const uint32_t lane = __lane_id(), wave = threadIdx.x / kWave;
-  const uint32_t incl = wave_incl_scan(v);
-  if (lane == kWave - 1) s4[wave] = incl;
-  __syncthreads();
-  uint32_t before = 0, tot = 0;
-#pragma unroll
-  for (uint32_t w = 0; w < 4; ++w) {
-    const uint32_t x = s4[w];
-    before += w < wave ? x : 0u;
-    tot += x;
-  }
-  __syncthreads();
-  *total = tot;
-  return before + incl - v;
-}
-
-__device__ inline float block_max(float v, float* s4) {
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-  if (__lane_id() == 0) s4[threadIdx.x / kWave] = v;
-  __syncthreads();
-  v = fmaxf(fmaxf(s4[0], s4[1]), fmaxf(s4[2], s4[3]));
-  __syncthreads();
-  return v;
-}
-
-__device__ inline float block_sum(float v, float* s4) {
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  if (__lane_id() == 0) s4[threadIdx.x / kWave] = v;
-  __syncthreads();
-  v = (s4[0] + s4[1]) + (s4[2] + s4[3]);
-  __syncthreads();
-  return v;
-}
-
 // ======================================================================
 // top-k selection for one (sequence, kv head), one 256-thread block
 // ======================================================================
 
+// Pages whose scores and page ids are staged in LDS (16 per thread); longer
+// rows are read straight from global memory.
+constexpr uint32_t kStageMaxPages = 16u * kThreads;
+
 struct TopkShared {
-  uint32_t hist[256];
-  uint32_t s4[4];
+  alignas(16) uint32_t hist[3][kThreads];  // radix histograms, rotating over 3 buffers
+  alignas(16) uint32_t key[kStageMaxPages];  // staged order keys, then the output
+  int32_t id[kStageMaxPages];                // staged page ids
   uint32_t red[8];
-  uint32_t bin, above, count;
+  uint32_t s4[4];
 };
+
+struct RadixResult {
+  uint32_t hmask;    // bits of (key - kmin) that decide the bucket (~0u << hi)
+  uint32_t thr;      // the bucket of the k-th key: (key - kmin) & hmask == thr
+  uint32_t kr;       // keys still to take from that bucket
+  bool take_bucket;  // the bucket is taken whole (else: hi == 0, equal keys)
+};
+
+// Finds the bucket holding the kr-th largest free key (free_mask bit j: key[j]
+// takes part) by a radix select over key - kmin, 8-bit digits from the top
+// set bit of kmax - kmin down (one head's scores span a narrow range, so the
+// first digit already spreads the keys); it stops as soon as the bucket of
+// the kr-th key is taken whole.  One barrier per pass: the histogram is
+// scanned by every wave, and buffers rotate over three, so the buffer cleared
+// in pass i was last read in pass i-2, before the barrier of pass i-1.
+// hist[0] must be zero on entry.
+template <int KPT, typename Mask>
+__device__ __forceinline__ RadixResult radix_select(const uint32_t (&rel)[KPT], Mask free_mask,
+                                                    uint32_t range, uint32_t kr, TopkShared& sh) {
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = __lane_id();
+  uint32_t prefix = 0u;
+  int hi = range == 0u ? 0 : 32 - __builtin_clz(range);
+  bool take_bucket = false;
+  uint32_t buf = 0;
+  while (hi > 0) {
+    const int w = hi < 8 ? hi : 8;
+    const int sft = hi - w;
+    const uint32_t hmask = hi >= 32 ? 0u : ~0u << hi;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      if (((free_mask >> j) & (Mask)1) && ((rel[j] ^ prefix) & hmask) == 0u)
+        atomicAdd(&sh.hist[buf][(rel[j] >> sft) & ((1u << w) - 1u)], 1u);
+    }
+    const uint32_t nxt = buf == 2u ? 0u : buf + 1u;
+    sh.hist[nxt][tid] = 0u;
+    __syncthreads();
+    // lane L holds bins 255-4L .. 252-4L (descending)
+    const uint4 h = *reinterpret_cast<const uint4*>(&sh.hist[buf][252u - 4u * lane]);
+    const uint32_t s4 = (h.x + h.y) + (h.z + h.w);
+    const uint32_t incl = wave_incl_scan(s4);
+    const uint32_t excl = incl - s4;
+    const bool hit = excl < kr && kr <= incl;  // exactly one lane
+    const uint32_t c0 = excl + h.w, c1 = c0 + h.z, c2 = c1 + h.y;
+    const uint32_t j = kr <= c0 ? 0u : kr <= c1 ? 1u : kr <= c2 ? 2u : 3u;
+    const uint32_t above_l = j == 0u ? excl : j == 1u ? c0 : j == 2u ? c1 : c2;
+    const uint32_t count_l = j == 0u ? h.w : j == 1u ? h.z : j == 2u ? h.y : h.x;
+    const uint32_t src = (uint32_t)__builtin_ctzll(__builtin_amdgcn_ballot_w64(hit));
+    const uint32_t jj = (uint32_t)__builtin_amdgcn_readlane((int)j, (int)src);
+    const uint32_t above = (uint32_t)__builtin_amdgcn_readlane((int)above_l, (int)src);
+    const uint32_t count = (uint32_t)__builtin_amdgcn_readlane((int)count_l, (int)src);
+    prefix |= (255u - 4u * src - jj) << sft;
+    kr -= above;
+    hi = sft;
+    buf = nxt;
+    if (count == kr) {  // every key of the bucket is selected
+      take_bucket = true;
+      break;
+    }
+  }
+  const uint32_t hmask = hi >= 32 ? 0u : ~0u << hi;
+  return RadixResult{hmask, prefix & hmask, kr, take_bucket};
+}
 
 // Selects k of P pages from fp32 `scores` (filter_util.py:373-380): with
 // `fixed`, pages 0 and P-1 always; the rest by descending score, ties to the
 // lower page index.  Writes kv_ids[page] of the selected pages to out[] in
-// ascending page order.
+// ascending page order (agent-coherent stores).
 //
-// Thread t owns pages [t*kpt, t*kpt + kpt), kpt = ceil(P/256) <= KPT, keys
-// held in registers.  The k-th largest free key is found by a radix select
-// over the key offset from the smallest free key, 8-bit digits from the top
-// set bit of the key range down (one head's scores span a narrow range, so
-// the first digit already spreads the histogram); it stops as soon as the
-// bucket holding the k-th key is taken whole.
+// Thread t owns pages [t*kpt, t*kpt + kpt) as register keys, kpt <= KPT and
+// P <= 256 * KPT.  With KPT <= 16 scores and ids are first copied to LDS
+// with coalesced loads and the output is compacted in LDS and stored
+// coalesced; with KPT = 64 (rows up to 16384 pages) keys are read and the
+// output written per thread.
 template <int KPT>
-__device__ __forceinline__ void topk_block(const float* __restrict__ scores, uint32_t P, uint32_t k, bool fixed,
-                           const int32_t* __restrict__ kv_ids, int32_t* __restrict__ out,
-                           TopkShared& sh) {
+__device__ __forceinline__ void topk_block(const float* __restrict__ scores, uint32_t P, uint32_t k,
+                                           bool fixed, const int32_t* __restrict__ kv_ids,
+                                           int32_t* __restrict__ out, TopkShared& sh) {
+  constexpr bool kStaged = KPT <= 16;
+  static_assert(KPT % 4 == 0 && (KPT <= 16 || KPT == 64), "keys per thread");
+  using Mask = typename std::conditional<(KPT > 32), uint64_t, uint32_t>::type;
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = __lane_id();
   const uint32_t wave = tid / kWave;
@@ -131,34 +167,49 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
     for (uint32_t i = tid; i < P; i += kThreads) st_agent_i32(out + i, kv_ids[i]);
     return;
   }
-  const uint32_t kpt = (P + kThreads - 1) / kThreads;
+  // kpt rounded up to 4 so staged keys are read as 16-byte LDS vectors
+  const uint32_t kpt = kStaged ? (((P + kThreads - 1) / kThreads + 3u) & ~3u)
+                               : (P + kThreads - 1) / kThreads;
   const uint32_t i0 = tid * kpt;
-  sh.hist[tid] = 0u;  // first pass histogram (visible after the barrier below)
+  const uint32_t nforced = fixed ? (P == 1u ? 1u : 2u) : 0u;
+  auto is_free = [&](uint32_t i) { return !(fixed && (i == 0u || i == P - 1u)); };
+  sh.hist[0][tid] = 0u;
 
-  // all of this thread's scores and page ids are loaded before any is used
-  float sc[KPT];
-  int32_t id[KPT];
-#pragma unroll
-  for (int j = 0; j < KPT; ++j) {
-    const uint32_t i = i0 + j;
-    const bool valid = (uint32_t)j < kpt && i < P;
-    sc[j] = valid ? ld_agent(scores + i) : 0.f;
-    id[j] = valid ? kv_ids[i] : 0;
-  }
   uint32_t key[KPT];
-  uint64_t free_mask = 0, valid_mask = 0;  // bit j: page i0+j exists / is not forced
   uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
+  if constexpr (kStaged) {
+    // coalesced copy: all loads issued before any is used
+    float sv[KPT];
+    int32_t iv[KPT];
 #pragma unroll
-  for (int j = 0; j < KPT; ++j) {
-    const uint32_t i = i0 + j;
-    const bool valid = (uint32_t)j < kpt && i < P;
-    const bool forced = fixed && (i == 0u || i == P - 1u);
-    key[j] = order_key(sc[j]);
-    if (valid) valid_mask |= 1ull << j;
-    if (valid && !forced) {
-      free_mask |= 1ull << j;
-      kmin = key[j] < kmin ? key[j] : kmin;
-      kmax = key[j] > kmax ? key[j] : kmax;
+    for (int m = 0; m < KPT; ++m) {
+      const uint32_t i = tid + (uint32_t)m * kThreads;
+      sv[m] = i < P ? ld_agent(scores + i) : 0.f;
+      iv[m] = i < P ? kv_ids[i] : 0;
+    }
+#pragma unroll
+    for (int m = 0; m < KPT; ++m) {
+      const uint32_t i = tid + (uint32_t)m * kThreads;
+      if (i < P) {
+        const uint32_t kk = order_key(sv[m]);
+        sh.key[i] = kk;
+        sh.id[i] = iv[m];
+        if (is_free(i)) {
+          kmin = kk < kmin ? kk : kmin;
+          kmax = kk > kmax ? kk : kmax;
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const uint32_t i = i0 + j;
+      const bool valid = (uint32_t)j < kpt && i < P;
+      key[j] = order_key(valid ? ld_agent(scores + i) : 0.f);
+      if (valid && is_free(i)) {
+        kmin = key[j] < kmin ? key[j] : kmin;
+        kmax = key[j] > kmax ? key[j] : kmax;
+      }
     }
   }
   kmin = wave_reduce_u32<false>(kmin);
@@ -171,104 +222,99 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
   kmin = sh.red[0];
   kmax = sh.red[4];
 #pragma unroll
-  for (int w = 1; w < 4; ++w) {
-    kmin = sh.red[w] < kmin ? sh.red[w] : kmin;
-    kmax = sh.red[4 + w] > kmax ? sh.red[4 + w] : kmax;
+  for (int w4 = 1; w4 < 4; ++w4) {
+    kmin = sh.red[w4] < kmin ? sh.red[w4] : kmin;
+    kmax = sh.red[4 + w4] > kmax ? sh.red[4 + w4] : kmax;
   }
-  const uint32_t nforced = fixed ? (P == 1u ? 1u : 2u) : 0u;
-  uint32_t kr = k - nforced;  // >= 1 because k >= 3 whenever k < P
-
-  const uint32_t range = kmax - kmin;
-  uint64_t prefix = 0;
-  int hi = range == 0u ? 0 : 32 - __builtin_clz(range);
-  bool take_bucket = false;  // the final bucket is taken whole
-  bool first = true;
-  while (hi > 0) {
-    const int w = hi < 8 ? hi : 8;
-    const int sft = hi - w;
-    if (!first) {
-      sh.hist[tid] = 0u;
-      __syncthreads();
-    }
-    first = false;
+  if constexpr (kStaged) {
 #pragma unroll
-    for (int j = 0; j < KPT; ++j) {
-      const uint64_t rel = (uint64_t)(key[j] - kmin);
-      if (((free_mask >> j) & 1ull) && (rel >> hi) == (prefix >> hi))
-        atomicAdd(&sh.hist[(uint32_t)(rel >> sft) & ((1u << w) - 1u)], 1u);
-    }
-    __syncthreads();
-    if (wave == 0) {
-      // lane L holds bins 255-4L .. 252-4L (descending)
-      uint32_t c[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) c[j] = sh.hist[255u - 4u * lane - j];
-      const uint32_t s4 = (c[0] + c[1]) + (c[2] + c[3]);
-      const uint32_t incl = wave_incl_scan(s4);
-      const uint32_t excl = incl - s4;
-      if (excl < kr && kr <= incl) {
-        // first of this lane's 4 bins whose running count reaches kr
-        const uint32_t c0 = excl + c[0], c1 = c0 + c[1], c2 = c1 + c[2];
-        const uint32_t j = kr <= c0 ? 0u : kr <= c1 ? 1u : kr <= c2 ? 2u : 3u;
-        sh.bin = 255u - 4u * lane - j;
-        sh.above = j == 0u ? excl : j == 1u ? c0 : j == 2u ? c1 : c2;
-        sh.count = j == 0u ? c[0] : j == 1u ? c[1] : j == 2u ? c[2] : c[3];
-      }
-    }
-    __syncthreads();
-    prefix |= (uint64_t)sh.bin << sft;
-    kr -= sh.above;
-    hi = sft;
-    if (sh.count == kr) {  // uniform: every key of the bucket is selected
-      take_bucket = true;
-      break;
+    for (int c = 0; c < KPT / 4; ++c) {
+      const uint4 v = *reinterpret_cast<const uint4*>(&sh.key[i0 + 4u * c]);
+      key[4 * c + 0] = v.x;
+      key[4 * c + 1] = v.y;
+      key[4 * c + 2] = v.z;
+      key[4 * c + 3] = v.w;
     }
   }
-  // selection classes at the final resolution `hi`:
-  //   above:  (rel >> hi) >  (prefix >> hi)  -- selected
-  //   bucket: (rel >> hi) == (prefix >> hi)  -- kr of them selected: all when
-  //           take_bucket, else (hi == 0, equal keys) the lowest pages first
-  const uint64_t thr = prefix >> hi;
-  uint32_t tot;
-  uint32_t eq_seen = 0;
-  if (!take_bucket) {  // ties: rank the equal keys by page index
-    uint32_t n_eq = 0;
-#pragma unroll
-    for (int j = 0; j < KPT; ++j)
-      if ((free_mask >> j) & 1ull) n_eq += ((uint64_t)(key[j] - kmin) >> hi) == thr ? 1u : 0u;
-    eq_seen = block_excl_scan(n_eq, sh.s4, &tot);
-  }
-  uint64_t take_mask = 0;
+  Mask free_mask = 0, valid_mask = 0;  // bit j: page i0+j exists / is not forced
+  uint32_t rel[KPT];
 #pragma unroll
   for (int j = 0; j < KPT; ++j) {
-    if (!((valid_mask >> j) & 1ull)) continue;
-    bool take;
-    if (!((free_mask >> j) & 1ull)) {
-      take = true;  // forced page
-    } else {
-      const uint64_t r = (uint64_t)(key[j] - kmin) >> hi;
-      if (r > thr) {
-        take = true;
-      } else if (r == thr) {
-        take = take_bucket || eq_seen < kr;
-        ++eq_seen;
-      } else {
-        take = false;
-      }
+    const uint32_t i = i0 + j;
+    rel[j] = key[j] - kmin;
+    if ((uint32_t)j < kpt && i < P) {
+      valid_mask |= (Mask)1 << j;
+      if (is_free(i)) free_mask |= (Mask)1 << j;
     }
-    if (take) take_mask |= 1ull << j;
   }
-  const uint32_t sel_before = block_excl_scan((uint32_t)__builtin_popcountll(take_mask), sh.s4, &tot);
-  uint32_t pos = sel_before;
+  // >= 1 because k >= 3 whenever k < P
+  const RadixResult rr = radix_select<KPT, Mask>(rel, free_mask, kmax - kmin, k - nforced, sh);
+
+  // selection classes at the final resolution:
+  //   above:  forced, or (rel & hmask) > thr  -- selected
+  //   bucket: (rel & hmask) == thr            -- rr.kr of them selected: all when
+  //           take_bucket, else (equal keys) the lowest pages first
+  Mask above_m = 0, eq_m = 0;
 #pragma unroll
-  for (int j = 0; j < KPT; ++j)
-    if ((take_mask >> j) & 1ull) st_agent_i32(out + pos++, id[j]);
+  for (int j = 0; j < KPT; ++j) {
+    if (!((valid_mask >> j) & 1u)) continue;
+    const uint32_t r = rel[j] & rr.hmask;
+    if (!((free_mask >> j) & 1u) || r > rr.thr) above_m |= (Mask)1 << j;
+    else if (r == rr.thr) eq_m |= (Mask)1 << j;
+  }
+  // one scan of (pages above, bucket pages) packed in 16-bit halves gives the
+  // output position: selected pages before mine = above before + min(bucket
+  // pages before, kr)
+  const uint32_t na = (uint32_t)__builtin_popcountll((uint64_t)above_m);
+  const uint32_t ne = (uint32_t)__builtin_popcountll((uint64_t)eq_m);
+  const uint32_t packed = na | (ne << 16);
+  const uint32_t incl = wave_incl_scan(packed);
+  if (lane == kWave - 1) sh.s4[wave] = incl;
+  __syncthreads();
+  uint32_t before = incl - packed;
+#pragma unroll
+  for (uint32_t w4 = 0; w4 < 4; ++w4) before += w4 < wave ? sh.s4[w4] : 0u;
+  const uint32_t eq_before = before >> 16;
+  uint32_t pos = (before & 0xFFFFu) + (eq_before < rr.kr ? eq_before : rr.kr);
+  uint32_t eq_rank = eq_before;
+  if constexpr (kStaged) {
+    // every key read from sh.key finished before the barrier above, so
+    // sh.key takes the compacted output
+    uint32_t* s_out = sh.key;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      bool take = (above_m >> j) & 1u;
+      if ((eq_m >> j) & 1u) take = rr.take_bucket || eq_rank++ < rr.kr;
+      if (take) s_out[pos++] = (uint32_t)sh.id[i0 + j];
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < k; i += kThreads) st_agent_i32(out + i, (int32_t)s_out[i]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      bool take = (above_m >> j) & 1u;
+      if ((eq_m >> j) & 1u) take = rr.take_bucket || eq_rank++ < rr.kr;
+      if (take) st_agent_i32(out + pos++, kv_ids[i0 + j]);
+    }
+  }
+}
+
+// top-k of a row of P <= kStageMaxPages pages with the fewest keys per thread
+__device__ __forceinline__ void topk_staged(const float* __restrict__ scores, uint32_t P, uint32_t k,
+                                            bool fixed, const int32_t* __restrict__ kv_ids,
+                                            int32_t* __restrict__ out, TopkShared& sh) {
+  if (P <= 4u * kThreads)
+    topk_block<4>(scores, P, k, fixed, kv_ids, out, sh);
+  else if (P <= 8u * kThreads)
+    topk_block<8>(scores, P, k, fixed, kv_ids, out, sh);
+  else
+    topk_block<16>(scores, P, k, fixed, kv_ids, out, sh);
 }
 
 // Pages per head the fused estimate + top-k kernel selects from (16 keys per
 // thread keep its register count at the scoring kernel's); longer sequences
 // use the standalone top-k kernel.
-constexpr uint32_t kFusedTopkMaxPages = 16u * kThreads;
+constexpr uint32_t kFusedTopkMaxPages = kStageMaxPages;
 
 // ======================================================================
 // page scores (+ optional fused top-k)
@@ -278,9 +324,12 @@ constexpr uint32_t kFusedTopkMaxPages = 16u * kThreads;
 // pages = two metadata pages (page_size 16), so its metadata page indices
 // are two scalar loads.
 struct EstShared {
-  TopkShared tk;
   float sc[kEstPagesPerBlock];
   uint32_t last;
+};
+struct EstTopkShared {
+  EstShared e;
+  TopkShared tk;
 };
 
 // Scores pages [128*chunk, 128*chunk + 128) of (sequence b, kv head h); with
@@ -288,8 +337,7 @@ struct EstShared {
 // true in the block that wrote the head's selection.
 template <int GROUP>
 __device__ __forceinline__ bool estimate_item(const EstimateArgs& a, uint32_t b, uint32_t h,
-                                              uint32_t chunk, EstShared& sm) {
-  TopkShared& sh = sm.tk;
+                                              uint32_t chunk, EstShared& sm, TopkShared* tk) {
   float* s_sc = sm.sc;
   const uint32_t lane = __lane_id();
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -301,6 +349,12 @@ __device__ __forceinline__ bool estimate_item(const EstimateArgs& a, uint32_t b,
   if (P > a.max_pages) P = a.max_pages;        // the grid covers max_pages per head
   if (P > kFusedTopkMaxPages && a.sel != nullptr) P = kFusedTopkMaxPages;
   if (chunk * kEstPagesPerBlock >= P) return false;  // uniform per block
+  // the selection size of the fused top-k, loaded up front (off the handoff path)
+  uint32_t lpl = 0u, budget = 0u;
+  if (a.sel != nullptr) {
+    lpl = (uint32_t)a.kv_last_page_len[b];
+    budget = a.token_budgets ? (uint32_t)a.token_budgets[b] : a.token_budget;
+  }
   const uint32_t mbeg = (uint32_t)a.meta_indptr[b];
   const uint32_t d0 = l16 * kVec;
   const bool value_aware = (a.flags & 1u) != 0u;
@@ -390,19 +444,23 @@ __device__ __forceinline__ bool estimate_item(const EstimateArgs& a, uint32_t b,
   // ---- fused top-k: the last block of this (sequence, head) selects
   const uint32_t nch = (P + kEstPagesPerBlock - 1) / kEstPagesPerBlock;
   if (!arrive_last(&a.counters[b * a.Hkv + h], nch, &sm.last)) return false;
-  const uint32_t L = (P - 1u) * kPageSize + (uint32_t)a.kv_last_page_len[b];
-  const uint32_t budget = a.token_budgets ? (uint32_t)a.token_budgets[b] : a.token_budget;
-  uint32_t k = num_selected_pages(L, budget, kPageSize, P);
+  uint32_t k = num_selected_pages((P - 1u) * kPageSize + lpl, budget, kPageSize, P);
   if (k > a.sel_stride) k = a.sel_stride;  // never write past a selection row
-  topk_block<16>(out, P, k, (a.flags & 2u) != 0u, a.kv_indices + pbeg,
-                 a.sel + ((size_t)b * a.Hkv + h) * a.sel_stride, sh);
+  topk_staged(out, P, k, (a.flags & 2u) != 0u, a.kv_indices + pbeg,
+              a.sel + ((size_t)b * a.Hkv + h) * a.sel_stride, *tk);
   return true;
 }
 
-template <int GROUP>
+template <int GROUP, bool FUSED>
 __global__ __launch_bounds__(kThreads) void estimate_kernel(EstimateArgs a) {
-  __shared__ EstShared sm;
-  estimate_item<GROUP>(a, blockIdx.z, blockIdx.y, blockIdx.x, sm);
+  if constexpr (FUSED) {
+    __shared__ EstTopkShared sm;
+    estimate_item<GROUP>(a, blockIdx.z, blockIdx.y, blockIdx.x, sm.e, &sm.tk);
+  } else {
+    __shared__ EstShared sm;
+    a.sel = nullptr;
+    estimate_item<GROUP>(a, blockIdx.z, blockIdx.y, blockIdx.x, sm, nullptr);
+  }
 }
 
 __global__ __launch_bounds__(kThreads) void topk_kernel(TopkArgs a) {
@@ -419,8 +477,8 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopkArgs a) {
   if (k > a.sel_stride) k = a.sel_stride;
   const float* row = a.scores + ((size_t)b * a.Hkv + h) * a.score_stride;
   int32_t* out = a.sel + ((size_t)b * a.Hkv + h) * a.sel_stride;
-  if (P <= kFusedTopkMaxPages)
-    topk_block<16>(row, P, k, (a.flags & 2u) != 0u, a.kv_indices + pbeg, out, sh);
+  if (P <= kStageMaxPages)
+    topk_staged(row, P, k, (a.flags & 2u) != 0u, a.kv_indices + pbeg, out, sh);
   else
     topk_block<kTopkMaxPages / kThreads>(row, P, k, (a.flags & 2u) != 0u, a.kv_indices + pbeg,
                                           out, sh);
@@ -433,8 +491,6 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopkArgs a) {
 struct DecShared {
   float o[4][kHeadDim];
   float ml[4][2];
-  float m[kMergeMaxChunks], l[kMergeMaxChunks];
-  float s4[4];
   uint32_t last, ok;
 };
 
@@ -451,15 +507,30 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
                                             uint32_t* error) {
   float (*s_o)[kHeadDim] = sm.o;
   float (*s_ml)[2] = sm.ml;
-  float* s_m = sm.m;
-  float* s_l = sm.l;
-  float* s4 = sm.s4;
   const uint32_t lane = __lane_id();
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t row = lane / kLanesPerRow;
   const uint32_t l16 = lane % kLanesPerRow;
   const uint32_t hkv = hq / (a.Hq / a.Hkv);
   const uint32_t S = kPageSize;
+  const uint32_t d0 = l16 * kVec;
+  const size_t bh = (size_t)b * a.Hq + hq;
+  const uint32_t idx0 = chunk * kDecPagesPerBlock + wave * kDecPagesPerWave;
+  const uint32_t* sel_row =
+      a.sel ? reinterpret_cast<const uint32_t*>(a.sel) + ((size_t)b * a.Hkv + hkv) * a.sel_stride
+            : nullptr;
+  // selection entries and q need no page-table load: issue them first
+  uint32_t selv[kDecPagesPerWave];
+#pragma unroll
+  for (int s = 0; s < kDecPagesPerWave; ++s)
+    selv[s] = sel_row && ready == nullptr && idx0 + s < a.sel_stride ? ld_agent_u32(sel_row + idx0 + s)
+                                                                     : 0u;
+  float qf[kVec];
+  {
+    const H8 qq = ld16(a.q + bh * kHeadDim + d0);
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) qf[j] = (float)qq.v[j];
+  }
   const uint32_t pbeg = (uint32_t)a.kv_indptr[b];
   const uint32_t P = (uint32_t)a.kv_indptr[b + 1] - pbeg;
   const uint32_t lpl = (uint32_t)a.kv_last_page_len[b];
@@ -491,35 +562,20 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
     }
     __syncthreads();
     if (sm.ok == 0u) return;
+#pragma unroll
+    for (int s = 0; s < kDecPagesPerWave; ++s)
+      selv[s] = idx0 + s < npages ? ld_agent_u32(sel_row + idx0 + s) : 0u;
   }
-  const uint32_t last_phys = (uint32_t)a.kv_indices[pbeg + P - 1u];
-  const uint32_t d0 = l16 * kVec;
-  const size_t bh = (size_t)b * a.Hq + hq;
 
-  // ---- page ids of this wave's pages, then all their K/V loads
-  uint32_t phys[kDecPagesPerWave], ntok[kDecPagesPerWave];
+  // ---- K/V loads of this wave's pages, issued as soon as the page ids are known
+  uint32_t phys[kDecPagesPerWave];
 #pragma unroll
-  for (int s = 0; s < kDecPagesPerWave; ++s) {
-    const uint32_t idx = chunk * kDecPagesPerBlock + wave * kDecPagesPerWave + s;
-    ntok[s] = 0u;
-    phys[s] = 0u;
-    if (idx < npages) {
-      phys[s] = a.sel ? ld_agent_u32(reinterpret_cast<const uint32_t*>(a.sel) +
-                                     ((size_t)b * a.Hkv + hkv) * a.sel_stride + idx)
-                      : (uint32_t)a.kv_indices[pbeg + idx];
-      ntok[s] = phys[s] == last_phys ? lpl : S;
-    }
-  }
-  float qf[kVec];
-  {
-    const H8 qq = ld16(a.q + bh * kHeadDim + d0);
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) qf[j] = (float)qq.v[j];
-  }
+  for (int s = 0; s < kDecPagesPerWave; ++s)
+    phys[s] = idx0 + s < npages ? (a.sel ? selv[s] : (uint32_t)a.kv_indices[pbeg + idx0 + s]) : 0u;
   H8 kk[kDecPagesPerWave][4], vv[kDecPagesPerWave][4];
 #pragma unroll
   for (int s = 0; s < kDecPagesPerWave; ++s) {
-    if (ntok[s] != 0u) {
+    if (idx0 + s < npages) {
       const size_t kbase = elem_off(a.g, phys[s], 0, hkv, 0) + d0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -534,6 +590,12 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
         for (int j = 0; j < kVec; ++j) kk[s][i].v[j] = vv[s][i].v[j] = (f16)0.f;
     }
   }
+  // tokens per page: the sequence's last page holds lpl of them
+  const uint32_t last_phys = (uint32_t)a.kv_indices[pbeg + P - 1u];
+  uint32_t ntok[kDecPagesPerWave];
+#pragma unroll
+  for (int s = 0; s < kDecPagesPerWave; ++s)
+    ntok[s] = idx0 + s < npages ? (phys[s] == last_phys ? lpl : S) : 0u;
 
   // ---- logits: fp16(q.k), then fp16(. / sqrt(d))  (quest_attention.py:265-268)
   float x[kDecPagesPerWave][4];
@@ -601,39 +663,39 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   // ---- the last block of this (sequence, head) merges the chunks
   if (!arrive_last(&a.counters[bh], nch, &sm.last)) return;
   const float* base = a.partial + bh * a.max_chunks * kPartialStride;
-  // (m, l) of every chunk, loaded together
-  float mc = -INFINITY;
-  for (uint32_t c = threadIdx.x; c < nch; c += kThreads) {
-    const float mm = ld_agent(base + c * kPartialStride + kHeadDim);
-    const float ll = ld_agent(base + c * kPartialStride + kHeadDim + 1);
-    s_m[c] = mm;
-    s_l[c] = ll;
-    mc = fmaxf(mc, mm);
-  }
-  const float M = block_max(mc, s4);
-  float lpart = 0.f;
-  for (uint32_t c = threadIdx.x; c < nch; c += kThreads) {
-    const float w = __expf(s_m[c] - M);
-    s_m[c] = w;  // becomes the chunk weight
-    lpart = lpart + w * s_l[c];
-  }
-  const float Lsum = block_sum(lpart, s4);  // ends with a barrier: weights visible
-  // o[d] = sum_c w_c o_c[d]: thread t sums dim t%128 over the chunks of
-  // parity t/128, eight loads in flight at a time
+  // chunks in groups of 16: every load of a group is issued before any is
+  // used (one memory round trip per group); thread t sums dim t%128 over the
+  // chunks of parity t/128, with the group max folded in online
   const uint32_t d = threadIdx.x % kHeadDim, half = threadIdx.x / kHeadDim;
-  float acc = 0.f;
-  for (uint32_t c0 = half; c0 < nch; c0 += 16u) {
-    float v[8];
+  float M = -INFINITY, Lsum = 0.f, acc = 0.f;
+  for (uint32_t g0 = 0; g0 < nch; g0 += 16u) {
+    const uint32_t ng = nch - g0 < 16u ? nch - g0 : 16u;
+    const float* gb = base + (size_t)g0 * kPartialStride;
+    float mv[16], lv[16], ov[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t c = c0 + 2u * i;
-      v[i] = c < nch ? ld_agent(base + c * kPartialStride + d) : 0.f;
+    for (int c = 0; c < 16; ++c) {
+      mv[c] = (uint32_t)c < ng ? ld_agent(gb + c * kPartialStride + kHeadDim) : -INFINITY;
+      lv[c] = (uint32_t)c < ng ? ld_agent(gb + c * kPartialStride + kHeadDim + 1) : 0.f;
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const uint32_t c = c0 + 2u * i;
-      if (c < nch) acc = acc + s_m[c] * v[i];
+      const uint32_t c = half + 2u * i;
+      ov[i] = c < ng ? ld_agent(gb + c * kPartialStride + d) : 0.f;
     }
+    float Mn = M;
+#pragma unroll
+    for (int c = 0; c < 16; ++c) Mn = fmaxf(Mn, mv[c]);
+    const float keep = M == -INFINITY ? 0.f : __expf(M - Mn);
+    Lsum = Lsum * keep;
+    acc = acc * keep;
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      mv[c] = mv[c] == -INFINITY ? 0.f : __expf(mv[c] - Mn);  // chunk weight
+      Lsum = Lsum + mv[c] * lv[c];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc = acc + mv[half + 2 * i] * ov[i];
+    M = Mn;
   }
   if (half == 1u) s_o[0][d] = acc;
   __syncthreads();
@@ -660,7 +722,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
 template <int GROUP>
 __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
   __shared__ union {
-    EstShared e;
+    EstTopkShared e;
     DecShared d;
   } sm;
   __shared__ uint32_t s_ticket, s_fin;
@@ -671,7 +733,7 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
   if (t < la.n_est) {
     const uint32_t bh = t / la.est_chunks, chunk = t % la.est_chunks;
     const uint32_t b = bh / la.e.Hkv, h = bh % la.e.Hkv;
-    if (estimate_item<GROUP>(la.e, b, h, chunk, sm.e)) {
+    if (estimate_item<GROUP>(la.e, b, h, chunk, sm.e.e, &sm.e.tk)) {
       // the head's selection is written: publish it
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
@@ -713,11 +775,18 @@ __global__ void fill_u32_kernel(uint32_t* p, size_t n, uint32_t v) {
 hipError_t launch_estimate(const EstimateArgs& a, uint32_t batch, uint32_t max_pages,
                            hipStream_t s) {
   dim3 grid((max_pages + kEstPagesPerBlock - 1) / kEstPagesPerBlock, a.Hkv, batch);
+  const bool fused = a.sel != nullptr;
   switch (a.Hq / a.Hkv) {
-    case 1: hipLaunchKernelGGL(estimate_kernel<1>, grid, dim3(kThreads), 0, s, a); break;
-    case 2: hipLaunchKernelGGL(estimate_kernel<2>, grid, dim3(kThreads), 0, s, a); break;
-    case 4: hipLaunchKernelGGL(estimate_kernel<4>, grid, dim3(kThreads), 0, s, a); break;
-    case 8: hipLaunchKernelGGL(estimate_kernel<8>, grid, dim3(kThreads), 0, s, a); break;
+#define AOAKV_EST(G)                                                                   \
+  case G:                                                                              \
+    if (fused) hipLaunchKernelGGL((estimate_kernel<G, true>), grid, dim3(kThreads), 0, s, a); \
+    else hipLaunchKernelGGL((estimate_kernel<G, false>), grid, dim3(kThreads), 0, s, a);      \
+    break;
+    AOAKV_EST(1)
+    AOAKV_EST(2)
+    AOAKV_EST(4)
+    AOAKV_EST(8)
+#undef AOAKV_EST
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -234,6 +234,66 @@ def test_topk_ties_break_to_lower_index():
     assert L == P * S
 
 
+@pytest.mark.parametrize("P", [1000, 1500, 2048, 3000, 4096, 5000, 16384])
+def test_topk_row_lengths(P):
+    """Standalone top-k over rows that take each keys-per-thread variant
+    (4 / 8 / 16 staged in LDS, 64 read directly); rows: plain normal scores,
+    scores rounded to create ties at the boundary, one huge outlier (the
+    first radix digit then holds almost every key), and mixed-sign scores
+    spanning the full key range."""
+    from aoakv import ops
+    _say(f"[topk] P={P}")
+    k = max(3, P // 16)
+    g = np.random.default_rng(P)
+    s = g.standard_normal((1, 4, P)).astype(np.float32)
+    s[0, 1] = np.round(s[0, 1] * 4) / 4
+    s[0, 2, g.integers(P)] = 1e30
+    s[0, 3] = (s[0, 3] * 1e20).astype(np.float32)
+    scores = torch.from_numpy(s).to(DEV)
+    indptr = torch.tensor([0, P], dtype=torch.int32, device=DEV)
+    perm = g.permutation(P).astype(np.int32)             # physical page ids
+    idx = torch.from_numpy(perm).to(DEV)
+    lpl = torch.tensor([S], dtype=torch.int32, device=DEV)
+    sel = torch.full((1, 4, k), -1, dtype=torch.int32, device=DEV)
+    for fixed in (True, False):
+        ops.topk_filtering(scores, indptr, idx, lpl, k * S, sel, S,
+                           ops.FLAG_FIXED if fixed else 0)
+        got = sel.cpu().numpy()[0]
+        ref = perm[sim.topk_pages(s[0], k, fixed)]
+        assert np.array_equal(got, ref), (P, fixed, np.nonzero(got != ref))
+
+
+@pytest.mark.parametrize("L", [32768, 3000 * S])
+def test_fused_estimate_topk_long_rows(L):
+    """The fused scoring + top-k kernel at config-2 length (2048 pages: 8 keys
+    per thread) and at 3000 pages (16 keys per thread) against the oracle."""
+    from aoakv import ops
+    _say(f"[estimate_topk fused] L={L}")
+    H, budget = 4, 2048
+    q, K, V = _sim_state(11, H, L)
+    ctrl = make_ctrl(H, L + 16, HND, budget, shuffle=5)
+    prefill(ctrl, K[:, :, :-1], V[:, :, :-1])
+    decode_append(ctrl, K[:, :, -1:], V[:, :, -1:])
+    st = sim.SimLayerState(K[:, :, :-1], V[:, :, :-1])
+    st.append(K[:, :, -1:], V[:, :, -1:])
+    scores_ref, pages_ref = sim.select_pages(st, q, budget, True, True)
+    P = len(ctrl.kv_cache.indicies)
+    qd = torch.from_numpy(q[0, :, 0].copy()).to(DEV)[None]
+    c = ctrl
+    ops.estimate_topk(qd, c.metadata_cache.buf_layer(0), c.metadata_indptr_for_append,
+                      c.metadata_indices, c.kv_indptr_for_append, c.kv_indices_with_last,
+                      c.kv_last_page_len_t, c.v_log_norm_layer(0), c.scores, c._sel,
+                      c.token_budget, c.workspace, P, HND, c.flags)
+    torch.cuda.synchronize()
+    scores = c.scores[0, :, :P].cpu().numpy()
+    np.testing.assert_allclose(scores, scores_ref[0, :, 0], rtol=2e-6, atol=2e-5)
+    sel = c.topk_dindices_buffer[0].cpu().numpy()
+    inv = {p: i for i, p in enumerate(c.kv_cache.indicies)}
+    sel_logical = np.vectorize(inv.get)(sel)
+    _selection_ok(sel_logical, pages_ref, scores_ref, True)
+    assert np.array_equal(sel_logical, sim.topk_pages(scores, pages_ref.shape[-1], True))
+
+
 # ------------------------------------------------------------------ attention
 
 @pytest.mark.parametrize("layout", [NHD, HND])
