@@ -182,10 +182,11 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
     float sv[KPT];
     int32_t iv[KPT];
 #pragma unroll
-    for (int m = 0; m < KPT; ++m) {
-      const uint32_t i = tid + (uint32_t)m * kThreads;
-      sv[m] = i < P ? ld_agent(scores + i) : 0.f;
-      iv[m] = i < P ? kv_ids[i] : 0;
+    for (int m = 0; m < KPT; ++m) {  // unconditional loads of clamped indices
+      uint32_t i = tid + (uint32_t)m * kThreads;
+      i = i < P ? i : P - 1u;
+      sv[m] = ld_agent(scores + i);
+      iv[m] = kv_ids[i];
     }
 #pragma unroll
     for (int m = 0; m < KPT; ++m) {
@@ -205,7 +206,7 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
     for (int j = 0; j < KPT; ++j) {
       const uint32_t i = i0 + j;
       const bool valid = (uint32_t)j < kpt && i < P;
-      key[j] = order_key(valid ? ld_agent(scores + i) : 0.f);
+      key[j] = order_key(ld_agent(scores + (valid ? i : P - 1u)));
       if (valid && is_free(i)) {
         kmin = key[j] < kmin ? key[j] : kmin;
         kmax = key[j] > kmax ? key[j] : kmax;
@@ -359,17 +360,22 @@ __device__ __forceinline__ bool estimate_item(const EstimateArgs& a, uint32_t b,
   const uint32_t d0 = l16 * kVec;
   const bool value_aware = (a.flags & 1u) != 0u;
 
-  const uint32_t page0 = chunk * kEstPagesPerBlock + wave * kEstPagesPerWave;
-  const bool wave_live = page0 < P;
-  uint32_t mp0 = 0, mp1 = 0;
-  if (wave_live) {
-    mp0 = (uint32_t)a.meta_indices[mbeg + page0 / kPageSize];
-    mp1 = page0 + kPageSize < P ? (uint32_t)a.meta_indices[mbeg + page0 / kPageSize + 1] : mp0;
-  }
-  // lane j < 32 fetches the value statistic of page page0 + j
-  float lvn_lane = 0.f;
-  if (value_aware && lane < (uint32_t)kEstPagesPerWave && page0 + lane < P)
-    lvn_lane = (float)a.v_log_norm[(size_t)(uint32_t)a.kv_indices[pbeg + page0 + lane] * a.Hkv + h];
+  // Every load below is unconditional, with an address that always lies in
+  // the sequence's pages: a page past P reads a page of this block (its
+  // score is never stored).  A load under a lane-dependent condition would
+  // make the compiler wait for it before issuing the next one.  Issue order:
+  // the page id for the value statistic, the metadata page ids, q, the 16
+  // metadata vectors, then the value statistic (used only after scoring).
+  const uint32_t pblk = chunk * kEstPagesPerBlock;  // < P
+  const uint32_t page0 = pblk + wave * kEstPagesPerWave;
+  uint32_t pj = page0 + (lane % (uint32_t)kEstPagesPerWave);  // lane j: page page0 + j % 32
+  pj = pj < P ? pj : P - 1u;
+  const uint32_t phys_j = (uint32_t)a.kv_indices[pbeg + pj];
+  __builtin_amdgcn_sched_barrier(0);  // keep the issue order written here
+  const uint32_t pl0 = page0 < P ? page0 : pblk;  // a live page of the wave's first half
+  const uint32_t pl1 = pl0 + kPageSize < P ? pl0 + kPageSize : pl0;
+  const uint32_t mp0 = (uint32_t)a.meta_indices[mbeg + pl0 / kPageSize];
+  const uint32_t mp1 = (uint32_t)a.meta_indices[mbeg + pl1 / kPageSize];
 
   float qf[GROUP][kVec];
 #pragma unroll
@@ -383,17 +389,16 @@ __device__ __forceinline__ bool estimate_item(const EstimateArgs& a, uint32_t b,
   H8 kmx[kSteps], kmn[kSteps];
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
-    const uint32_t p = page0 + s * 4 + row;
-    if (p < P) {
-      const uint32_t mp = s < kSteps / 2 ? mp0 : mp1;
-      const size_t off = elem_off(a.g, mp, 0, h, (s * 4 + row) % kPageSize) + d0;
-      kmx[s] = ld16(a.meta + off);
-      kmn[s] = ld16(a.meta + off + a.g.kv);
-    } else {
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) kmx[s].v[j] = kmn[s].v[j] = (f16)0.f;
-    }
+    const uint32_t mp = s < kSteps / 2 ? mp0 : mp1;
+    const size_t off = elem_off(a.g, mp, 0, h, (s * 4 + row) % kPageSize) + d0;
+    kmx[s] = ld16(a.meta + off);
+    kmn[s] = ld16(a.meta + off + a.g.kv);
   }
+  __builtin_amdgcn_sched_barrier(0);
+  // without the value term v_log_norm may be null: read q instead (unused)
+  const f16 lvn_raw = *(value_aware ? a.v_log_norm + (size_t)phys_j * a.Hkv + h : a.q);
+
+  float sc[kSteps];  // score of page page0 + 4s + row (same in all lanes of the row)
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
     float x[GROUP];
@@ -408,10 +413,8 @@ __device__ __forceinline__ bool estimate_item(const EstimateArgs& a, uint32_t b,
       }
       x[g] = row_sum16(acc);
     }
-    const float lvn = __shfl(lvn_lane, s * 4 + (int)row);
-    float score;
     if (value_aware) {
-      // 2 * (bound / sqrt(d)), logsumexp over the group, + 2 * log-norm
+      // 2 * (bound / sqrt(d)), logsumexp over the group (+ 2 * log-norm below)
       float m = -INFINITY;
 #pragma unroll
       for (int g = 0; g < GROUP; ++g) {
@@ -425,12 +428,19 @@ __device__ __forceinline__ bool estimate_item(const EstimateArgs& a, uint32_t b,
         for (int g = 0; g < GROUP; ++g) se = se + expf(x[g] - m);
         lse = logf(se) + m;
       }
-      score = lse + 2.0f * lvn;
+      sc[s] = lse;
     } else {
-      score = x[0];
+      float t = x[0];
 #pragma unroll
-      for (int g = 1; g < GROUP; ++g) score = score + x[g];
+      for (int g = 1; g < GROUP; ++g) t = t + x[g];
+      sc[s] = t;
     }
+  }
+  const float lvn_lane = (float)lvn_raw;
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) {
+    float score = sc[s];
+    if (value_aware) score = score + 2.0f * __shfl(lvn_lane, s * 4 + (int)row);
     if (l16 == 0u) s_sc[wave * kEstPagesPerWave + s * 4 + row] = score;
   }
   __syncthreads();
@@ -519,25 +529,32 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   const uint32_t* sel_row =
       a.sel ? reinterpret_cast<const uint32_t*>(a.sel) + ((size_t)b * a.Hkv + hkv) * a.sel_stride
             : nullptr;
-  // selection entries and q need no page-table load: issue them first
-  uint32_t selv[kDecPagesPerWave];
-#pragma unroll
-  for (int s = 0; s < kDecPagesPerWave; ++s)
-    selv[s] = sel_row && ready == nullptr && idx0 + s < a.sel_stride ? ld_agent_u32(sel_row + idx0 + s)
-                                                                     : 0u;
-  float qf[kVec];
-  {
-    const H8 qq = ld16(a.q + bh * kHeadDim + d0);
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) qf[j] = (float)qq.v[j];
-  }
+  // Loads are unconditional with clamped addresses and masked afterwards (a
+  // load under a lane- or page-dependent condition makes the compiler wait
+  // for it before issuing the next).  The page-table words, the selection
+  // entries and q need no earlier load, so they are all issued first.
   const uint32_t pbeg = (uint32_t)a.kv_indptr[b];
   const uint32_t P = (uint32_t)a.kv_indptr[b + 1] - pbeg;
   const uint32_t lpl = (uint32_t)a.kv_last_page_len[b];
+  const int32_t tbv = *(a.token_budgets ? a.token_budgets + b : a.kv_indptr + b);
+  const uint32_t budget = a.token_budgets ? (uint32_t)tbv : a.token_budget;
+  const uint32_t ich = chunk * kDecPagesPerBlock;  // the chunk's first entry
+  // dense decode reads its page ids from kv_indices below; its "selection"
+  // loads read kv_indptr[0] (never used)
+  const uint32_t* sel_src = sel_row ? sel_row : reinterpret_cast<const uint32_t*>(a.kv_indptr);
+  const uint32_t sel_last = sel_row ? a.sel_stride - 1u : 0u;
+  uint32_t selv[kDecPagesPerWave], sel_ch = 0u;
+  if (ready == nullptr) {  // a compile-time constant in the two-launch path
+    sel_ch = ld_agent_u32(sel_src + (ich < sel_last ? ich : sel_last));
+#pragma unroll
+    for (int s = 0; s < kDecPagesPerWave; ++s)
+      selv[s] = ld_agent_u32(sel_src + (idx0 + s < sel_last ? idx0 + s : sel_last));
+  }
+  const H8 qq = ld16(a.q + bh * kHeadDim + d0);
+  __builtin_amdgcn_sched_barrier(0);  // keep the issue order written here
   if (P == 0u || lpl == 0u || lpl > S) return;  // malformed page table
   uint32_t npages = P;
   if (a.sel != nullptr) {
-    const uint32_t budget = a.token_budgets ? (uint32_t)a.token_budgets[b] : a.token_budget;
     npages = num_selected_pages((P - 1u) * S + lpl, budget, S, P);
     if (npages > a.sel_stride) npages = a.sel_stride;
   }
@@ -562,40 +579,49 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
     }
     __syncthreads();
     if (sm.ok == 0u) return;
+    sel_ch = ld_agent_u32(sel_row + ich);
 #pragma unroll
     for (int s = 0; s < kDecPagesPerWave; ++s)
-      selv[s] = idx0 + s < npages ? ld_agent_u32(sel_row + idx0 + s) : 0u;
+      selv[s] = ld_agent_u32(sel_row + (idx0 + s < sel_last ? idx0 + s : sel_last));
   }
 
-  // ---- K/V loads of this wave's pages, issued as soon as the page ids are known
+  // ---- K/V loads of this wave's pages; an entry past the selection reads
+  // the chunk's first selected page instead (masked below)
   uint32_t phys[kDecPagesPerWave];
+  bool live[kDecPagesPerWave];
 #pragma unroll
-  for (int s = 0; s < kDecPagesPerWave; ++s)
-    phys[s] = idx0 + s < npages ? (a.sel ? selv[s] : (uint32_t)a.kv_indices[pbeg + idx0 + s]) : 0u;
+  for (int s = 0; s < kDecPagesPerWave; ++s) {
+    live[s] = idx0 + s < npages;
+    if (a.sel != nullptr) {
+      phys[s] = live[s] ? selv[s] : sel_ch;
+    } else {
+      const uint32_t i = live[s] ? idx0 + s : ich;
+      phys[s] = (uint32_t)a.kv_indices[pbeg + i];
+    }
+  }
   H8 kk[kDecPagesPerWave][4], vv[kDecPagesPerWave][4];
 #pragma unroll
   for (int s = 0; s < kDecPagesPerWave; ++s) {
-    if (idx0 + s < npages) {
-      const size_t kbase = elem_off(a.g, phys[s], 0, hkv, 0) + d0;
+    const size_t kbase = elem_off(a.g, phys[s], 0, hkv, 0) + d0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t t = i * 4 + row;
-        kk[s][i] = ld16(a.kv + kbase + (size_t)t * a.g.tok);
-        vv[s][i] = ld16(a.kv + kbase + a.g.kv + (size_t)t * a.g.tok);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < kVec; ++j) kk[s][i].v[j] = vv[s][i].v[j] = (f16)0.f;
-    }
+    for (int i = 0; i < 4; ++i) kk[s][i] = ld16(a.kv + kbase + (size_t)(i * 4 + row) * a.g.tok);
   }
+#pragma unroll
+  for (int s = 0; s < kDecPagesPerWave; ++s) {
+    const size_t vbase = elem_off(a.g, phys[s], 1, hkv, 0) + d0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vv[s][i] = ld16(a.kv + vbase + (size_t)(i * 4 + row) * a.g.tok);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float qf[kVec];
+#pragma unroll
+  for (int j = 0; j < kVec; ++j) qf[j] = (float)qq.v[j];
   // tokens per page: the sequence's last page holds lpl of them
   const uint32_t last_phys = (uint32_t)a.kv_indices[pbeg + P - 1u];
   uint32_t ntok[kDecPagesPerWave];
 #pragma unroll
   for (int s = 0; s < kDecPagesPerWave; ++s)
-    ntok[s] = idx0 + s < npages ? (phys[s] == last_phys ? lpl : S) : 0u;
+    ntok[s] = live[s] ? (phys[s] == last_phys ? lpl : S) : 0u;
 
   // ---- logits: fp16(q.k), then fp16(. / sqrt(d))  (quest_attention.py:265-268)
   float x[kDecPagesPerWave][4];
@@ -672,16 +698,25 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
     const uint32_t ng = nch - g0 < 16u ? nch - g0 : 16u;
     const float* gb = base + (size_t)g0 * kPartialStride;
     float mv[16], lv[16], ov[8];
+    // unconditional loads of clamped chunk indices, masked after
 #pragma unroll
     for (int c = 0; c < 16; ++c) {
-      mv[c] = (uint32_t)c < ng ? ld_agent(gb + c * kPartialStride + kHeadDim) : -INFINITY;
-      lv[c] = (uint32_t)c < ng ? ld_agent(gb + c * kPartialStride + kHeadDim + 1) : 0.f;
+      const uint32_t cc = (uint32_t)c < ng ? (uint32_t)c : ng - 1u;
+      mv[c] = ld_agent(gb + cc * kPartialStride + kHeadDim);
+      lv[c] = ld_agent(gb + cc * kPartialStride + kHeadDim + 1);
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const uint32_t c = half + 2u * i;
-      ov[i] = c < ng ? ld_agent(gb + c * kPartialStride + d) : 0.f;
+      ov[i] = ld_agent(gb + (c < ng ? c : ng - 1u) * kPartialStride + d);
     }
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      mv[c] = (uint32_t)c < ng ? mv[c] : -INFINITY;
+      lv[c] = (uint32_t)c < ng ? lv[c] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ov[i] = half + 2u * i < ng ? ov[i] : 0.f;
     float Mn = M;
 #pragma unroll
     for (int c = 0; c < 16; ++c) Mn = fmaxf(Mn, mv[c]);
