@@ -62,36 +62,43 @@ int check_group(uint32_t hq, uint32_t hkv) {
 }
 
 struct Workspace {
-  uint32_t* ctl;  // [0] ticket counter, [1] finished blocks, [2] error flag
+  uint32_t* ctl;  // [2] error flag of the single-launch layer
   uint32_t* est_counters;
   uint32_t* dec_counters;
-  uint32_t* ready;
   float* partial;
+  uint32_t* hsel;
+  uint32_t* hpart;
   size_t bytes;
 };
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-// [ctl: 64 u32][est counters: B*Hkv][dec counters: B*Hq][ready: B*Hkv]
-// [partials: B*Hq*chunks*stride f32]; every region 256-byte aligned.  The
-// control words sit at offset 0 so a caller can read the error flag
-// (word 2) without knowing the shapes.
+// [ctl: 64 u32][est counters: B*Hkv lines][dec counters: B*Hq lines]
+// [partials: B*Hq*chunks*stride f32][hsel: B*Hq*max_sel u32]
+// [hpart: B*Hq*chunks*stride u32]; every region 256-byte aligned.  The
+// control words sit at offset 0 so a caller can read the error flag (word
+// 2) without knowing the shapes.  All of it starts zeroed
+// (aoakv_workspace_init) and every launch leaves it zeroed again, except
+// the two-launch partials, which are always written before they are read.
 size_t ws_layout(uint32_t B, uint32_t hq, uint32_t hkv, uint32_t max_sel_pages, void* base,
                  Workspace* w) {
-  const size_t off_est = 256;
-  const size_t off_dec = off_est + round_up((size_t)B * hkv * 4u, 256);
-  const size_t off_rdy = off_dec + round_up((size_t)B * hq * 4u, 256);
-  const size_t off_part = off_rdy + round_up((size_t)B * hkv * 4u, 256);
   const size_t part =
       (size_t)B * hq * aoakv::decode_chunks(max_sel_pages) * aoakv::partial_stride() * 4u;
-  const size_t total = off_part + round_up(part, 256);
+  const size_t off_est = 256;
+  const size_t cnt = (size_t)aoakv::counter_stride() * 4u;  // bytes per counter
+  const size_t off_dec = off_est + round_up((size_t)B * hkv * cnt, 256);
+  const size_t off_part = off_dec + round_up((size_t)B * hq * cnt, 256);
+  const size_t off_hsel = off_part + round_up(part, 256);
+  const size_t off_hpart = off_hsel + round_up((size_t)B * hq * max_sel_pages * 4u, 256);
+  const size_t total = off_hpart + round_up(part, 256);
   if (w) {
     char* c = static_cast<char*>(base);
     w->ctl = reinterpret_cast<uint32_t*>(c);
     w->est_counters = reinterpret_cast<uint32_t*>(c + off_est);
     w->dec_counters = reinterpret_cast<uint32_t*>(c + off_dec);
-    w->ready = reinterpret_cast<uint32_t*>(c + off_rdy);
     w->partial = reinterpret_cast<float*>(c + off_part);
+    w->hsel = reinterpret_cast<uint32_t*>(c + off_hsel);
+    w->hpart = reinterpret_cast<uint32_t*>(c + off_hpart);
     w->bytes = total;
   }
   return total;
@@ -413,13 +420,19 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
     la.e.token_budget = token_budget;
     la.e.token_budgets = token_budgets;
     la.e.counters = w.est_counters;
+    const uint32_t max_sel = sel_stride < max_pages ? sel_stride : max_pages;
+    la.e.hsel = w.hsel;
+    la.e.hsel_stride = max_sel;
     la.d = da;
+    la.d.hsel = w.hsel;
+    la.d.hsel_stride = max_sel;
+    la.d.hpart = w.hpart;
+    la.d.error = w.ctl + 2;
     la.est_chunks = aoakv::est_chunks(max_pages);
     la.n_est = batch_size * num_kv_heads * la.est_chunks;
+    la.n_workers = la.n_est < aoakv::layer_score_workers() ? la.n_est : aoakv::layer_score_workers();
+    la.n_heads = batch_size * num_kv_heads;
     la.n_dec = batch_size * num_qo_heads * da.max_chunks;
-    la.n_ready = batch_size * num_kv_heads;
-    la.ready = w.ready;
-    la.ctl = w.ctl;
     return hip_status(aoakv::launch_layer(la, s), "sparse_decode_layer");
   }
   if (int e = launch_estimate_topk(ea, w, sel_pages, sel_stride, token_budget, token_budgets,

@@ -156,7 +156,14 @@ __device__ __forceinline__ RadixResult radix_select(const uint32_t (&rel)[KPT], 
 template <int KPT>
 __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uint32_t P, uint32_t k,
                                            bool fixed, const int32_t* __restrict__ kv_ids,
-                                           int32_t* __restrict__ out, TopkShared& sh) {
+                                           int32_t* __restrict__ out, TopkShared& sh,
+                                           uint32_t* hout, uint32_t hstride, uint32_t hcopies) {
+  // page i of the output, also as id + 1 into the hcopies handoff rows
+  auto put = [&](uint32_t i, int32_t id) {
+    st_agent_i32(out + i, id);
+    if (hout != nullptr)
+      for (uint32_t c = 0; c < hcopies; ++c) st_agent_u32(hout + c * hstride + i, (uint32_t)id + 1u);
+  };
   constexpr bool kStaged = KPT <= 16;
   static_assert(KPT % 4 == 0 && (KPT <= 16 || KPT == 64), "keys per thread");
   using Mask = typename std::conditional<(KPT > 32), uint64_t, uint32_t>::type;
@@ -164,7 +171,7 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
   const uint32_t lane = __lane_id();
   const uint32_t wave = tid / kWave;
   if (k >= P) {  // everything selected
-    for (uint32_t i = tid; i < P; i += kThreads) st_agent_i32(out + i, kv_ids[i]);
+    for (uint32_t i = tid; i < P; i += kThreads) put(i, kv_ids[i]);
     return;
   }
   // kpt rounded up to 4 so staged keys are read as 16-byte LDS vectors
@@ -289,13 +296,13 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
       if (take) s_out[pos++] = (uint32_t)sh.id[i0 + j];
     }
     __syncthreads();
-    for (uint32_t i = tid; i < k; i += kThreads) st_agent_i32(out + i, (int32_t)s_out[i]);
+    for (uint32_t i = tid; i < k; i += kThreads) put(i, (int32_t)s_out[i]);
   } else {
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
       bool take = (above_m >> j) & 1u;
       if ((eq_m >> j) & 1u) take = rr.take_bucket || eq_rank++ < rr.kr;
-      if (take) st_agent_i32(out + pos++, kv_ids[i0 + j]);
+      if (take) put(pos++, kv_ids[i0 + j]);
     }
   }
 }
@@ -303,13 +310,15 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
 // top-k of a row of P <= kStageMaxPages pages with the fewest keys per thread
 __device__ __forceinline__ void topk_staged(const float* __restrict__ scores, uint32_t P, uint32_t k,
                                             bool fixed, const int32_t* __restrict__ kv_ids,
-                                            int32_t* __restrict__ out, TopkShared& sh) {
+                                            int32_t* __restrict__ out, TopkShared& sh,
+                                            uint32_t* hout = nullptr, uint32_t hstride = 0u,
+                                            uint32_t hcopies = 0u) {
   if (P <= 4u * kThreads)
-    topk_block<4>(scores, P, k, fixed, kv_ids, out, sh);
+    topk_block<4>(scores, P, k, fixed, kv_ids, out, sh, hout, hstride, hcopies);
   else if (P <= 8u * kThreads)
-    topk_block<8>(scores, P, k, fixed, kv_ids, out, sh);
+    topk_block<8>(scores, P, k, fixed, kv_ids, out, sh, hout, hstride, hcopies);
   else
-    topk_block<16>(scores, P, k, fixed, kv_ids, out, sh);
+    topk_block<16>(scores, P, k, fixed, kv_ids, out, sh, hout, hstride, hcopies);
 }
 
 // Pages per head the fused estimate + top-k kernel selects from (16 keys per
@@ -333,29 +342,32 @@ struct EstTopkShared {
   TopkShared tk;
 };
 
-// Scores pages [128*chunk, 128*chunk + 128) of (sequence b, kv head h); with
-// a.sel set, the last block of the head also selects its pages.  Returns
-// true in the block that wrote the head's selection.
+// Pages of sequence b the scoring covers: never past a score row or the
+// max_pages the grid covers, and within the fused top-k's limit when fused.
+__device__ inline uint32_t est_pages(const EstimateArgs& a, uint32_t b, uint32_t* pbeg_out) {
+  const uint32_t pbeg = (uint32_t)a.kv_indptr[b];
+  uint32_t P = (uint32_t)a.kv_indptr[b + 1] - pbeg;
+  if (P > a.score_stride) P = a.score_stride;
+  if (P > a.max_pages) P = a.max_pages;
+  if (P > kFusedTopkMaxPages && a.sel != nullptr) P = kFusedTopkMaxPages;
+  *pbeg_out = pbeg;
+  return P;
+}
+
+// Scores pages [128*chunk, 128*chunk + 128) of (sequence b, kv head h) and
+// stores them (agent-coherent).  Returns false, uniformly, when the chunk
+// holds no page.
 template <int GROUP>
-__device__ __forceinline__ bool estimate_item(const EstimateArgs& a, uint32_t b, uint32_t h,
-                                              uint32_t chunk, EstShared& sm, TopkShared* tk) {
+__device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, uint32_t h,
+                                           uint32_t chunk, EstShared& sm) {
   float* s_sc = sm.sc;
   const uint32_t lane = __lane_id();
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t row = lane / kLanesPerRow;
   const uint32_t l16 = lane % kLanesPerRow;
-  const uint32_t pbeg = (uint32_t)a.kv_indptr[b];
-  uint32_t P = (uint32_t)a.kv_indptr[b + 1] - pbeg;
-  if (P > a.score_stride) P = a.score_stride;  // never write past a score row
-  if (P > a.max_pages) P = a.max_pages;        // the grid covers max_pages per head
-  if (P > kFusedTopkMaxPages && a.sel != nullptr) P = kFusedTopkMaxPages;
+  uint32_t pbeg;
+  const uint32_t P = est_pages(a, b, &pbeg);
   if (chunk * kEstPagesPerBlock >= P) return false;  // uniform per block
-  // the selection size of the fused top-k, loaded up front (off the handoff path)
-  uint32_t lpl = 0u, budget = 0u;
-  if (a.sel != nullptr) {
-    lpl = (uint32_t)a.kv_last_page_len[b];
-    budget = a.token_budgets ? (uint32_t)a.token_budgets[b] : a.token_budget;
-  }
   const uint32_t mbeg = (uint32_t)a.meta_indptr[b];
   const uint32_t d0 = l16 * kVec;
   const bool value_aware = (a.flags & 1u) != 0u;
@@ -450,15 +462,44 @@ __device__ __forceinline__ bool estimate_item(const EstimateArgs& a, uint32_t b,
     if (threadIdx.x < (uint32_t)kEstPagesPerBlock && p < P) st_agent(out + p, s_sc[threadIdx.x]);
   }
 
-  if (a.sel == nullptr) return false;
-  // ---- fused top-k: the last block of this (sequence, head) selects
-  const uint32_t nch = (P + kEstPagesPerBlock - 1) / kEstPagesPerBlock;
-  if (!arrive_last(&a.counters[b * a.Hkv + h], nch, &sm.last)) return false;
+  return true;
+}
+
+// Top-k of (sequence b, kv head h) from its stored scores, every chunk
+// written; lpl and budget of the sequence are passed in (loaded early).
+template <int GROUP>
+__device__ __forceinline__ void select_item(const EstimateArgs& a, uint32_t b, uint32_t h,
+                                            uint32_t lpl, uint32_t budget, TopkShared& tk) {
+  uint32_t pbeg;
+  const uint32_t P = est_pages(a, b, &pbeg);
   uint32_t k = num_selected_pages((P - 1u) * kPageSize + lpl, budget, kPageSize, P);
   if (k > a.sel_stride) k = a.sel_stride;  // never write past a selection row
-  topk_staged(out, P, k, (a.flags & 2u) != 0u, a.kv_indices + pbeg,
-              a.sel + ((size_t)b * a.Hkv + h) * a.sel_stride, *tk);
-  return true;
+  // no handoff entries for a sequence the decode items skip (malformed
+  // last-page length): nothing would read and clear them
+  const bool handoff = a.hsel != nullptr && lpl >= 1u && lpl <= (uint32_t)kPageSize;
+  uint32_t* hout = handoff ? a.hsel + ((size_t)b * a.Hq + h * GROUP) * a.hsel_stride : nullptr;
+  topk_staged(a.scores + ((size_t)b * a.Hkv + h) * a.score_stride, P, k, (a.flags & 2u) != 0u,
+              a.kv_indices + pbeg, a.sel + ((size_t)b * a.Hkv + h) * a.sel_stride, tk, hout,
+              a.hsel_stride, GROUP);
+}
+
+// Scores one chunk; with a.sel set, the last block of the head to finish
+// also selects its pages (arrival counter per head).
+template <int GROUP>
+__device__ __forceinline__ void estimate_item(const EstimateArgs& a, uint32_t b, uint32_t h,
+                                              uint32_t chunk, EstShared& sm, TopkShared* tk) {
+  // the selection size of the fused top-k, loaded up front (off the handoff path)
+  uint32_t lpl = 0u, budget = 0u;
+  if (a.sel != nullptr) {
+    lpl = (uint32_t)a.kv_last_page_len[b];
+    budget = a.token_budgets ? (uint32_t)a.token_budgets[b] : a.token_budget;
+  }
+  if (!score_item<GROUP>(a, b, h, chunk, sm)) return;
+  if (a.sel == nullptr) return;
+  uint32_t pbeg;
+  const uint32_t nch = (est_pages(a, b, &pbeg) + kEstPagesPerBlock - 1) / kEstPagesPerBlock;
+  if (!arrive_last(&a.counters[(b * a.Hkv + h) * kCounterStride], nch, &sm.last)) return;
+  select_item<GROUP>(a, b, h, lpl, budget, *tk);
 }
 
 template <int GROUP, bool FUSED>
@@ -491,7 +532,7 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopkArgs a) {
     topk_staged(row, P, k, (a.flags & 2u) != 0u, a.kv_indices + pbeg, out, sh);
   else
     topk_block<kTopkMaxPages / kThreads>(row, P, k, (a.flags & 2u) != 0u, a.kv_indices + pbeg,
-                                          out, sh);
+                                          out, sh, nullptr, 0u, 0u);
 }
 
 // ======================================================================
@@ -501,20 +542,48 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopkArgs a) {
 struct DecShared {
   float o[4][kHeadDim];
   float ml[4][2];
-  uint32_t last, ok;
+  uint32_t sel[kDecPagesPerBlock];
+  uint32_t last;
 };
 
-// Bound on polls of a ready flag before a decode item gives up (it then
-// flags an error and skips its pages, so every wave still exits).
+// Bound on polls of a handoff word before a wait gives up (it then sets the
+// error flag and goes on with stand-in data, so every wave still exits).
 constexpr uint32_t kSpinLimit = 1u << 18;
 
+// Polls an agent-coherent handoff word until it is written (non-zero);
+// returns the value - 1, or 0 after kSpinLimit polls with *error set.
+__device__ inline uint32_t wait_word(const uint32_t* p, uint32_t* error) {
+  uint32_t v, it = 0u;
+  while ((v = ld_agent_u32(p)) == 0u) {
+    __builtin_amdgcn_s_sleep(1);
+    if (++it > kSpinLimit) {
+      atomicOr(error, 1u);
+      return 0u;
+    }
+  }
+  return v - 1u;
+}
+
+// A float as a handoff word: bits + 1, never 0 (the all-ones NaN pattern,
+// which arithmetic never produces, is stored as the canonical NaN).
+__device__ inline uint32_t to_word(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  return (u == 0xFFFFFFFFu ? 0x7FC00000u : u) + 1u;
+}
+
 // Attends pages [8*chunk, 8*chunk + 8) of the selection of (sequence b,
-// query head hq) and, in the last block of the head, merges the chunks.
-// With `ready` set, waits first for the head's selection to be published
-// in this launch (ready[b * Hkv + hkv] != 0).
+// query head hq) and merges the head's chunks.
+//   HANDOFF = false (two launches): the selection comes from the previous
+//     launch; chunks hand their partial (o, m, l) to the last block to
+//     arrive at a per-head counter.
+//   HANDOFF = true (one launch): the selection is read from the handoff rows
+//     the head's top-k writes in this launch, each entry polled until
+//     written; partials go to handoff words and the head's last chunk
+//     polls them and merges.  Every block only waits on blocks with smaller
+//     indices, which were dispatched before it.
+template <bool HANDOFF>
 __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uint32_t hq,
-                                            uint32_t chunk, DecShared& sm, const uint32_t* ready,
-                                            uint32_t* error) {
+                                            uint32_t chunk, DecShared& sm) {
   float (*s_o)[kHeadDim] = sm.o;
   float (*s_ml)[2] = sm.ml;
   const uint32_t lane = __lane_id();
@@ -539,12 +608,12 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   const int32_t tbv = *(a.token_budgets ? a.token_budgets + b : a.kv_indptr + b);
   const uint32_t budget = a.token_budgets ? (uint32_t)tbv : a.token_budget;
   const uint32_t ich = chunk * kDecPagesPerBlock;  // the chunk's first entry
-  // dense decode reads its page ids from kv_indices below; its "selection"
-  // loads read kv_indptr[0] (never used)
-  const uint32_t* sel_src = sel_row ? sel_row : reinterpret_cast<const uint32_t*>(a.kv_indptr);
-  const uint32_t sel_last = sel_row ? a.sel_stride - 1u : 0u;
   uint32_t selv[kDecPagesPerWave], sel_ch = 0u;
-  if (ready == nullptr) {  // a compile-time constant in the two-launch path
+  if (!HANDOFF) {
+    // dense decode reads its page ids from kv_indices below; its
+    // "selection" loads read kv_indptr[0] (never used)
+    const uint32_t* sel_src = sel_row ? sel_row : reinterpret_cast<const uint32_t*>(a.kv_indptr);
+    const uint32_t sel_last = sel_row ? a.sel_stride - 1u : 0u;
     sel_ch = ld_agent_u32(sel_src + (ich < sel_last ? ich : sel_last));
 #pragma unroll
     for (int s = 0; s < kDecPagesPerWave; ++s)
@@ -564,25 +633,18 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   if (npages > cap * kDecPagesPerBlock) npages = cap * kDecPagesPerBlock;
   const uint32_t nch = (npages + kDecPagesPerBlock - 1) / kDecPagesPerBlock;
   if (chunk >= nch) return;  // uniform per block
-  if (ready != nullptr && a.sel != nullptr) {
-    if (threadIdx.x == 0) {
-      uint32_t ok = 1u, it = 0u;
-      while (ld_agent_u32(ready + b * a.Hkv + hkv) == 0u) {
-        __builtin_amdgcn_s_sleep(2);
-        if (++it > kSpinLimit) {
-          atomicOr(error, 1u);
-          ok = 0u;
-          break;
-        }
-      }
-      sm.ok = ok;
-    }
+  if (HANDOFF) {
+    // this chunk's entries of the head's selection, each polled until the
+    // top-k of this launch has written it, then cleared for the next launch
+    uint32_t* hrow = a.hsel + bh * a.hsel_stride;
+    const uint32_t e = ich + threadIdx.x;
+    if (threadIdx.x < (uint32_t)kDecPagesPerBlock)
+      sm.sel[threadIdx.x] = e < npages ? wait_word(hrow + e, a.error) : 0u;
     __syncthreads();
-    if (sm.ok == 0u) return;
-    sel_ch = ld_agent_u32(sel_row + ich);
+    if (threadIdx.x < (uint32_t)kDecPagesPerBlock && e < npages) st_agent_u32(hrow + e, 0u);
+    sel_ch = sm.sel[0];
 #pragma unroll
-    for (int s = 0; s < kDecPagesPerWave; ++s)
-      selv[s] = ld_agent_u32(sel_row + (idx0 + s < sel_last ? idx0 + s : sel_last));
+    for (int s = 0; s < kDecPagesPerWave; ++s) selv[s] = sm.sel[wave * kDecPagesPerWave + s];
   }
 
   // ---- K/V loads of this wave's pages; an entry past the selection reads
@@ -671,7 +733,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
     }
   }
   __syncthreads();
-  float* part = a.partial + (bh * a.max_chunks + chunk) * kPartialStride;
+  const size_t part_off = (bh * a.max_chunks + chunk) * kPartialStride;
   if (threadIdx.x < (uint32_t)kHeadDim + 2u) {
     const uint32_t d = threadIdx.x;
     const float M = fmaxf(fmaxf(s_ml[0][0], s_ml[1][0]), fmaxf(s_ml[2][0], s_ml[3][0]));
@@ -683,40 +745,86 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
       acc = acc + sc * val;
     }
     // slots 0..127: o; slot 128: m; slot 129: l
-    st_agent(part + d, d == (uint32_t)kHeadDim ? M : acc);
+    const float val = d == (uint32_t)kHeadDim ? M : acc;
+    if (HANDOFF) st_agent_u32(a.hpart + part_off + d, to_word(val));
+    else st_agent(a.partial + part_off + d, val);
   }
 
-  // ---- the last block of this (sequence, head) merges the chunks
-  if (!arrive_last(&a.counters[bh], nch, &sm.last)) return;
-  const float* base = a.partial + bh * a.max_chunks * kPartialStride;
+  // ---- one block of this (sequence, head) merges the chunks
+  if (HANDOFF) {
+    if (chunk != nch - 1u) return;  // the head's last chunk
+  } else {
+    if (!arrive_last(&a.counters[bh * kCounterStride], nch, &sm.last)) return;
+  }
+  const size_t base = bh * a.max_chunks * kPartialStride;
   // chunks in groups of 16: every load of a group is issued before any is
-  // used (one memory round trip per group); thread t sums dim t%128 over the
-  // chunks of parity t/128, with the group max folded in online
+  // used (one memory round trip per group; handoff words are re-polled until
+  // written); thread t sums dim t%128 over the chunks of parity t/128, with
+  // the group max folded in online
   const uint32_t d = threadIdx.x % kHeadDim, half = threadIdx.x / kHeadDim;
   float M = -INFINITY, Lsum = 0.f, acc = 0.f;
   for (uint32_t g0 = 0; g0 < nch; g0 += 16u) {
     const uint32_t ng = nch - g0 < 16u ? nch - g0 : 16u;
-    const float* gb = base + (size_t)g0 * kPartialStride;
-    float mv[16], lv[16], ov[8];
+    const size_t gb = base + (size_t)g0 * kPartialStride;
     // unconditional loads of clamped chunk indices, masked after
+    uint32_t mw[16], lw[16], ow[8];
+    auto load_group = [&]() {
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        const uint32_t cc = (uint32_t)c < ng ? (uint32_t)c : ng - 1u;
+        const size_t at = gb + cc * kPartialStride + kHeadDim;
+        if (HANDOFF) {
+          mw[c] = ld_agent_u32(a.hpart + at);
+          lw[c] = ld_agent_u32(a.hpart + at + 1);
+        } else {
+          mw[c] = __builtin_bit_cast(uint32_t, ld_agent(a.partial + at));
+          lw[c] = __builtin_bit_cast(uint32_t, ld_agent(a.partial + at + 1));
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t c = half + 2u * i;
+        const size_t at = gb + (c < ng ? c : ng - 1u) * kPartialStride + d;
+        ow[i] = HANDOFF ? ld_agent_u32(a.hpart + at)
+                        : __builtin_bit_cast(uint32_t, ld_agent(a.partial + at));
+      }
+    };
+    load_group();
+    if (HANDOFF) {
+      // re-poll until every word of the group is written, then decode
+      auto missing = [&]() {
+        bool z = false;
+#pragma unroll
+        for (int c = 0; c < 16; ++c) z |= (uint32_t)c < ng && (mw[c] == 0u || lw[c] == 0u);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) z |= half + 2u * i < ng && ow[i] == 0u;
+        return z;
+      };
+      uint32_t it = 0u;
+      while (missing()) {
+        if (++it > kSpinLimit) {
+          atomicOr(a.error, 1u);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        load_group();
+      }
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        mw[c] -= 1u;
+        lw[c] -= 1u;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ow[i] -= 1u;
+    }
+    float mv[16], lv[16], ov[8];
 #pragma unroll
     for (int c = 0; c < 16; ++c) {
-      const uint32_t cc = (uint32_t)c < ng ? (uint32_t)c : ng - 1u;
-      mv[c] = ld_agent(gb + cc * kPartialStride + kHeadDim);
-      lv[c] = ld_agent(gb + cc * kPartialStride + kHeadDim + 1);
+      mv[c] = (uint32_t)c < ng ? __builtin_bit_cast(float, mw[c]) : -INFINITY;
+      lv[c] = (uint32_t)c < ng ? __builtin_bit_cast(float, lw[c]) : 0.f;
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t c = half + 2u * i;
-      ov[i] = ld_agent(gb + (c < ng ? c : ng - 1u) * kPartialStride + d);
-    }
-#pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      mv[c] = (uint32_t)c < ng ? mv[c] : -INFINITY;
-      lv[c] = (uint32_t)c < ng ? lv[c] : 0.f;
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) ov[i] = half + 2u * i < ng ? ov[i] : 0.f;
+    for (int i = 0; i < 8; ++i) ov[i] = half + 2u * i < ng ? __builtin_bit_cast(float, ow[i]) : 0.f;
     float Mn = M;
 #pragma unroll
     for (int c = 0; c < 16; ++c) Mn = fmaxf(Mn, mv[c]);
@@ -735,68 +843,104 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   if (half == 1u) s_o[0][d] = acc;
   __syncthreads();
   if (half == 0u) a.o[bh * kHeadDim + d] = r16((acc + s_o[0][d]) / Lsum);
+  if (HANDOFF) {
+    // every thread has read its words (barrier above): clear them for the
+    // next launch -- o words by their reader, m / l words by thread c
+    for (uint32_t g0 = 0; g0 < nch; g0 += 16u) {
+      const size_t gb = base + (size_t)g0 * kPartialStride;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t c = g0 + half + 2u * i;
+        if (c < nch) st_agent_u32(a.hpart + gb + (half + 2u * i) * kPartialStride + d, 0u);
+      }
+      const uint32_t c = g0 + threadIdx.x;
+      if (threadIdx.x < 16u && c < nch) {
+        st_agent_u32(a.hpart + gb + threadIdx.x * kPartialStride + kHeadDim, 0u);
+        st_agent_u32(a.hpart + gb + threadIdx.x * kPartialStride + kHeadDim + 1, 0u);
+      }
+    }
+  }
 }
 
 __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
   __shared__ DecShared sm;
-  decode_item(a, blockIdx.z, blockIdx.y, blockIdx.x, sm, nullptr, nullptr);
+  decode_item<false>(a, blockIdx.z, blockIdx.y, blockIdx.x, sm);
 }
 
 // ======================================================================
 // one launch per decode layer
 // ======================================================================
 //
-// Workgroups take tickets from an atomic counter in the order they start.
-// Tickets [0, n_est) are scoring items ordered head by head (the last item
-// of a head also runs its top-k and publishes a ready flag); tickets
-// [n_est, n_est + n_dec) are decode items, also head by head, which wait for
-// their head's flag.  A decode item only ever waits on items with smaller
-// tickets, i.e. on workgroups that have already started, and those never
-// wait, so the wait always ends (and is bounded by kSpinLimit regardless).
-// The last workgroup to finish resets the ticket counter and the flags.
+// Workgroups, in index order:
+//   [0, n_workers)            scoring workers: item i = n_workers*r + w in
+//                             rounds r, items head by head, so the heads
+//                             finish one after another and the later steps
+//                             of early heads overlap the scoring of later
+//                             ones; each scored item bumps its head's count
+//   [.., + n_heads)           one top-k per (sequence, kv head): waits for
+//                             the head's count, selects, writes the handoff
+//                             selection
+//   [.., + n_dec)             decode items, head by head: poll their
+//                             selection entries; the head's last chunk
+//                             polls the other chunks' partials and merges
+// Workgroups are dispatched in index order, so every wait is on workgroups
+// that have already started and that never wait on later ones; each wait is
+// bounded by kSpinLimit regardless (then the error flag is set).  Counters
+// and handoff words are cleared by their readers, so the workspace is zero
+// again for the next launch.  No counter is shared by all workgroups
+// (same-address device atomics serialize at ~12 ns each).
 template <int GROUP>
 __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
   __shared__ union {
     EstTopkShared e;
     DecShared d;
   } sm;
-  __shared__ uint32_t s_ticket, s_fin;
-  if (threadIdx.x == 0)
-    s_ticket = __hip_atomic_fetch_add(la.ctl + 0, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  const uint32_t t = s_ticket;
-  if (t < la.n_est) {
-    const uint32_t bh = t / la.est_chunks, chunk = t % la.est_chunks;
-    const uint32_t b = bh / la.e.Hkv, h = bh % la.e.Hkv;
-    if (estimate_item<GROUP>(la.e, b, h, chunk, sm.e.e, &sm.e.tk)) {
-      // the head's selection is written: publish it
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
-      if (threadIdx.x == 0)
-        __hip_atomic_store(la.ready + b * la.e.Hkv + h, 1u, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+  __shared__ uint32_t s_ok;
+  const uint32_t t = blockIdx.x;
+  if (t < la.n_workers) {
+    for (uint32_t i = t; i < la.n_est; i += la.n_workers) {
+      const uint32_t bh = i / la.est_chunks, chunk = i % la.est_chunks;
+      const uint32_t b = bh / la.e.Hkv, h = bh % la.e.Hkv;
+      if (score_item<GROUP>(la.e, b, h, chunk, sm.e.e)) {
+        // the scores are stored once the memory counter drains; the barrier
+        // also ends this item's use of LDS before the next item's
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (threadIdx.x == 0)
+          __hip_atomic_fetch_add(la.e.counters + bh * kCounterStride, 1u, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
-  } else if (t < la.n_est + la.n_dec) {
-    const uint32_t u = t - la.n_est;
+  } else if (t < la.n_workers + la.n_heads) {
+    const uint32_t bh = t - la.n_workers;
+    const uint32_t b = bh / la.e.Hkv, h = bh % la.e.Hkv;
+    const uint32_t lpl = (uint32_t)la.e.kv_last_page_len[b];
+    const uint32_t budget =
+        la.e.token_budgets ? (uint32_t)la.e.token_budgets[b] : la.e.token_budget;
+    uint32_t pbeg;
+    const uint32_t P = est_pages(la.e, b, &pbeg);
+    if (P == 0u) return;
+    const uint32_t nch = (P + kEstPagesPerBlock - 1) / kEstPagesPerBlock;
+    if (threadIdx.x == 0) {
+      uint32_t it = 0u, ok = 1u;
+      while (ld_agent_u32(la.e.counters + bh * kCounterStride) < nch) {
+        __builtin_amdgcn_s_sleep(1);
+        if (++it > kSpinLimit) {
+          atomicOr(la.d.error, 1u);
+          ok = 0u;
+          break;
+        }
+      }
+      st_agent_u32(la.e.counters + bh * kCounterStride, 0u);  // every item of the head counted
+      s_ok = ok;
+    }
+    __syncthreads();
+    if (s_ok != 0u) select_item<GROUP>(la.e, b, h, lpl, budget, sm.e.tk);
+  } else if (t < la.n_workers + la.n_heads + la.n_dec) {
+    const uint32_t u = t - la.n_workers - la.n_heads;
     const uint32_t bh = u / la.d.max_chunks, chunk = u % la.d.max_chunks;
     const uint32_t b = bh / la.d.Hq, hq = bh % la.d.Hq;
-    decode_item(la.d, b, hq, chunk, sm.d, la.ready, la.ctl + 2);
-  }
-  // ---- the last workgroup to finish resets the launch state
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t prev =
-        __hip_atomic_fetch_add(la.ctl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_fin = prev == gridDim.x - 1u ? 1u : 0u;
-  }
-  __syncthreads();
-  if (s_fin != 0u) {
-    for (uint32_t i = threadIdx.x; i < la.n_ready; i += kThreads)
-      __hip_atomic_store(la.ready + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (threadIdx.x == 0) {
-      __hip_atomic_store(la.ctl + 0, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(la.ctl + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    decode_item<true>(la.d, b, hq, chunk, sm.d);
   }
 }
 
@@ -828,7 +972,7 @@ hipError_t launch_estimate(const EstimateArgs& a, uint32_t batch, uint32_t max_p
 }
 
 hipError_t launch_layer(const LayerArgs& la, hipStream_t s) {
-  const uint32_t grid = la.n_est + la.n_dec;
+  const uint32_t grid = la.n_workers + la.n_heads + la.n_dec;
   switch (la.e.Hq / la.e.Hkv) {
     case 1: hipLaunchKernelGGL(layer_kernel<1>, dim3(grid), dim3(kThreads), 0, s, la); break;
     case 2: hipLaunchKernelGGL(layer_kernel<2>, dim3(grid), dim3(kThreads), 0, s, la); break;
@@ -867,5 +1011,9 @@ uint32_t partial_stride() { return kPartialStride; }
 uint32_t decode_max_chunks() { return kMergeMaxChunks; }
 uint32_t topk_max_pages() { return kTopkMaxPages; }
 uint32_t fused_topk_max_pages() { return kFusedTopkMaxPages; }
+// One scoring worker per CU of the MI355X: the heads' chunks are scored in
+// rounds of 256, head by head.
+uint32_t layer_score_workers() { return 256u; }
+uint32_t counter_stride() { return kCounterStride; }
 
 }  // namespace aoakv

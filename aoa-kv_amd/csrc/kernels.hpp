@@ -6,6 +6,10 @@
 
 namespace aoakv {
 
+// Per-head arrival counters sit one 128-byte line apart: counters sharing a
+// line slow each other's atomics and polls.
+constexpr uint32_t kCounterStride = 32;
+
 struct AppendPrefillArgs {
   const f16* k;            // [N, H, D]
   const f16* v;            // [N, H, D]
@@ -55,6 +59,10 @@ struct EstimateArgs {
   uint32_t token_budget;
   const int32_t* token_budgets;
   uint32_t* counters;  // [B * Hkv]
+  // single launch only: the selection again, per query head, as page + 1
+  // (0 = not yet written), for the decode items of the same launch
+  uint32_t* hsel;      // [B, Hq, hsel_stride] or nullptr
+  uint32_t hsel_stride;
 };
 
 struct TopkArgs {
@@ -85,6 +93,12 @@ struct DecodeArgs {
   uint32_t* counters;  // [B*Hq]
   uint32_t Hq, Hkv, S, max_chunks;
   PageGeom g;
+  // single launch only: handoff buffers whose words hold value + 1 (0 = not
+  // yet written); every word is cleared again by its reader
+  uint32_t* hsel;      // [B, Hq, hsel_stride] selection of this launch
+  uint32_t hsel_stride;
+  uint32_t* hpart;     // [B*Hq, max_chunks, kPartialStride] split-K partials
+  uint32_t* error;     // set when a wait gave up
 };
 
 struct PrefillArgs {
@@ -99,14 +113,13 @@ struct PrefillArgs {
 
 // One decode layer in one launch (see layer_kernel in decode.hip).
 struct LayerArgs {
-  EstimateArgs e;      // with sel / counters of the fused top-k
-  DecodeArgs d;
+  EstimateArgs e;      // with sel / counters / hsel of the top-k
+  DecodeArgs d;        // with hsel / hpart / error
   uint32_t n_est;      // scoring items: B * Hkv * est_chunks
-  uint32_t est_chunks; // 128-page chunks per (sequence, head) item row
+  uint32_t est_chunks; // 128-page chunks per (sequence, head)
+  uint32_t n_workers;  // scoring workgroups (<= n_est), items taken round-robin
+  uint32_t n_heads;    // top-k workgroups: B * Hkv
   uint32_t n_dec;      // decode items: B * Hq * d.max_chunks
-  uint32_t n_ready;    // B * Hkv
-  uint32_t* ready;     // [B * Hkv] selection published in this launch
-  uint32_t* ctl;       // [0] ticket counter, [1] finished blocks, [2] error flag
 };
 
 hipError_t launch_append_prefill(const AppendPrefillArgs& a, hipStream_t s);
@@ -124,5 +137,7 @@ uint32_t partial_stride();
 uint32_t decode_max_chunks();  // split-K chunks per head the merge holds
 uint32_t topk_max_pages();     // pages per (sequence, head) top-k supports
 uint32_t fused_topk_max_pages();  // ... and the fused estimate + top-k kernel
+uint32_t layer_score_workers();   // scoring workgroups of the single-launch layer
+uint32_t counter_stride();        // u32 words between per-head counters (one cache line each)
 
 }  // namespace aoakv

@@ -331,11 +331,12 @@ def test_full_decode_step_matches_simulation(layout, L):
     o2 = decode_layer(qd, ctrl, 0).cpu().numpy()[0]
     assert np.array_equal(bits(o2), bits(o))
     assert np.array_equal(ctrl.topk_dindices_buffer.cpu().numpy()[0], sel.cpu().numpy())
-    ctrl.topk_dindices_buffer.fill_(-1)
-    o3 = decode_layer(qd, ctrl, 0, single_launch=True).cpu().numpy()[0]
-    assert np.array_equal(bits(o3), bits(o))
-    assert np.array_equal(ctrl.topk_dindices_buffer.cpu().numpy()[0], sel.cpu().numpy())
-    assert int(ctrl.workspace[8:12].view(torch.int32).item()) == 0, "spin-wait error flag set"
+    for rep in range(3):  # the ready flags must be clear again for every launch
+        ctrl.topk_dindices_buffer.fill_(-1)
+        o3 = decode_layer(qd, ctrl, 0, single_launch=True).cpu().numpy()[0]
+        assert np.array_equal(bits(o3), bits(o)), rep
+        assert np.array_equal(ctrl.topk_dindices_buffer.cpu().numpy()[0], sel.cpu().numpy())
+        assert int(ctrl.workspace[8:12].view(torch.int32).item()) == 0, "spin-wait error flag set"
 
 
 @pytest.mark.parametrize("layout", [NHD, HND])
@@ -351,6 +352,22 @@ def test_dense_decode_matches_dense_attention(layout):
     o = decode_sparse_attn(qd, ctrl, 0, None).cpu().numpy()[0].astype(np.float32)
     ref = sim.masked_decode_attention(q, K, V, None)[0, :, 0].astype(np.float32)
     assert np.abs(o - ref).max() <= 2e-3
+
+
+def _single_launch_matches(args, kwargs, o_ref, sel_ref, ws, reps=3):
+    """The one-launch layer (FLAG_SINGLE_LAUNCH) repeats the two-launch result
+    bit for bit, launch after launch, without its spin-wait error flag."""
+    from aoakv import ops
+    o, sel = args[1], args[11]
+    for rep in range(reps):
+        o.fill_(0)
+        sel.fill_(-1)
+        ops.sparse_decode_layer(*args, **kwargs,
+                                flags=ops.FLAG_VALUE_AWARE | ops.FLAG_FIXED | ops.FLAG_SINGLE_LAUNCH)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(o.cpu().numpy()), bits(o_ref)), rep
+        assert np.array_equal(sel.cpu().numpy(), sel_ref), rep
+        assert int(ws[8:12].view(torch.int32).item()) == 0, "spin-wait error flag set"
 
 
 def test_batched_ragged_decode_matches_simulation():
@@ -400,11 +417,15 @@ def test_batched_ragged_decode_matches_simulation():
     ws = ops.decode_workspace(B, H, H, kmax)
     qd = t(np.stack(qs))
     o = torch.empty_like(qd)
-    ops.sparse_decode_layer(qd, o, kv, t(indptr), t(kv_indices), lpl, meta, t(m_indptr),
-                            t(m_indices), lvn, scores, sel, 0, ws, maxP, HND,
-                            token_budgets=t(np.array(budgets, np.int32)))
+    args = (qd, o, kv, t(indptr), t(kv_indices), lpl, meta, t(m_indptr), t(m_indices), lvn,
+            scores, sel, 0, ws, maxP, HND)
+    kwargs = dict(token_budgets=t(np.array(budgets, np.int32)))
+    ops.sparse_decode_layer(*args, **kwargs)
+    o_dev, sel_dev = o, sel
     o = o.cpu().numpy()
     sel = sel.cpu().numpy()
+    _single_launch_matches(args, kwargs, o, sel, ws)
+    o_dev.copy_(torch.from_numpy(o))
     scores = scores.cpu().numpy()
     differs_from_quest = 0
     for b, (st, q, sc, pg) in enumerate(states):
@@ -451,8 +472,9 @@ def test_gqa_selection_and_decode():
     ws = ops.decode_workspace(1, Hq, Hkv, k)
     qd = torch.from_numpy(q[0, :, 0].copy()).to(DEV)[None]
     o = torch.empty_like(qd)
-    ops.sparse_decode_layer(qd, o, kv, indptr, idx, lpl, meta, mindptr, midx, lvn, scores, sel,
-                            budget, ws, P, HND)
+    args = (qd, o, kv, indptr, idx, lpl, meta, mindptr, midx, lvn, scores, sel, budget, ws, P, HND)
+    ops.sparse_decode_layer(*args)
+    _single_launch_matches(args, {}, o.cpu().numpy(), sel.cpu().numpy(), ws)
     sc = scores.cpu().numpy()[0]
     np.testing.assert_allclose(sc, scores_ref[0, :, 0], rtol=1e-5, atol=1e-4)
     sl = sel.cpu().numpy()[0]
