@@ -7,8 +7,10 @@ pages per head; keys N(0,1) with 4 of 128 channels x8, values N(0,1).  A
 step is one layer's sparse decode: value-aware page scores of all 2048 pages,
 per-head top-k, split-K attention over the selected pages.  The 32 layers
 (2.15 GB of cache+metadata touched per pass, far above the 256 MB MALL) are
-visited round-robin; the 32 launches pairs of a pass are captured in a HIP
-graph and replayed, as a decode loop would run them.
+visited round-robin; the 32 launches of a pass (one per layer) are captured
+in a HIP graph and replayed, as a decode loop would run them.  The
+two-launch path (scores + top-k, then decode) is timed beside it and must
+give the same bits.
 
 Prints ONE JSON line (rank 0).  Extra measurements (bulk metadata build,
 decode appends, eager launch path, per-kernel times) go under "extra".
@@ -278,6 +280,9 @@ def main():
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip appends / eager timings")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="for rocprofv3 --pmc: a 64 MiB device copy x3 (calibration), then one "
+                         "eager pass of the 32 one-launch layers; prints nothing else")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -326,6 +331,19 @@ def main():
     for l in range(n_layers):
         layer(l)
     torch.cuda.synchronize()
+    if args.pmc_pass:
+        src = torch.empty(64 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        for l in range(n_layers):
+            ops.sparse_decode_layer(q[l], o[l], kv[l], indptr, idx[l], lpl, meta[l], mindptr,
+                                    midx, lvn[l], scores[l], sel[l], BUDGET, ws, P, layout,
+                                    flags | ops.FLAG_SINGLE_LAUNCH)
+        torch.cuda.synchronize()
+        log("[bench] pmc pass done")
+        return
 
     def capture(fn):
         g = torch.cuda.CUDAGraph()
@@ -353,6 +371,7 @@ def main():
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e3 / (reps * n_layers)  # us per layer
 
+    # two launches per layer (scores + top-k, then decode)
     g_layer = capture(layer)
     time_graph(g_layer, warm)
     # replays must reproduce the eager result exactly
@@ -361,9 +380,9 @@ def main():
     g_layer.replay()
     torch.cuda.synchronize()
     replay_exact = bool(torch.equal(o, o_eager) and torch.equal(sel, sel_eager))
+    us_two = time_graph(g_layer, steps)
 
-    log(f"[bench] timing {steps} layers (graph replay) ...")
-    us_layer = time_graph(g_layer, steps)
+    # one launch per layer: the measured path
     def layer1(l):
         ops.sparse_decode_layer(q[l], o[l], kv[l], indptr, idx[l], lpl, meta[l], mindptr, midx,
                                 lvn[l], scores[l], sel[l], BUDGET, ws, P, layout,
@@ -371,7 +390,18 @@ def main():
 
     g_one = capture(layer1)
     time_graph(g_one, warm)
+    o.zero_()
+    sel.zero_()
+    g_one.replay()
+    torch.cuda.synchronize()
+    one_exact = bool(torch.equal(o, o_eager) and torch.equal(sel, sel_eager))
+    log(f"[bench] timing {steps} layers (graph replay, one launch per layer) ...")
     us_one = time_graph(g_one, steps)
+    spin_err = int(ws[8:12].view(torch.int32).item())
+    if spin_err != 0 or not one_exact:
+        raise SystemExit(f"single-launch layer failed: error flag {spin_err}, "
+                         f"equal to two launches: {one_exact}")
+    us_layer = us_one
     g_est, g_dec = capture(est), capture(dec)
     time_graph(g_est, warm)
     time_graph(g_dec, warm)
@@ -384,7 +414,7 @@ def main():
         t1 = torch.cuda.Event(enable_timing=True)
         t0.record()
         for i in range(steps):
-            layer(i % n_layers)
+            layer1(i % n_layers)
         t1.record()
         torch.cuda.synchronize()
         extra["eager_us_per_layer"] = round(t0.elapsed_time(t1) * 1e3 / steps, 3)
@@ -402,11 +432,19 @@ def main():
         log("[bench] config 5 (ragged batch) ...")
         extra["config5_ragged_batch16"] = ragged_batch_bench(dev, layout)
 
-    dom_us, dom_bytes, dom_name = (us_est, EST_BYTES, "estimate_kernel (score + fused top-k)") \
-        if us_est >= us_dec else (us_dec, DEC_BYTES, "decode_kernel (split-K sparse attention)")
+    # the measured path is one kernel per layer: it is the dominant kernel
+    dom_us, dom_bytes, dom_name = us_one, LAYER_BYTES, \
+        "layer_kernel (scores + top-k + split-K sparse attention, one launch)"
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9
+    # HBM bytes per launch of layer_kernel from the two rocprofv3 --pmc runs
+    # (FETCH_SIZE, WRITE_SIZE of `bench.py --pmc-pass`, each scaled by the
+    # counter's reading for a 64 MiB copy), kept beside their summaries
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "layer_kernel_traffic.json")
+    if args.layout == "hnd" and os.path.exists(tpath):
+        traffic = json.load(open(tpath)).get("traffic_bytes")
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom_name,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": dom_name,
             "bytes_per_launch": dom_bytes, "us_per_launch": round(dom_us, 3)}
 
     result = {
@@ -417,14 +455,15 @@ def main():
         "config": {"workload": "BASELINE config 2: sparse decode layer (value-aware scores of "
                                "2048 pages + per-head top-128 + split-K attention), 32 heads x "
                                "128, 32768 ctx, page 16, budget 2048, 32 rotated layers",
-                   "layout": args.layout.upper(), "launches_per_layer": 2,
+                   "layout": args.layout.upper(), "launches_per_layer": 1,
                    "hip_graph": True},
         "layer_GBps": round(LAYER_BYTES / (us_layer * 1e-6) / 1e9, 1),
         "layer_bytes": LAYER_BYTES,
         "layer_hbm_frac": round(LAYER_BYTES / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-        "per_kernel_us": {"estimate_topk": round(us_est, 3), "decode": round(us_dec, 3)},
-        "single_launch_us_per_layer": round(us_one, 3),
+        "two_launch_us_per_layer": round(us_two, 3),
+        "two_launch_kernel_us": {"estimate_topk": round(us_est, 3), "decode": round(us_dec, 3)},
         "graph_replay_exact": replay_exact,
+        "one_launch_equals_two_launches": one_exact,
         "roofline": roof,
     }
     if not args.no_cpu_baseline:
