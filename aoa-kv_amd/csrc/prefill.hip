@@ -16,9 +16,18 @@
 //   A and B elements with the same (l/32, j) share a k;
 //   C: register i of lane l -> row 8*(i/4) + 4*(l/32) + i%4, column l%32.
 //
-// Block = 4 waves = 128 queries of one head; K/V tiles of 64 keys (4 pages)
-// are gathered from the page table into LDS (K row-major, V transposed) with
-// the next tile's loads in flight during the current tile's MFMAs.
+// Block = 4 waves = 128 queries of one head.  K and V tiles of 64 keys go
+// from the paged cache straight into LDS (global_load_lds_dwordx4, no
+// register staging), double-buffered so tile i+1 loads while tile i is
+// computed.  Rows are 256 bytes (one key, 128 dims) with the 16-byte chunk j
+// of row r stored at chunk j ^ (r % 16), so the K reads of a wave (32 rows,
+// one chunk each) and the V reads below hit distinct banks.  Each wave
+// loads the 16 rows of one page per tile, so its page id is one scalar load,
+// fetched a tile ahead.  The V^T operand of O^T += V^T P^T is read from the
+// row-major V tile with ds_read_b64_tr_b16: in each 16-lane group, output
+// lane 4a+b receives element b of the 8-byte blocks addressed by lanes a,
+// a+4, a+8, a+12 (checked on the hardware), so four lanes pointing at four
+// consecutive key rows give each lane one dim of four keys.
 #include "kernels.hpp"
 
 namespace aoakv {
@@ -26,13 +35,16 @@ namespace aoakv {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_short4;
+typedef __attribute__((address_space(3))) char lds_char;
 
 constexpr int kPfThreads = 256;
 constexpr int kPfQueriesPerWave = 32;
 constexpr int kPfQueriesPerBlock = 128;
 constexpr int kPfTileKeys = 64;
-constexpr int kKRow = kHeadDim + 8;    // LDS row of K (halfs), padded against bank conflicts
-constexpr int kVRow = kPfTileKeys + 8; // LDS row of V^T (halfs)
+constexpr int kPfRowBytes = kHeadDim * 2;                   // one key row
+constexpr int kPfTileBytes = kPfTileKeys * kPfRowBytes;     // 16 KB
 constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ inline floatx16 mfma32(const half8& a, const half8& b, const floatx16& c) {
@@ -42,9 +54,12 @@ __device__ inline floatx16 mfma32(const half8& a, const half8& b, const floatx16
 // row of accumulator register i for lane group g
 __device__ inline int crow(int i, int g) { return 8 * (i / 4) + 4 * g + (i % 4); }
 
-__global__ __launch_bounds__(kPfThreads) void prefill_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) f16 sK[kPfTileKeys * kKRow];
-  __shared__ __attribute__((aligned(16))) f16 sVt[kHeadDim * kVRow];
+// byte offset of 16-byte chunk j of key row r in a swizzled tile
+__device__ inline int tile_off(int r, int j) { return r * kPfRowBytes + 16 * (j ^ (r & 15)); }
+
+__global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
+  // [buffer][K | V] tiles
+  __shared__ __attribute__((aligned(16))) char s_tiles[2][2][kPfTileBytes];
   const int tid = threadIdx.x;
   const int lane = (int)__lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -55,6 +70,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(PrefillArgs a) {
   const uint32_t qt = nqt - 1u - blockIdx.x;  // heaviest query tiles first
   const uint32_t L = a.L, Lq = a.Lq;
   const uint32_t off = L - Lq;                 // position of query 0
+  const uint32_t npages = (L + kPageSize - 1) / kPageSize;
 
   const uint32_t q = qt * kPfQueriesPerBlock + wave * kPfQueriesPerWave + c;
   const bool q_live = q < Lq;
@@ -77,24 +93,39 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(PrefillArgs a) {
                                                           16 * s + 8 * g)
                      : half8{};
 
-  // ---- tile loader: thread t covers keys 4*(t/16) .. +4, dims 8*(t%16) .. +8
-  const int lk = 4 * (tid / 16), ld = 8 * (tid % 16);
-  half8 pk0, pk1, pk2, pk3, pv0, pv1, pv2, pv3;
-#define AOAKV_PF_LOAD(R, K0)                                                         \
-  {                                                                                  \
-    const uint32_t key = (K0) + lk + R;                                              \
-    if (key < L) {                                                                   \
-      const uint32_t phys = (uint32_t)a.kv_indices[key / kPageSize];                 \
-      const size_t e = elem_off(a.g, phys, 0, h, key % kPageSize) + ld;              \
-      pk##R = *reinterpret_cast<const half8*>(a.kv + e);                             \
-      pv##R = *reinterpret_cast<const half8*>(a.kv + e + a.g.kv);                    \
-    } else {                                                                         \
-      pk##R = half8{};                                                               \
-      pv##R = half8{};                                                               \
-    }                                                                                \
-  }
-#define AOAKV_PF_LOAD_TILE(K0) \
-  AOAKV_PF_LOAD(0, K0) AOAKV_PF_LOAD(1, K0) AOAKV_PF_LOAD(2, K0) AOAKV_PF_LOAD(3, K0)
+  // ---- tile loader: wave w fills rows 16w .. 16w+15 (one page) of K and V,
+  // 4 rows (1 KB) per instruction; lane l lands at byte 16*l of its
+  // instruction's rows, i.e. row l/16, chunk slot l%16 -> it fetches the
+  // global chunk (l%16) ^ (row % 16).  A page past the sequence reads the
+  // last page (its keys are masked).
+  auto page_of = [&](uint32_t tile) -> uint32_t {
+    uint32_t p = tile * (kPfTileKeys / kPageSize) + (uint32_t)wave;
+    p = p < npages ? p : npages - 1u;
+    return (uint32_t)a.kv_indices[p];
+  };
+  const int lrow = lane / 16, lslot = lane % 16;
+  auto load_tile = [&](int buf, uint32_t phys) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 16 * wave + 4 * i + lrow;  // row in the tile; r % 16 = 4i + lrow
+      const int j = lslot ^ (r & 15);
+      const size_t e = elem_off(a.g, phys, 0, h, (uint32_t)(r & 15)) + 8 * j;
+      __builtin_amdgcn_global_load_lds(a.kv + e, &s_tiles[buf][0][(16 * wave + 4 * i) * kPfRowBytes],
+                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds(a.kv + e + a.g.kv,
+                                       &s_tiles[buf][1][(16 * wave + 4 * i) * kPfRowBytes], 16, 0, 0);
+    }
+  };
+
+  // ---- per-lane LDS offsets.  K operand (S^T = K Q^T): row ks*32 + c,
+  // chunk 2s + g.  V^T operand via the transpose read: in 16-lane group G,
+  // lane r = 4m + a addresses key row key0 + m, dims 32t + 16*(G%2) + 4a.
+  const int vm = (lane % 16) / 4, va4 = lane % 4, vG = lane / 16;
+  auto v_off = [&](int t, int key0) {
+    const int row = key0 + vm;
+    const int dim = 32 * t + 16 * (vG % 2) + 4 * va4;
+    return row * kPfRowBytes + 16 * ((dim / 8) ^ (row & 15)) + 2 * (dim % 8);
+  };
 
   floatx16 acc_o[4];
 #pragma unroll
@@ -102,22 +133,22 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(PrefillArgs a) {
   float m_run = -INFINITY, l_run = 0.f;
   const float scale = a.sm_scale * kLog2e;
 
-  AOAKV_PF_LOAD_TILE(0u)
+  load_tile(0, page_of(0u));
+  uint32_t phys_next = page_of(1u);
   for (uint32_t it = 0; it < ntiles; ++it) {
     const uint32_t k0 = it * kPfTileKeys;
-    __syncthreads();  // every wave is done reading the previous tile
-    *reinterpret_cast<half8*>(&sK[(lk + 0) * kKRow + ld]) = pk0;
-    *reinterpret_cast<half8*>(&sK[(lk + 1) * kKRow + ld]) = pk1;
-    *reinterpret_cast<half8*>(&sK[(lk + 2) * kKRow + ld]) = pk2;
-    *reinterpret_cast<half8*>(&sK[(lk + 3) * kKRow + ld]) = pk3;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {  // V transposed: 4 keys of dim ld+j
-      const half4 col = {pv0[j], pv1[j], pv2[j], pv3[j]};
-      *reinterpret_cast<half4*>(&sVt[(ld + j) * kVRow + lk]) = col;
-    }
+    const int buf = (int)(it & 1u);
+    // tile `it` has landed in LDS (this wave's loads: vmcnt; the others':
+    // the barrier), and every wave is done with the other buffer
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (it + 1 < ntiles) AOAKV_PF_LOAD_TILE(k0 + kPfTileKeys)  // in flight during the MFMAs
+    if (it + 1 < ntiles) {  // in flight during this tile's MFMAs
+      load_tile(buf ^ 1, phys_next);
+      phys_next = page_of(it + 2u);
+    }
     if (k0 >= wave_kend) continue;  // wave-uniform: tile entirely above this wave's queries
+    const lds_char* sK = (const lds_char*)&s_tiles[buf][0][0];
+    const lds_char* sV = (const lds_char*)&s_tiles[buf][1][0];
 
     // ---- S^T = K Q^T for two 32-key sub-tiles
     floatx16 acc_s[2];
@@ -126,7 +157,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(PrefillArgs a) {
       acc_s[ks] = floatx16{};
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
-        const half8 ka = *reinterpret_cast<const half8*>(&sK[(ks * 32 + c) * kKRow + 16 * s + 8 * g]);
+        const half8 ka = *reinterpret_cast<const __attribute__((address_space(3))) half8*>(
+            sK + tile_off(ks * 32 + c, 2 * s + g));
         acc_s[ks] = mfma32(ka, qreg[s], acc_s[ks]);
       }
     }
@@ -166,20 +198,22 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(PrefillArgs a) {
       for (int i = 0; i < 16; ++i) acc_o[t][i] *= alpha;
 
     // ---- O^T += V^T P^T.  B element j of half hf of sub-tile ks is the
-    // probability of key ks*32 + 8*(2*hf + j/4) + 4*g + j%4, so the A operand
-    // (V^T) lane reads those keys for its dim: two runs of 4 keys.
+    // probability of key ks*32 + 16*hf + 8*(j/4) + 4*g + j%4, so the A
+    // operand of lane l is dim 32t + l%32 of keys key0 .. key0+3 (j < 4)
+    // and key0+8 .. key0+11 (j >= 4), key0 = ks*32 + 16*hf + 4*g.
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const f16* vrow = &sVt[(t * 32 + c) * kVRow];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
-          const int kb = ks * 32 + 16 * hf + 4 * g;
-          const half4 lo = *reinterpret_cast<const half4*>(vrow + kb);
-          const half4 hi = *reinterpret_cast<const half4*>(vrow + kb + 8);
-          const half8 va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-          acc_o[t] = mfma32(va, pb[ks][hf], acc_o[t]);
+          const int key0 = ks * 32 + 16 * hf + 4 * g;
+          const half4 lo = __builtin_bit_cast(
+              half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(sV + v_off(t, key0))));
+          const half4 hi = __builtin_bit_cast(
+              half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(sV + v_off(t, key0 + 8))));
+          const half8 vfrag = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+          acc_o[t] = mfma32(vfrag, pb[ks][hf], acc_o[t]);
         }
       }
     }
@@ -200,8 +234,6 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(PrefillArgs a) {
     }
   }
 }
-#undef AOAKV_PF_LOAD_TILE
-#undef AOAKV_PF_LOAD
 
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t s) {
   const uint32_t nqt = (a.Lq + kPfQueriesPerBlock - 1) / kPfQueriesPerBlock;
