@@ -127,75 +127,89 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
     return row * kPfRowBytes + 16 * ((dim / 8) ^ (row & 15)) + 2 * (dim % 8);
   };
 
+  // lane-constant byte offsets inside a tile (the loop adds the buffer base)
+  int k_off[8], v_lo[4], v_hi[4];
+#pragma unroll
+  for (int s8 = 0; s8 < 8; ++s8) k_off[s8] = tile_off(c, 2 * s8 + g);  // + ks * 32 rows below
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {  // key0 = 4g (+ ks*32 + 16*hf below) and key0 + 8
+    v_lo[t] = v_off(t, 4 * g);
+    v_hi[t] = v_off(t, 4 * g + 8);
+  }
+  // rows ks*32 + 16*hf + r have r % 16 == (row) % 16, so adding whole
+  // multiples of 16 rows keeps every swizzle: offsets step by 16 rows
+  constexpr int kRow16 = 16 * kPfRowBytes;
+
   floatx16 acc_o[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) acc_o[t] = floatx16{};
-  float m_run = -INFINITY, l_run = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;  // running max of the unscaled scores
   const float scale = a.sm_scale * kLog2e;
+  // smallest query position of this wave: tiles with every key at or below
+  // it (and below L) need no mask
+  const uint32_t wave_q0 = off + qt * kPfQueriesPerBlock + wave * kPfQueriesPerWave;
 
-  load_tile(0, page_of(0u));
-  uint32_t phys_next = page_of(1u);
-  for (uint32_t it = 0; it < ntiles; ++it) {
-    const uint32_t k0 = it * kPfTileKeys;
-    const int buf = (int)(it & 1u);
-    // tile `it` has landed in LDS (this wave's loads: vmcnt; the others':
-    // the barrier), and every wave is done with the other buffer
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (it + 1 < ntiles) {  // in flight during this tile's MFMAs
-      load_tile(buf ^ 1, phys_next);
-      phys_next = page_of(it + 2u);
-    }
-    if (k0 >= wave_kend) continue;  // wave-uniform: tile entirely above this wave's queries
-    const lds_char* sK = (const lds_char*)&s_tiles[buf][0][0];
-    const lds_char* sV = (const lds_char*)&s_tiles[buf][1][0];
-
+  // one 64-key tile from LDS buffer `tile_base`
+  auto tile = [&](const lds_char* tile_base, uint32_t k0) {
+    const lds_char* sK = tile_base;
+    const lds_char* sV = tile_base + kPfTileBytes;
     // ---- S^T = K Q^T for two 32-key sub-tiles
     floatx16 acc_s[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       acc_s[ks] = floatx16{};
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
+      for (int s8 = 0; s8 < 8; ++s8) {
         const half8 ka = *reinterpret_cast<const __attribute__((address_space(3))) half8*>(
-            sK + tile_off(ks * 32 + c, 2 * s + g));
-        acc_s[ks] = mfma32(ka, qreg[s], acc_s[ks]);
+            sK + k_off[s8] + 2 * ks * kRow16);
+        acc_s[ks] = mfma32(ka, qreg[s8], acc_s[ks]);
       }
     }
-    // ---- scale, causal / length mask, running max of this query
-    float mt = -INFINITY;
+    // ---- causal / length mask (only where a key can be past L or past
+    // some query of the wave), running max of this query
+    const bool full = k0 + kPfTileKeys <= L && (!a.causal || k0 + kPfTileKeys - 1u <= wave_q0);
+    if (!full) {
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+      for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const uint32_t key = k0 + ks * 32 + crow(i, g);
-        const bool ok = key < L && (!a.causal || key <= qpos);
-        const float x = ok ? acc_s[ks][i] * scale : -INFINITY;
-        acc_s[ks][i] = x;
-        mt = fmaxf(mt, x);
-      }
+        for (int i = 0; i < 16; ++i) {
+          const uint32_t key = k0 + ks * 32 + crow(i, g);
+          const bool ok = key < L && (!a.causal || key <= qpos);
+          acc_s[ks][i] = ok ? acc_s[ks][i] : -INFINITY;
+        }
     }
+    float mt = acc_s[0][0];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mt = fmaxf(mt, acc_s[ks][i]);
     mt = fmaxf(mt, __shfl_xor(mt, 32));
+    // every query sees key 0 in the first tile, so m_new is finite
     const float m_new = fmaxf(m_run, mt);
-    const float alpha = m_new == -INFINITY ? 1.f : exp2f(m_run - m_new);
+    const float neg_m = -m_new * scale;
     float lt = 0.f;
     half8 pb[2][2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float p = m_new == -INFINITY ? 0.f : exp2f(acc_s[ks][i] - m_new);
+        // 2^((s - m) * scale); a masked score (-inf) gives 0
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(acc_s[ks][i], scale, neg_m));
         lt += p;
         pb[ks][i / 8][i % 8] = (f16)p;
       }
     }
     lt += __shfl_xor(lt, 32);
-    l_run = l_run * alpha + lt;
+    if (__builtin_amdgcn_ballot_w64(m_new != m_run) != 0) {  // some max moved: rescale
+      const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale);  // m_run = -inf: 0
+      l_run = l_run * alpha;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc_o[t][i] *= alpha;
+    }
+    l_run = l_run + lt;
     m_run = m_new;
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc_o[t][i] *= alpha;
 
     // ---- O^T += V^T P^T.  B element j of half hf of sub-tile ks is the
     // probability of key ks*32 + 16*hf + 8*(j/4) + 4*g + j%4, so the A
@@ -207,15 +221,37 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
       for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
-          const int key0 = ks * 32 + 16 * hf + 4 * g;
+          const int rows = (2 * ks + hf) * kRow16;
           const half4 lo = __builtin_bit_cast(
-              half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(sV + v_off(t, key0))));
+              half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(sV + v_lo[t] + rows)));
           const half4 hi = __builtin_bit_cast(
-              half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(sV + v_off(t, key0 + 8))));
+              half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(sV + v_hi[t] + rows)));
           const half8 vfrag = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
           acc_o[t] = mfma32(vfrag, pb[ks][hf], acc_o[t]);
         }
       }
+    }
+  };
+
+  load_tile(0, page_of(0u));
+  uint32_t phys_next = page_of(1u);
+  const lds_char* base = (const lds_char*)&s_tiles[0][0][0];
+  // two tiles per trip so each buffer's base is a constant offset
+  for (uint32_t it = 0; it < ntiles; it += 2) {
+#pragma unroll
+    for (uint32_t u = 0; u < 2; ++u) {
+      const uint32_t ti = it + u;
+      if (ti >= ntiles) break;  // uniform
+      // tile ti has landed in LDS (this wave's loads: vmcnt; the others':
+      // the barrier), and every wave is done with the other buffer
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (ti + 1 < ntiles) {  // in flight during this tile's MFMAs
+        load_tile((int)(u ^ 1u), phys_next);
+        phys_next = page_of(ti + 2u);
+      }
+      if (ti * kPfTileKeys < wave_kend)  // wave-uniform: skip tiles above this wave's queries
+        tile(base + u * 2 * kPfTileBytes, ti * kPfTileKeys);
     }
   }
 
