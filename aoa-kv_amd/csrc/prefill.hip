@@ -58,8 +58,10 @@ __device__ inline int crow(int i, int g) { return 8 * (i / 4) + 4 * g + (i % 4);
 __device__ inline int tile_off(int r, int j) { return r * kPfRowBytes + 16 * (j ^ (r & 15)); }
 
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
-  // [buffer][K | V] tiles
-  __shared__ __attribute__((aligned(16))) char s_tiles[2][2][kPfTileBytes];
+  // two buffers of [K | V] tiles, separate objects so the compiler sees that
+  // the loads into one never alias the reads of the other (no wait on them)
+  __shared__ __attribute__((aligned(16))) char s_buf0[2 * kPfTileBytes];
+  __shared__ __attribute__((aligned(16))) char s_buf1[2 * kPfTileBytes];
   const int tid = threadIdx.x;
   const int lane = (int)__lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -98,22 +100,27 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
   // instruction's rows, i.e. row l/16, chunk slot l%16 -> it fetches the
   // global chunk (l%16) ^ (row % 16).  A page past the sequence reads the
   // last page (its keys are masked).
+  // The page table is read through the constant address space: the kernel
+  // never writes it, and a scalar load keeps it off the vector memory
+  // counter that the K/V tile loads are waited on with.
+  const __attribute__((address_space(4))) int32_t* kv_idx =
+      (const __attribute__((address_space(4))) int32_t*)a.kv_indices;
   auto page_of = [&](uint32_t tile) -> uint32_t {
     uint32_t p = tile * (kPfTileKeys / kPageSize) + (uint32_t)wave;
     p = p < npages ? p : npages - 1u;
-    return (uint32_t)a.kv_indices[p];
+    return (uint32_t)kv_idx[p];
   };
   const int lrow = lane / 16, lslot = lane % 16;
-  auto load_tile = [&](int buf, uint32_t phys) {
+  auto load_tile = [&](char* buf, uint32_t phys) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * wave + 4 * i + lrow;  // row in the tile; r % 16 = 4i + lrow
       const int j = lslot ^ (r & 15);
       const size_t e = elem_off(a.g, phys, 0, h, (uint32_t)(r & 15)) + 8 * j;
-      __builtin_amdgcn_global_load_lds(a.kv + e, &s_tiles[buf][0][(16 * wave + 4 * i) * kPfRowBytes],
-                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds(a.kv + e, buf + (16 * wave + 4 * i) * kPfRowBytes, 16, 0, 0);
       __builtin_amdgcn_global_load_lds(a.kv + e + a.g.kv,
-                                       &s_tiles[buf][1][(16 * wave + 4 * i) * kPfRowBytes], 16, 0, 0);
+                                       buf + kPfTileBytes + (16 * wave + 4 * i) * kPfRowBytes, 16, 0,
+                                       0);
     }
   };
 
@@ -153,18 +160,26 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
   auto tile = [&](const lds_char* tile_base, uint32_t k0) {
     const lds_char* sK = tile_base;
     const lds_char* sV = tile_base + kPfTileBytes;
-    // ---- S^T = K Q^T for two 32-key sub-tiles
+    // ---- S^T = K Q^T for two 32-key sub-tiles.  All 8 K fragments of a
+    // sub-tile are read before its MFMAs, and the second sub-tile's reads
+    // go out before the first sub-tile's MFMAs, so no MFMA waits on a
+    // just-issued LDS read.
     floatx16 acc_s[2];
+    half8 kf0[8], kf1[8];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      acc_s[ks] = floatx16{};
+    for (int s8 = 0; s8 < 8; ++s8)
+      kf0[s8] = *reinterpret_cast<const __attribute__((address_space(3))) half8*>(sK + k_off[s8]);
 #pragma unroll
-      for (int s8 = 0; s8 < 8; ++s8) {
-        const half8 ka = *reinterpret_cast<const __attribute__((address_space(3))) half8*>(
-            sK + k_off[s8] + 2 * ks * kRow16);
-        acc_s[ks] = mfma32(ka, qreg[s8], acc_s[ks]);
-      }
-    }
+    for (int s8 = 0; s8 < 8; ++s8)
+      kf1[s8] = *reinterpret_cast<const __attribute__((address_space(3))) half8*>(
+          sK + k_off[s8] + 2 * kRow16);
+    __builtin_amdgcn_sched_barrier(0);
+    acc_s[0] = floatx16{};
+#pragma unroll
+    for (int s8 = 0; s8 < 8; ++s8) acc_s[0] = mfma32(kf0[s8], qreg[s8], acc_s[0]);
+    acc_s[1] = floatx16{};
+#pragma unroll
+    for (int s8 = 0; s8 < 8; ++s8) acc_s[1] = mfma32(kf1[s8], qreg[s8], acc_s[1]);
     // ---- causal / length mask (only where a key can be past L or past
     // some query of the wave), running max of this query
     const bool full = k0 + kPfTileKeys <= L && (!a.causal || k0 + kPfTileKeys - 1u <= wave_q0);
@@ -184,8 +199,13 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) mt = fmaxf(mt, acc_s[ks][i]);
     mt = fmaxf(mt, __shfl_xor(mt, 32));
-    // every query sees key 0 in the first tile, so m_new is finite
-    const float m_new = fmaxf(m_run, mt);
+    // Lazy rescaling: the reference max m_run moves only when some query's
+    // tile max exceeds it by more than 2^8 in probability (the first tile
+    // always moves it: every query sees key 0 there).  Otherwise
+    // probabilities stay <= 256, exact in fp16 relative terms, and the
+    // final o = O / l divides both by the same reference.
+    const bool move = __builtin_amdgcn_ballot_w64((mt - m_run) * scale > 8.f) != 0;
+    const float m_new = move ? fmaxf(m_run, mt) : m_run;
     const float neg_m = -m_new * scale;
     float lt = 0.f;
     half8 pb[2][2];
@@ -200,7 +220,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
       }
     }
     lt += __shfl_xor(lt, 32);
-    if (__builtin_amdgcn_ballot_w64(m_new != m_run) != 0) {  // some max moved: rescale
+    if (move) {  // the reference moved for some query: rescale
       const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale);  // m_run = -inf: 0
       l_run = l_run * alpha;
 #pragma unroll
@@ -215,28 +235,37 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
     // probability of key ks*32 + 16*hf + 8*(j/4) + 4*g + j%4, so the A
     // operand of lane l is dim 32t + l%32 of keys key0 .. key0+3 (j < 4)
     // and key0+8 .. key0+11 (j >= 4), key0 = ks*32 + 16*hf + 4*g.
+    // the 4 fragments (8 transpose reads) of dim block t+1 are read while
+    // dim block t's MFMAs run
+    auto vfrags = [&](int t, half8 (&vf)[4]) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const int rows = (2 * ks + hf) * kRow16;
-          const half4 lo = __builtin_bit_cast(
-              half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(sV + v_lo[t] + rows)));
-          const half4 hi = __builtin_bit_cast(
-              half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(sV + v_hi[t] + rows)));
-          const half8 vfrag = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-          acc_o[t] = mfma32(vfrag, pb[ks][hf], acc_o[t]);
-        }
+      for (int kk = 0; kk < 4; ++kk) {  // kk = 2*ks + hf
+        const int rows = kk * kRow16;
+        const half4 lo = __builtin_bit_cast(
+            half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(sV + v_lo[t] + rows)));
+        const half4 hi = __builtin_bit_cast(
+            half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(sV + v_hi[t] + rows)));
+        vf[kk] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
       }
+    };
+    half8 vfa[4], vfb[4];
+    vfrags(0, vfa);
+#pragma unroll
+    for (int t = 0; t < 4; t += 2) {
+      vfrags(t + 1, vfb);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) acc_o[t] = mfma32(vfa[kk], pb[kk / 2][kk % 2], acc_o[t]);
+      if (t + 2 < 4) vfrags(t + 2, vfa);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) acc_o[t + 1] = mfma32(vfb[kk], pb[kk / 2][kk % 2], acc_o[t + 1]);
     }
   };
 
-  load_tile(0, page_of(0u));
+  load_tile(s_buf0, page_of(0u));
   uint32_t phys_next = page_of(1u);
-  const lds_char* base = (const lds_char*)&s_tiles[0][0][0];
-  // two tiles per trip so each buffer's base is a constant offset
+  // two tiles per trip: even tiles in buffer 0, odd tiles in buffer 1
   for (uint32_t it = 0; it < ntiles; it += 2) {
 #pragma unroll
     for (uint32_t u = 0; u < 2; ++u) {
@@ -247,11 +276,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       if (ti + 1 < ntiles) {  // in flight during this tile's MFMAs
-        load_tile((int)(u ^ 1u), phys_next);
+        load_tile(u == 0u ? s_buf1 : s_buf0, phys_next);
         phys_next = page_of(ti + 2u);
       }
       if (ti * kPfTileKeys < wave_kend)  // wave-uniform: skip tiles above this wave's queries
-        tile(base + u * 2 * kPfTileBytes, ti * kPfTileKeys);
+        tile((const lds_char*)(u == 0u ? s_buf0 : s_buf1), ti * kPfTileKeys);
     }
   }
 
