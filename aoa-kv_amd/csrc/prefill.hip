@@ -19,9 +19,10 @@
 // Block = 4 waves = 128 queries of one head.  K and V tiles of 64 keys go
 // from the paged cache straight into LDS (global_load_lds_dwordx4, no
 // register staging), double-buffered so tile i+1 loads while tile i is
-// computed.  Rows are 256 bytes (one key, 128 dims) with the 16-byte chunk j
-// of row r stored at chunk j ^ (r % 16), so the K reads of a wave (32 rows,
-// one chunk each) and the V reads below hit distinct banks.  Each wave
+// computed.  Rows are 256 bytes (one key, 128 dims) with their 16-byte
+// chunks permuted per row (k_swz / v_swz below), so the K reads of a wave
+// and the V transpose reads hit distinct banks (no LDS bank conflicts,
+// measured with SQ_LDS_BANK_CONFLICT).  Each wave
 // loads the 16 rows of one page per tile, so its page id is one scalar load,
 // fetched a tile ahead.  The V^T operand of O^T += V^T P^T is read from the
 // row-major V tile with ds_read_b64_tr_b16: in each 16-lane group, output
@@ -54,8 +55,17 @@ __device__ inline floatx16 mfma32(const half8& a, const half8& b, const floatx16
 // row of accumulator register i for lane group g
 __device__ inline int crow(int i, int g) { return 8 * (i / 4) + 4 * g + (i % 4); }
 
-// byte offset of 16-byte chunk j of key row r in a swizzled tile
-__device__ inline int tile_off(int r, int j) { return r * kPfRowBytes + 16 * (j ^ (r & 15)); }
+// Chunk swizzles (16-byte chunk j of key row r sits at chunk j ^ swz(r)).
+// K is read as one chunk of 32 consecutive rows per instruction: XOR with
+// r % 16 spreads them over all 16 chunk positions.  V is read with the
+// transpose read: a 16-lane group takes 2 adjacent chunks of 4 consecutive
+// rows (the other group of the half-wave the next 2 chunks), so XOR with
+// 4 * (r % 4) gives those 16 chunks distinct positions.
+__device__ inline int k_swz(int r) { return r & 15; }
+__device__ inline int v_swz(int r) { return 4 * (r & 3); }
+
+// byte offset of 16-byte chunk j of key row r in a K tile
+__device__ inline int tile_off(int r, int j) { return r * kPfRowBytes + 16 * (j ^ k_swz(r)); }
 
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
   // two buffers of [K | V] tiles, separate objects so the compiler sees that
@@ -115,10 +125,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * wave + 4 * i + lrow;  // row in the tile; r % 16 = 4i + lrow
-      const int j = lslot ^ (r & 15);
-      const size_t e = elem_off(a.g, phys, 0, h, (uint32_t)(r & 15)) + 8 * j;
-      __builtin_amdgcn_global_load_lds(a.kv + e, buf + (16 * wave + 4 * i) * kPfRowBytes, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(a.kv + e + a.g.kv,
+      const size_t e = elem_off(a.g, phys, 0, h, (uint32_t)(r & 15));
+      __builtin_amdgcn_global_load_lds(a.kv + e + 8 * (lslot ^ k_swz(r)),
+                                       buf + (16 * wave + 4 * i) * kPfRowBytes, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(a.kv + e + a.g.kv + 8 * (lslot ^ v_swz(r)),
                                        buf + kPfTileBytes + (16 * wave + 4 * i) * kPfRowBytes, 16, 0,
                                        0);
     }
@@ -131,7 +141,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
   auto v_off = [&](int t, int key0) {
     const int row = key0 + vm;
     const int dim = 32 * t + 16 * (vG % 2) + 4 * va4;
-    return row * kPfRowBytes + 16 * ((dim / 8) ^ (row & 15)) + 2 * (dim % 8);
+    return row * kPfRowBytes + 16 * ((dim / 8) ^ v_swz(row)) + 2 * (dim % 8);
   };
 
   // lane-constant byte offsets inside a tile (the loop adds the buffer base)
@@ -143,8 +153,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
     v_lo[t] = v_off(t, 4 * g);
     v_hi[t] = v_off(t, 4 * g + 8);
   }
-  // rows ks*32 + 16*hf + r have r % 16 == (row) % 16, so adding whole
-  // multiples of 16 rows keeps every swizzle: offsets step by 16 rows
+  // adding whole multiples of 16 rows keeps both swizzles: offsets step by
+  // 16 rows
   constexpr int kRow16 = 16 * kPfRowBytes;
 
   floatx16 acc_o[4];
