@@ -280,6 +280,8 @@ def main():
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip appends / eager timings")
+    ap.add_argument("--prefill-pass", action="store_true",
+                    help="config 4 only: causal paged prefill at 8k and 16k tokens, one JSON line")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="for rocprofv3 --pmc: a 64 MiB device copy x3 (calibration), then one "
                          "eager pass of the 32 one-launch layers; prints nothing else")
@@ -303,6 +305,17 @@ def main():
     n_layers = 32
     steps = max(n_layers, (args.steps // n_layers) * n_layers)
     warm = max(n_layers, (args.warmup // n_layers) * n_layers)
+
+    if args.prefill_pass:
+        res = {"workload": "BASELINE config 4: causal paged prefill, 32 heads x 128, fp16",
+               "layout": args.layout.upper(), "mfma_peak_tflops": 2500.0}
+        for Lp in (8192, 16384):
+            us, tf = prefill_bench(dev, layout, Lp)
+            res[f"prefill_{Lp // 1024}k_us"] = round(us, 1)
+            res[f"prefill_{Lp // 1024}k_TFLOPs"] = round(tf, 1)
+            res[f"prefill_{Lp // 1024}k_mfma_frac"] = round(tf / 2500.0, 4)
+        print(json.dumps(res))
+        return
 
     log(f"[bench] {aoakv.version()} layout={args.layout} building {n_layers} layers ...")
     B = build_layers(n_layers, layout, dev)
