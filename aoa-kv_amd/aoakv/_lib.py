@@ -17,6 +17,7 @@ AOAKV_ERR_HIP = 3
 FLAG_VALUE_AWARE = 1
 FLAG_FIXED = 2
 FLAG_SINGLE_LAUNCH = 4
+FLAG_QUEST_KERNEL = 8
 
 _u32 = ctypes.c_uint32
 _p = ctypes.c_void_p
@@ -38,7 +39,7 @@ SIGNATURES = {
     "aoakv_decode_workspace_size": [_u32, _u32, _u32, _u32, _u32],
     "aoakv_workspace_init": [_p, _sz, _p],
     "aoakv_decode_sparse_attn": [_p, _p, _p, _p, _p, _p, _p, _u32, _u32, _p, _p, _sz, _u32,
-                                 _u32, _u32, _u32, _u32, _u32, _u32, _p],
+                                 _u32, _u32, _u32, _u32, _u32, _u32, _u32, _p],
     "aoakv_sparse_decode_layer": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _u32, _p,
                                   _u32, _u32, _p, _p, _sz, _u32, _u32, _u32, _u32, _u32,
                                   _u32, _u32, _u32, _p],

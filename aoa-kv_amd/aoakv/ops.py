@@ -11,7 +11,8 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._lib import FLAG_FIXED, FLAG_SINGLE_LAUNCH, FLAG_VALUE_AWARE  # noqa: F401  (re-exported)
+from ._lib import (FLAG_FIXED, FLAG_QUEST_KERNEL, FLAG_SINGLE_LAUNCH,  # noqa: F401  (re-exported)
+                   FLAG_VALUE_AWARE)
 
 NHD = 0
 HND = 1
@@ -150,8 +151,10 @@ def decode_workspace(batch: int, num_qo_heads: int, num_kv_heads: int, max_sel_p
 
 def decode_sparse_attn(q, o, kv_data, kv_indptr, kv_indices, kv_last_page_len, sel_pages,
                        token_budget: int, workspace, max_pages: int, num_kv_heads: int,
-                       layout: int, token_budgets=None):
-    """Reference: quest/ops/csrc/approx_attn.cu:68-151.  sel_pages None = dense."""
+                       layout: int, token_budgets=None, flags: int = 0):
+    """Reference: quest/ops/csrc/approx_attn.cu:68-151.  sel_pages None = dense.
+    ``flags`` = FLAG_QUEST_KERNEL: sel_pages rows hold the pages chosen
+    besides the last page, which is attended as well."""
     _need(q, "q", torch.float16)
     _need(o, "o", torch.float16)
     _need(kv_data, "kv_data", torch.float16)
@@ -173,7 +176,7 @@ def decode_sparse_attn(q, o, kv_data, kv_indptr, kv_indices, kv_last_page_len, s
               kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
               _ptr(sel_pages), 0 if sel_pages is None else sel_pages.shape[-1], token_budget,
               _ptr(token_budgets), workspace.data_ptr(), workspace.numel(), B, max_pages, Hq,
-              Hkv, D, S, layout, _stream())
+              Hkv, D, S, layout, flags, _stream())
 
 
 def sparse_decode_layer(q, o, kv_data, kv_indptr, kv_indices, kv_last_page_len, metadata_data,

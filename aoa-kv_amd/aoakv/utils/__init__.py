@@ -11,7 +11,10 @@ Same names, same argument meaning, same call order as QuestAttention.forward
     o = decode_sparse_attn(q, ctrl, layer, ctrl.topk_dindices_buffer)
 
 ``decode_sparse_attn(q, ctrl, layer, ctrl.kv_indices_without_last)`` (or
-``None``) attends every page, as the reference's dense-layer path does.
+``None``) attends every page, as the reference's dense-layer path does.  Any
+other ``topk_indices`` tensor of physical page ids, ``[Hkv, n]``, is attended
+as given (with the quest_kernel convention the last page is added, as the
+reference's ``decode_sparse_attn`` does with ``kv_last_page_idx``).
 """
 from __future__ import annotations
 
@@ -71,7 +74,8 @@ def prefill_forward(q: torch.Tensor, iController: InferenceController, layer_idx
 
 def decode_estimate(q: torch.Tensor, iController: InferenceController, layer_idx: int
                     ) -> torch.Tensor:
-    """Page scores of every page, [Hkv, P] fp32 (reference __init__.py:177-214)."""
+    """Page scores of every page, [Hkv, P] fp32 (reference __init__.py:177-214);
+    [Hkv, P - 1] with the quest_kernel convention (the last page unscored)."""
     c = iController
     P = len(c.kv_cache.indicies)
     ops.estimate_attn_score(
@@ -79,12 +83,13 @@ def decode_estimate(q: torch.Tensor, iController: InferenceController, layer_idx
         c.metadata_indptr_for_append, c.metadata_indices, c.kv_indptr_for_append,
         c.kv_indices_with_last, c.kv_last_page_len_t, c.v_log_norm_layer(layer_idx), P,
         c.layout, c.flags)
-    return c.scores[0, :, :P]
+    return c.scores[0, :, :P - 1 if c.quest_kernel else P]
 
 
 def decode_topk(estimated_attn_score: torch.Tensor, iController: InferenceController):
     """Top-k pages per kv head into ``topk_dindices_buffer`` [Hkv, k] (physical
-    page ids, ascending) (reference __init__.py:216-246)."""
+    page ids, ascending) (reference __init__.py:216-246); [Hkv, k - 1], the
+    pages besides the last, with the quest_kernel convention."""
     c = iController
     ops.topk_filtering(c.scores, c.kv_indptr_for_append, c.kv_indices_with_last,
                        c.kv_last_page_len_t, c.token_budget, c._sel, c.page_size, c.flags)
@@ -100,12 +105,26 @@ def decode_sparse_attn(q: torch.Tensor, iController: InferenceController, layer_
     ``iController.kv_indices_without_last``."""
     c = iController
     dense = topk_indices is None or topk_indices is c.kv_indices_without_last
+    if dense:
+        sel = None
+    elif (topk_indices.dtype == torch.int32 and topk_indices.is_cuda and
+          topk_indices.untyped_storage().data_ptr() == c._sel.untyped_storage().data_ptr()):
+        sel = c._sel  # this controller's own top-k output (row stride max_kv_pages)
+    else:
+        if topk_indices.dim() == 3:
+            topk_indices = topk_indices[0]
+        if topk_indices.dim() != 2 or topk_indices.shape[0] != c.num_kv_heads:
+            raise ValueError(f"topk_indices must be [{c.num_kv_heads}, n] physical page ids, "
+                             f"got {tuple(topk_indices.shape)}")
+        sel = topk_indices.to(device=c.device, dtype=torch.int32).contiguous().unsqueeze(0)
+        if sel.shape[-1] == 0:  # quest_kernel with a one-page budget: the last page only
+            sel = torch.zeros((1, c.num_kv_heads, 1), dtype=torch.int32, device=c.device)
     q3 = q.view(1, c.num_heads, c.head_dim)
     o = torch.empty_like(q3)
     ops.decode_sparse_attn(
         q3, o, c.kv_cache.buf_layer(layer_idx), c.kv_indptr_for_append, c.kv_indices_with_last,
-        c.kv_last_page_len_t, None if dense else c._sel, c.token_budget, c.workspace,
-        len(c.kv_cache.indicies), c.num_kv_heads, c.layout)
+        c.kv_last_page_len_t, sel, c.token_budget, c.workspace, len(c.kv_cache.indicies),
+        c.num_kv_heads, c.layout, flags=c.flags & ops.FLAG_QUEST_KERNEL)
     return o.view_as(q)
 
 

@@ -11,6 +11,12 @@ switch trees.  Differences, by design:
   synchronises with the host;
 * scores are fp32 and the per-page value statistic is written for every
   page, with the page mean of V kept in ``v_mean`` for the running mean.
+
+``semantics="quest_kernel"`` switches to the reference kernel's convention
+instead (controller.py:113-124, quest/utils/__init__.py:196-246): the last
+page is never scored and always attended, ``inference_page_budget - 1``
+pages are selected from the others, and ``topk_dindices_buffer`` is the
+reference's ``[H, inference_page_budget - 1]`` top-k output.
 """
 from __future__ import annotations
 
@@ -27,9 +33,13 @@ class InferenceController:
     def __init__(self, num_layers, num_heads, head_dim, page_size, page_budget, max_seq_len,
                  dtype, device, layout: int = TensorLayout.HND,
                  num_kv_heads: Optional[int] = None, fixed: bool = True,
-                 value_aware: bool = True, shuffle_seed: Optional[int] = None):
+                 value_aware: bool = True, shuffle_seed: Optional[int] = None,
+                 semantics: str = "sim"):
         if dtype != torch.float16:
             raise TypeError("only float16 caches are supported")
+        if semantics not in ("sim", "quest_kernel"):
+            raise ValueError(f"semantics must be 'sim' or 'quest_kernel', got {semantics!r}")
+        self.semantics = semantics
         self.num_layers = num_layers
         self.num_heads = num_heads
         self.num_kv_heads = num_kv_heads or num_heads
@@ -85,7 +95,15 @@ class InferenceController:
         self._page_budget = page_budget
 
     @property
+    def quest_kernel(self) -> bool:
+        return self.semantics == "quest_kernel"
+
+    @property
     def flags(self) -> int:
+        """Selection flags of the scoring / top-k / decode calls (``fixed``
+        applies to the simulation's convention only)."""
+        if self.quest_kernel:
+            return ops.FLAG_QUEST_KERNEL | (ops.FLAG_VALUE_AWARE if self.value_aware else 0)
         return ((ops.FLAG_VALUE_AWARE if self.value_aware else 0) |
                 (ops.FLAG_FIXED if self.fixed else 0))
 
@@ -115,7 +133,8 @@ class InferenceController:
             P = len(kv)
             self.inference_page_budget = min(self._page_budget, P)
             k = self.num_selected_pages()
-            self.topk_dindices_buffer = self._sel[:, :, :k]
+            # quest_kernel: the rows hold the pages chosen besides the last
+            self.topk_dindices_buffer = self._sel[:, :, :k - 1 if self.quest_kernel else k]
 
     def end_forward(self):
         pass
@@ -127,9 +146,13 @@ class InferenceController:
         return len(self.kv_cache.indicies) > self.inference_page_budget
 
     def num_selected_pages(self) -> int:
-        """k of the simulation's rule (filter_util.py:373)."""
+        """Pages attended per kv head: the simulation's k (filter_util.py:373)
+        or, with the quest_kernel convention, min(page_budget, P) including
+        the last page (controller.py:118)."""
         L = self.kv_cache.seqlen
         P = len(self.kv_cache.indicies)
+        if self.quest_kernel:
+            return min(max(1, self._page_budget), P)
         return min(max(3, min(L, self.token_budget) // self.page_size), P)
 
     def clean_states(self):

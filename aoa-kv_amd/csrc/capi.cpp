@@ -52,6 +52,24 @@ int check_shape(uint32_t head_dim, uint32_t page_size, uint32_t layout, uint32_t
   return AOAKV_OK;
 }
 
+// Selection flags a scoring / top-k / decode entry point accepts.
+constexpr uint32_t kSelectFlags =
+    AOAKV_FLAG_VALUE_AWARE | AOAKV_FLAG_FIXED | AOAKV_FLAG_QUEST_KERNEL;
+
+int check_flags(uint32_t flags, uint32_t allowed, const char* fn) {
+  if (flags & ~allowed) return fail(AOAKV_ERR_INVALID, "%s: unknown flags 0x%x", fn, flags);
+  if ((flags & AOAKV_FLAG_FIXED) && (flags & AOAKV_FLAG_QUEST_KERNEL))
+    return fail(AOAKV_ERR_INVALID,
+                "%s: AOAKV_FLAG_FIXED does not apply to AOAKV_FLAG_QUEST_KERNEL (the last page "
+                "is always attended, no page is forced into the selection)",
+                fn);
+  return AOAKV_OK;
+}
+
+// Smallest selection row: the simulation's k is at least 3; the
+// quest_kernel convention selects k - 1 >= 0 pages besides the last.
+uint32_t min_sel_stride(uint32_t flags) { return (flags & AOAKV_FLAG_QUEST_KERNEL) ? 1u : 3u; }
+
 int check_group(uint32_t hq, uint32_t hkv) {
   if (hkv == 0u || hq % hkv != 0u)
     return fail(AOAKV_ERR_INVALID, "num_qo_heads %u not a multiple of num_kv_heads %u", hq, hkv);
@@ -132,7 +150,7 @@ int launch_estimate_topk(aoakv::EstimateArgs ea, const Workspace& w, int32_t* se
   ta.sel_stride = sel_stride;
   ta.Hkv = ea.Hkv;
   ta.S = page_size;
-  ta.flags = flags;
+  ta.flags = flags & kSelectFlags;
   return hip_status(aoakv::launch_topk(ta, batch_size, s), "topk");
 }
 
@@ -227,13 +245,16 @@ static int fill_estimate(aoakv::EstimateArgs& a, const void* q, float* scores,
   REQUIRE(q && scores && metadata_data && metadata_indptr && metadata_indices && kv_indptr &&
               kv_indices && kv_last_page_len,
           "estimate_attn_score: null pointer argument");
-  REQUIRE(!(flags & AOAKV_FLAG_VALUE_AWARE) || v_log_norm,
-          "estimate_attn_score: value-aware scoring needs v_log_norm");
   REQUIRE(batch_size >= 1u && batch_size <= 65535u, "estimate_attn_score: bad batch_size %u",
           batch_size);
-  REQUIRE(max_pages >= 1u && score_stride >= max_pages,
-          "estimate_attn_score: score_stride %u < max_pages %u", score_stride, max_pages);
-  REQUIRE((flags & ~7u) == 0u, "estimate_attn_score: unknown flags 0x%x", flags);
+  if (int e = check_flags(flags, kSelectFlags | AOAKV_FLAG_SINGLE_LAUNCH, "estimate_attn_score"))
+    return e;
+  // the quest_kernel convention leaves the last page unscored
+  const uint32_t row = (flags & AOAKV_FLAG_QUEST_KERNEL) ? max_pages - 1u : max_pages;
+  REQUIRE(max_pages >= 1u && score_stride >= row && score_stride >= 1u,
+          "estimate_attn_score: score_stride %u < %u scores per row", score_stride, row);
+  REQUIRE(!(flags & AOAKV_FLAG_VALUE_AWARE) || v_log_norm,
+          "estimate_attn_score: value-aware scoring needs v_log_norm");
   a.q = static_cast<const aoakv::f16*>(q);
   a.scores = scores;
   a.score_stride = score_stride;
@@ -285,8 +306,9 @@ int aoakv_topk_filtering(const float* scores, uint32_t score_stride,
   REQUIRE(batch_size >= 1u && batch_size <= 65535u && num_kv_heads >= 1u &&
               num_kv_heads <= 65535u,
           "topk_filtering: bad batch_size %u / num_kv_heads %u", batch_size, num_kv_heads);
-  REQUIRE(sel_stride >= 3u, "topk_filtering: sel_stride %u < 3", sel_stride);
-  REQUIRE((flags & ~3u) == 0u, "topk_filtering: unknown flags 0x%x", flags);
+  if (int e = check_flags(flags, kSelectFlags, "topk_filtering")) return e;
+  REQUIRE(sel_stride >= min_sel_stride(flags), "topk_filtering: sel_stride %u < %u", sel_stride,
+          min_sel_stride(flags));
   aoakv::TopkArgs a{};
   a.scores = scores;
   a.score_stride = score_stride;
@@ -327,7 +349,7 @@ static int fill_decode(aoakv::DecodeArgs& a, Workspace& w, const void* q, void* 
                        const int32_t* token_budgets, void* workspace, size_t workspace_bytes,
                        uint32_t batch_size, uint32_t max_pages, uint32_t num_qo_heads,
                        uint32_t num_kv_heads, uint32_t head_dim, uint32_t page_size,
-                       uint32_t layout) {
+                       uint32_t layout, uint32_t flags) {
   if (int e = check_shape(head_dim, page_size, layout, num_qo_heads)) return e;
   if (int e = check_group(num_qo_heads, num_kv_heads)) return e;
   REQUIRE(q && o && kv_data && kv_indptr && kv_indices && kv_last_page_len && workspace,
@@ -335,8 +357,13 @@ static int fill_decode(aoakv::DecodeArgs& a, Workspace& w, const void* q, void* 
   REQUIRE(batch_size >= 1u && batch_size <= 65535u, "decode_sparse_attn: bad batch_size %u",
           batch_size);
   REQUIRE(max_pages >= 1u, "decode_sparse_attn: max_pages must be >= 1");
-  const uint32_t max_sel = sel_pages ? (sel_stride < max_pages ? sel_stride : max_pages) : max_pages;
-  REQUIRE(!sel_pages || sel_stride >= 3u, "decode_sparse_attn: sel_stride %u < 3", sel_stride);
+  const bool quest = (flags & AOAKV_FLAG_QUEST_KERNEL) != 0u;
+  // pages attended per head: the selection row (plus the last page with the
+  // quest_kernel convention), at most every page
+  const uint32_t row = sel_stride + (quest ? 1u : 0u);
+  const uint32_t max_sel = sel_pages ? (row < max_pages ? row : max_pages) : max_pages;
+  REQUIRE(!sel_pages || sel_stride >= min_sel_stride(flags), "decode_sparse_attn: sel_stride %u < %u",
+          sel_stride, min_sel_stride(flags));
   REQUIRE(aoakv::decode_chunks(max_sel) <= aoakv::decode_max_chunks(),
           "decode_sparse_attn: %u pages per head exceed the %u the split-K merge holds", max_sel,
           aoakv::decode_max_chunks() * 8u);
@@ -359,6 +386,7 @@ static int fill_decode(aoakv::DecodeArgs& a, Workspace& w, const void* q, void* 
   a.Hkv = num_kv_heads;
   a.S = page_size;
   a.max_chunks = aoakv::decode_chunks(max_sel);
+  a.flags = flags & AOAKV_FLAG_QUEST_KERNEL;
   a.g = aoakv::make_geom(layout, num_kv_heads, page_size, head_dim);
   return AOAKV_OK;
 }
@@ -370,13 +398,14 @@ int aoakv_decode_sparse_attn(const void* q, void* o, const void* kv_data,
                              const int32_t* token_budgets, void* workspace,
                              size_t workspace_bytes, uint32_t batch_size, uint32_t max_pages,
                              uint32_t num_qo_heads, uint32_t num_kv_heads, uint32_t head_dim,
-                             uint32_t page_size, uint32_t layout, void* stream) {
+                             uint32_t page_size, uint32_t layout, uint32_t flags, void* stream) {
+  if (int e = check_flags(flags, AOAKV_FLAG_QUEST_KERNEL, "decode_sparse_attn")) return e;
   aoakv::DecodeArgs a{};
   Workspace w{};
   if (int e = fill_decode(a, w, q, o, kv_data, kv_indptr, kv_indices, kv_last_page_len,
                           sel_pages, sel_stride, token_budget, token_budgets, workspace,
                           workspace_bytes, batch_size, max_pages, num_qo_heads, num_kv_heads,
-                          head_dim, page_size, layout))
+                          head_dim, page_size, layout, flags))
     return e;
   return hip_status(aoakv::launch_decode(a, batch_size, static_cast<hipStream_t>(stream)),
                     "decode_sparse_attn");
@@ -402,15 +431,17 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
                             v_log_norm, batch_size, max_pages, num_qo_heads, num_kv_heads,
                             head_dim, page_size, layout, flags))
     return e;
+  REQUIRE(sel_stride >= min_sel_stride(flags), "sparse_decode_layer: sel_stride %u < %u",
+          sel_stride, min_sel_stride(flags));
   aoakv::DecodeArgs da{};
   Workspace w{};
   if (int e = fill_decode(da, w, q, o, kv_data, kv_indptr, kv_indices, kv_last_page_len,
                           sel_pages, sel_stride, token_budget, token_budgets, workspace,
                           workspace_bytes, batch_size, max_pages, num_qo_heads, num_kv_heads,
-                          head_dim, page_size, layout))
+                          head_dim, page_size, layout, flags))
     return e;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  ea.flags &= 3u;
+  ea.flags &= kSelectFlags;
   if ((flags & AOAKV_FLAG_SINGLE_LAUNCH) && max_pages <= aoakv::fused_topk_max_pages()) {
     // one launch: scoring, top-k and decode items of every head
     aoakv::LayerArgs la{};
@@ -453,7 +484,8 @@ int aoakv_estimate_topk(const void* q, const void* metadata_data, const int32_t*
   REQUIRE(sel_pages && workspace, "estimate_topk: sel_pages and workspace are required");
   REQUIRE(max_pages <= aoakv::topk_max_pages(), "estimate_topk: max_pages %u > %u", max_pages,
           aoakv::topk_max_pages());
-  REQUIRE(sel_stride >= 3u, "estimate_topk: sel_stride %u < 3", sel_stride);
+  REQUIRE(sel_stride >= min_sel_stride(flags), "estimate_topk: sel_stride %u < %u", sel_stride,
+          min_sel_stride(flags));
   aoakv::EstimateArgs ea{};
   if (int e = fill_estimate(ea, q, scores, score_stride, metadata_data, metadata_indptr,
                             metadata_indices, kv_indptr, kv_indices, kv_last_page_len,

@@ -170,6 +170,7 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = __lane_id();
   const uint32_t wave = tid / kWave;
+  if (k == 0u) return;  // (quest_kernel convention with a budget of one page)
   if (k >= P) {  // everything selected
     for (uint32_t i = tid; i < P; i += kThreads) put(i, kv_ids[i]);
     return;
@@ -255,7 +256,7 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
       if (is_free(i)) free_mask |= (Mask)1 << j;
     }
   }
-  // >= 1 because k >= 3 whenever k < P
+  // >= 1: k == 0 returned above, and with fixed forcing k >= 3 > nforced
   const RadixResult rr = radix_select<KPT, Mask>(rel, free_mask, kmax - kmin, k - nforced, sh);
 
   // selection classes at the final resolution:
@@ -347,7 +348,10 @@ struct EstTopkShared {
 __device__ inline uint32_t est_pages(const EstimateArgs& a, uint32_t b, uint32_t* pbeg_out) {
   const uint32_t pbeg = (uint32_t)a.kv_indptr[b];
   uint32_t P = (uint32_t)a.kv_indptr[b + 1] - pbeg;
-  if (P > a.score_stride) P = a.score_stride;
+  // a score row holds a score per page, or per page but the last with the
+  // quest_kernel convention (the last page is not scored)
+  const uint32_t rowcap = a.score_stride + ((a.flags & kFlagQuestKernel) ? 1u : 0u);
+  if (P > rowcap) P = rowcap;
   if (P > a.max_pages) P = a.max_pages;
   if (P > kFusedTopkMaxPages && a.sel != nullptr) P = kFusedTopkMaxPages;
   *pbeg_out = pbeg;
@@ -370,7 +374,7 @@ __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, ui
   if (chunk * kEstPagesPerBlock >= P) return false;  // uniform per block
   const uint32_t mbeg = (uint32_t)a.meta_indptr[b];
   const uint32_t d0 = l16 * kVec;
-  const bool value_aware = (a.flags & 1u) != 0u;
+  const bool value_aware = (a.flags & kFlagValueAware) != 0u;
 
   // Every load below is unconditional, with an address that always lies in
   // the sequence's pages: a page past P reads a page of this block (its
@@ -459,7 +463,9 @@ __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, ui
   float* out = a.scores + ((size_t)b * a.Hkv + h) * a.score_stride;
   {
     const uint32_t p = chunk * kEstPagesPerBlock + threadIdx.x;
-    if (threadIdx.x < (uint32_t)kEstPagesPerBlock && p < P) st_agent(out + p, s_sc[threadIdx.x]);
+    const uint32_t nstore = (a.flags & kFlagQuestKernel) ? P - 1u : P;
+    if (threadIdx.x < (uint32_t)kEstPagesPerBlock && p < nstore)
+      st_agent(out + p, s_sc[threadIdx.x]);
   }
 
   return true;
@@ -471,16 +477,21 @@ template <int GROUP>
 __device__ __forceinline__ void select_item(const EstimateArgs& a, uint32_t b, uint32_t h,
                                             uint32_t lpl, uint32_t budget, TopkShared& tk) {
   uint32_t pbeg;
-  const uint32_t P = est_pages(a, b, &pbeg);
-  uint32_t k = num_selected_pages((P - 1u) * kPageSize + lpl, budget, kPageSize, P);
+  uint32_t P = est_pages(a, b, &pbeg);
+  uint32_t k = num_selected_pages((P - 1u) * kPageSize + lpl, budget, kPageSize, P, a.flags);
+  if (a.flags & kFlagQuestKernel) {
+    // the last page is attended without selection: k - 1 of the others
+    P -= 1u;
+    k -= 1u;
+  }
   if (k > a.sel_stride) k = a.sel_stride;  // never write past a selection row
   // no handoff entries for a sequence the decode items skip (malformed
   // last-page length): nothing would read and clear them
   const bool handoff = a.hsel != nullptr && lpl >= 1u && lpl <= (uint32_t)kPageSize;
   uint32_t* hout = handoff ? a.hsel + ((size_t)b * a.Hq + h * GROUP) * a.hsel_stride : nullptr;
-  topk_staged(a.scores + ((size_t)b * a.Hkv + h) * a.score_stride, P, k, (a.flags & 2u) != 0u,
-              a.kv_indices + pbeg, a.sel + ((size_t)b * a.Hkv + h) * a.sel_stride, tk, hout,
-              a.hsel_stride, GROUP);
+  topk_staged(a.scores + ((size_t)b * a.Hkv + h) * a.score_stride, P, k,
+              (a.flags & kFlagFixed) != 0u, a.kv_indices + pbeg,
+              a.sel + ((size_t)b * a.Hkv + h) * a.sel_stride, tk, hout, a.hsel_stride, GROUP);
 }
 
 // Scores one chunk; with a.sel set, the last block of the head to finish
@@ -520,19 +531,26 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopkArgs a) {
   const uint32_t pbeg = (uint32_t)a.kv_indptr[b];
   uint32_t P = (uint32_t)a.kv_indptr[b + 1] - pbeg;
   if (P == 0u) return;
-  if (P > a.score_stride) P = a.score_stride;
+  const bool quest = (a.flags & kFlagQuestKernel) != 0u;
+  const uint32_t rowcap = a.score_stride + (quest ? 1u : 0u);  // see est_pages
+  if (P > rowcap) P = rowcap;
   if (P > kTopkMaxPages) P = kTopkMaxPages;
   const uint32_t L = (P - 1u) * a.S + (uint32_t)a.kv_last_page_len[b];
   const uint32_t budget = a.token_budgets ? (uint32_t)a.token_budgets[b] : a.token_budget;
-  uint32_t k = num_selected_pages(L, budget, a.S, P);
+  uint32_t k = num_selected_pages(L, budget, a.S, P, a.flags);
+  if (quest) {  // the last page is attended without selection
+    P -= 1u;
+    k -= 1u;
+  }
   if (k > a.sel_stride) k = a.sel_stride;
+  const bool fixed = (a.flags & kFlagFixed) != 0u;
   const float* row = a.scores + ((size_t)b * a.Hkv + h) * a.score_stride;
   int32_t* out = a.sel + ((size_t)b * a.Hkv + h) * a.sel_stride;
   if (P <= kStageMaxPages)
-    topk_staged(row, P, k, (a.flags & 2u) != 0u, a.kv_indices + pbeg, out, sh);
+    topk_staged(row, P, k, fixed, a.kv_indices + pbeg, out, sh);
   else
-    topk_block<kTopkMaxPages / kThreads>(row, P, k, (a.flags & 2u) != 0u, a.kv_indices + pbeg,
-                                          out, sh, nullptr, 0u, 0u);
+    topk_block<kTopkMaxPages / kThreads>(row, P, k, fixed, a.kv_indices + pbeg, out, sh, nullptr,
+                                          0u, 0u);
 }
 
 // ======================================================================
@@ -581,7 +599,10 @@ __device__ inline uint32_t to_word(float x) {
 //     written; partials go to handoff words and the head's last chunk
 //     polls them and merges.  Every block only waits on blocks with smaller
 //     indices, which were dispatched before it.
-template <bool HANDOFF>
+// QUEST (quest_kernel convention): the selection rows hold the pages chosen
+// besides the last page, which is always attended as the final entry
+// (quest/utils/__init__.py:237, approx_attn.cu:68-151).
+template <bool HANDOFF, bool QUEST>
 __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uint32_t hq,
                                             uint32_t chunk, DecShared& sm) {
   float (*s_o)[kHeadDim] = sm.o;
@@ -622,10 +643,15 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   const H8 qq = ld16(a.q + bh * kHeadDim + d0);
   __builtin_amdgcn_sched_barrier(0);  // keep the issue order written here
   if (P == 0u || lpl == 0u || lpl > S) return;  // malformed page table
+  // physical id of the sequence's last page (the one holding lpl tokens)
+  uint32_t last_phys = 0u;
+  if constexpr (QUEST) last_phys = (uint32_t)a.kv_indices[pbeg + P - 1u];
   uint32_t npages = P;
   if (a.sel != nullptr) {
-    npages = num_selected_pages((P - 1u) * S + lpl, budget, S, P);
-    if (npages > a.sel_stride) npages = a.sel_stride;
+    npages = num_selected_pages((P - 1u) * S + lpl, budget, S, P,
+                                QUEST ? kFlagQuestKernel : 0u);
+    const uint32_t row_cap = a.sel_stride + (QUEST ? 1u : 0u);
+    if (npages > row_cap) npages = row_cap;
   }
   // the grid holds max_chunks blocks per head; never index partials past it
   const uint32_t cap =
@@ -633,15 +659,18 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   if (npages > cap * kDecPagesPerBlock) npages = cap * kDecPagesPerBlock;
   const uint32_t nch = (npages + kDecPagesPerBlock - 1) / kDecPagesPerBlock;
   if (chunk >= nch) return;  // uniform per block
+  // entries [0, nsel) come from the selection; with QUEST the entry after
+  // them is the last page
+  const uint32_t nsel = (QUEST && a.sel != nullptr) ? npages - 1u : npages;
   if (HANDOFF) {
     // this chunk's entries of the head's selection, each polled until the
     // top-k of this launch has written it, then cleared for the next launch
     uint32_t* hrow = a.hsel + bh * a.hsel_stride;
     const uint32_t e = ich + threadIdx.x;
     if (threadIdx.x < (uint32_t)kDecPagesPerBlock)
-      sm.sel[threadIdx.x] = e < npages ? wait_word(hrow + e, a.error) : 0u;
+      sm.sel[threadIdx.x] = e < nsel ? wait_word(hrow + e, a.error) : 0u;
     __syncthreads();
-    if (threadIdx.x < (uint32_t)kDecPagesPerBlock && e < npages) st_agent_u32(hrow + e, 0u);
+    if (threadIdx.x < (uint32_t)kDecPagesPerBlock && e < nsel) st_agent_u32(hrow + e, 0u);
     sel_ch = sm.sel[0];
 #pragma unroll
     for (int s = 0; s < kDecPagesPerWave; ++s) selv[s] = sm.sel[wave * kDecPagesPerWave + s];
@@ -656,6 +685,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
     live[s] = idx0 + s < npages;
     if (a.sel != nullptr) {
       phys[s] = live[s] ? selv[s] : sel_ch;
+      if (QUEST && idx0 + s >= nsel) phys[s] = last_phys;
     } else {
       const uint32_t i = live[s] ? idx0 + s : ich;
       phys[s] = (uint32_t)a.kv_indices[pbeg + i];
@@ -679,7 +709,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
 #pragma unroll
   for (int j = 0; j < kVec; ++j) qf[j] = (float)qq.v[j];
   // tokens per page: the sequence's last page holds lpl of them
-  const uint32_t last_phys = (uint32_t)a.kv_indices[pbeg + P - 1u];
+  if constexpr (!QUEST) last_phys = (uint32_t)a.kv_indices[pbeg + P - 1u];
   uint32_t ntok[kDecPagesPerWave];
 #pragma unroll
   for (int s = 0; s < kDecPagesPerWave; ++s)
@@ -862,9 +892,10 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   }
 }
 
+template <bool QUEST>
 __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
   __shared__ DecShared sm;
-  decode_item<false>(a, blockIdx.z, blockIdx.y, blockIdx.x, sm);
+  decode_item<false, QUEST>(a, blockIdx.z, blockIdx.y, blockIdx.x, sm);
 }
 
 // ======================================================================
@@ -889,7 +920,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
 // and handoff words are cleared by their readers, so the workspace is zero
 // again for the next launch.  No counter is shared by all workgroups
 // (same-address device atomics serialize at ~12 ns each).
-template <int GROUP>
+template <int GROUP, bool QUEST>
 __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
   __shared__ union {
     EstTopkShared e;
@@ -940,7 +971,7 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
     const uint32_t u = t - la.n_workers - la.n_heads;
     const uint32_t bh = u / la.d.max_chunks, chunk = u % la.d.max_chunks;
     const uint32_t b = bh / la.d.Hq, hq = bh % la.d.Hq;
-    decode_item<true>(la.d, b, hq, chunk, sm.d);
+    decode_item<true, QUEST>(la.d, b, hq, chunk, sm.d);
   }
 }
 
@@ -973,11 +1004,18 @@ hipError_t launch_estimate(const EstimateArgs& a, uint32_t batch, uint32_t max_p
 
 hipError_t launch_layer(const LayerArgs& la, hipStream_t s) {
   const uint32_t grid = la.n_workers + la.n_heads + la.n_dec;
+  const bool quest = (la.e.flags & kFlagQuestKernel) != 0u;
   switch (la.e.Hq / la.e.Hkv) {
-    case 1: hipLaunchKernelGGL(layer_kernel<1>, dim3(grid), dim3(kThreads), 0, s, la); break;
-    case 2: hipLaunchKernelGGL(layer_kernel<2>, dim3(grid), dim3(kThreads), 0, s, la); break;
-    case 4: hipLaunchKernelGGL(layer_kernel<4>, dim3(grid), dim3(kThreads), 0, s, la); break;
-    case 8: hipLaunchKernelGGL(layer_kernel<8>, dim3(grid), dim3(kThreads), 0, s, la); break;
+#define AOAKV_LAYER(G)                                                                       \
+  case G:                                                                                    \
+    if (quest) hipLaunchKernelGGL((layer_kernel<G, true>), dim3(grid), dim3(kThreads), 0, s, la); \
+    else hipLaunchKernelGGL((layer_kernel<G, false>), dim3(grid), dim3(kThreads), 0, s, la);      \
+    break;
+    AOAKV_LAYER(1)
+    AOAKV_LAYER(2)
+    AOAKV_LAYER(4)
+    AOAKV_LAYER(8)
+#undef AOAKV_LAYER
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -994,7 +1032,8 @@ hipError_t launch_topk(const TopkArgs& a, uint32_t batch, hipStream_t s) {
 
 hipError_t launch_decode(const DecodeArgs& a, uint32_t batch, hipStream_t s) {
   dim3 grid(a.max_chunks, a.Hq, batch);
-  hipLaunchKernelGGL(decode_kernel, grid, dim3(kThreads), 0, s, a);
+  if (a.flags & kFlagQuestKernel) hipLaunchKernelGGL(decode_kernel<true>, grid, dim3(kThreads), 0, s, a);
+  else hipLaunchKernelGGL(decode_kernel<false>, grid, dim3(kThreads), 0, s, a);
   return hipGetLastError();
 }
 

@@ -208,13 +208,29 @@ __device__ inline uint32_t order_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// k = min(max(3, min(L, budget) / page_size), P)  (filter_util.py:373,
-// quest_attention.py:326).
+// Selection flags (the bits of the C ABI's AOAKV_FLAG_*).
+constexpr uint32_t kFlagValueAware = 1u;
+constexpr uint32_t kFlagFixed = 2u;
+constexpr uint32_t kFlagQuestKernel = 8u;
+
+// Pages attended per (sequence, kv head).
+//   simulation:   k = min(max(3, min(L, budget) / page_size), P)
+//                 (filter_util.py:373, quest_attention.py:326)
+//   quest_kernel: k = min(max(1, budget / page_size), P): the last page plus
+//                 k - 1 pages selected from the others (controller.py:118,
+//                 quest/utils/__init__.py:237)
 __host__ __device__ inline uint32_t num_selected_pages(uint32_t L, uint32_t budget,
-                                                       uint32_t page_size, uint32_t P) {
-  uint32_t tb = L < budget ? L : budget;
-  uint32_t k = tb / page_size;
-  if (k < 3u) k = 3u;
+                                                       uint32_t page_size, uint32_t P,
+                                                       uint32_t flags) {
+  uint32_t k;
+  if (flags & kFlagQuestKernel) {
+    k = budget / page_size;
+    if (k < 1u) k = 1u;
+  } else {
+    const uint32_t tb = L < budget ? L : budget;
+    k = tb / page_size;
+    if (k < 3u) k = 3u;
+  }
   return k < P ? k : P;
 }
 

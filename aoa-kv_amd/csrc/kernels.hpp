@@ -92,6 +92,7 @@ struct DecodeArgs {
   float* partial;      // [B*Hq, max_chunks, kPartialStride]
   uint32_t* counters;  // [B*Hq]
   uint32_t Hq, Hkv, S, max_chunks;
+  uint32_t flags;      // kFlagQuestKernel: the quest_kernel selection convention
   PageGeom g;
   // single launch only: handoff buffers whose words hold value + 1 (0 = not
   // yet written); every word is cleared again by its reader

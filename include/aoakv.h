@@ -39,6 +39,8 @@
  *     quest_attention.py:196-382): every page, including the partial last
  *     one, is scored; fixed selection forces the first and last page;
  *     k = min(max(3, min(L, budget) / page_size), P); scores are fp32.
+ *     AOAKV_FLAG_QUEST_KERNEL selects the reference kernel's convention
+ *     instead (see there).
  *   - Every call is asynchronous on `stream` (a hipStream_t), allocates no
  *     device memory and performs no host synchronisation.
  *   - Return value: 0 on success, otherwise an AOAKV_ERR_* code;
@@ -68,8 +70,19 @@ extern "C" {
 #define AOAKV_FLAG_VALUE_AWARE 1u /* AOA-KV score (else plain Quest bound)   */
 #define AOAKV_FLAG_FIXED 2u       /* force first and last page (sim `fixed`) */
 /* aoakv_sparse_decode_layer only: run scoring, top-k and decode in ONE launch
- * (ticketed work items, per-head ready flags) instead of two launches. */
+ * (scoring workers, per-head top-k and decode items handing over through
+ * the workspace) instead of two launches. */
 #define AOAKV_FLAG_SINGLE_LAUNCH 4u
+/* The reference KERNEL's selection convention instead of the simulation's
+ * (controller.py:113-124, quest/utils/__init__.py:196-246,
+ * decode_attn.cuh:297-306): the last page is not scored and is always
+ * attended; k = min(max(1, budget / page_size), P) pages are attended, the
+ * last one plus the k - 1 best of the others.  Score rows then hold P - 1
+ * entries and selection rows the k - 1 chosen pages (the reference's
+ * [H, page_budget - 1] top-k output); the decode adds the last page itself.
+ * Not combinable with AOAKV_FLAG_FIXED.  The value statistic is still read
+ * at the page's own physical index. */
+#define AOAKV_FLAG_QUEST_KERNEL 8u
 
 /* Thread-local description of the last failure ("" when none). */
 const char* aoakv_last_error(void);
@@ -125,7 +138,8 @@ int aoakv_append_kv_cache_decode(const void* k, const void* v, uint32_t batch_si
  *   plain Quest: bound [summed over a GQA group]
  *
  * q: [B, num_qo_heads, head_dim] fp16.  scores: [B, num_kv_heads,
- * score_stride] fp32, entry p < P_b written.  max_pages >= every P_b.
+ * score_stride] fp32, entry p < P_b written (p < P_b - 1 with
+ * AOAKV_FLAG_QUEST_KERNEL).  max_pages >= every P_b.
  */
 int aoakv_estimate_attn_score(const void* q, float* scores, uint32_t score_stride,
                               const void* metadata_data, const int32_t* metadata_indptr,
@@ -146,7 +160,9 @@ int aoakv_estimate_attn_score(const void* q, float* scores, uint32_t score_strid
  * towards the lower page index.  Output: sel_pages[B, num_kv_heads,
  * sel_stride] int32 PHYSICAL page ids (kv_indices entries) of the selected
  * pages in ascending logical order; entries >= k_b untouched.
- * sel_stride >= max_b k_b.  Supports P_b <= 16384.
+ * sel_stride >= max_b k_b.  Supports P_b <= 16384.  With
+ * AOAKV_FLAG_QUEST_KERNEL: k_b - 1 pages chosen among the first P_b - 1
+ * (score rows of P_b - 1 entries), the last page not written.
  */
 int aoakv_topk_filtering(const float* scores, uint32_t score_stride,
                          const int32_t* kv_indptr, const int32_t* kv_indices,
@@ -181,7 +197,10 @@ int aoakv_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
  * q, o: [B, num_qo_heads, head_dim] fp16.  sel_pages as written by
  * aoakv_topk_filtering (physical ids, per kv head, sel_stride); the number
  * of pages per (b, head) is recomputed from the same k rule.  sel_pages ==
- * NULL attends every page (dense decode).
+ * NULL attends every page (dense decode).  flags: AOAKV_FLAG_QUEST_KERNEL
+ * (the rows hold the k - 1 pages besides the last page, which is attended
+ * as well, as BatchDecodeWithPagedKVCacheKernel does with kv_last_page_idx)
+ * or 0.
  */
 int aoakv_decode_sparse_attn(const void* q, void* o, const void* kv_data,
                              const int32_t* kv_indptr, const int32_t* kv_indices,
@@ -190,7 +209,7 @@ int aoakv_decode_sparse_attn(const void* q, void* o, const void* kv_data,
                              const int32_t* token_budgets, void* workspace,
                              size_t workspace_bytes, uint32_t batch_size, uint32_t max_pages,
                              uint32_t num_qo_heads, uint32_t num_kv_heads, uint32_t head_dim,
-                             uint32_t page_size, uint32_t layout, void* stream);
+                             uint32_t page_size, uint32_t layout, uint32_t flags, void* stream);
 
 /*
  * One decode layer: estimate + top-k (fused, last-arriving workgroup per

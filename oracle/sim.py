@@ -270,6 +270,23 @@ def topk_pages(scores: np.ndarray, k: int, fixed_selection: bool) -> np.ndarray:
     return np.sort(order, axis=-1)
 
 
+def quest_kernel_pages(scores: np.ndarray, page_budget: int) -> np.ndarray:
+    """The reference KERNEL's selection convention (``controller.py:113-124``,
+    ``quest/utils/__init__.py:196-246``, ``decode_attn.cuh:297-306``; the
+    reference's own test of it is ``quest/tests/test_approx_attention.py:38-93``):
+    the last page is not scored and is always attended; with
+    ``k = min(max(1, page_budget), P)`` the k - 1 best of the other pages are
+    selected (ties towards the lower page index) and the last page added.
+
+    scores (..., P) fp32, entry P-1 ignored -> (..., k) int64, ascending."""
+    P = scores.shape[-1]
+    k = min(max(1, page_budget), P)
+    head = scores[..., :P - 1].astype(np.float64)
+    order = np.argsort(-head, axis=-1, kind="stable")[..., :k - 1]
+    last = np.full(order.shape[:-1] + (1,), P - 1, dtype=order.dtype)
+    return np.sort(np.concatenate([order, last], axis=-1), axis=-1)
+
+
 def local_heavy_hitter_mask_value_aware_group_consistent_sum(
         attn_weights, token_budget, chunk_size, value_states_page_mean,
         num_key_value_groups, head_dim, fixed_selection=False,
@@ -378,9 +395,15 @@ class SimLayerState:
 
 def select_pages(state: SimLayerState, q: np.ndarray, token_budget: int,
                  fixed: bool = True, value_aware: bool = True,
-                 num_key_value_groups: int = 1):
+                 num_key_value_groups: int = 1, semantics: str = "sim"):
     """Scoring and selection of one decode step (``quest_attention.py:296-332``).
+
+    ``semantics="quest_kernel"`` keeps the same page scores but selects by
+    the reference kernel's convention (``quest_kernel_pages`` with a page
+    budget of ``token_budget // page_size``; ``fixed`` does not apply).
     Returns (scores (1, nkvh, 1, P) fp32, pages (1, nkvh, 1, k) int64)."""
+    if semantics not in ("sim", "quest_kernel"):
+        raise ValueError(f"unknown semantics {semantics!r}")
     L = state.kv_len
     P = math.ceil(L / state.chunk_size)
     w = compute_attn_weights_for_selection(q, state.page_filters, num_key_value_groups,
@@ -393,18 +416,20 @@ def select_pages(state: SimLayerState, q: np.ndarray, token_budget: int,
     else:
         _, scores, pages = local_heavy_hitter_mask_group_consistent_sum(
             w, tb, state.chunk_size, num_key_value_groups, fixed, return_pages=True)
+    if semantics == "quest_kernel":
+        pages = quest_kernel_pages(scores, token_budget // state.chunk_size)
     return scores, pages
 
 
 def decode_step(state: SimLayerState, q: np.ndarray, k_new: np.ndarray, v_new: np.ndarray,
                 token_budget: int, fixed: bool = True, value_aware: bool = True,
-                num_key_value_groups: int = 1):
+                num_key_value_groups: int = 1, semantics: str = "sim"):
     """One value-aware decode step of one layer (``quest_attention.py:249-356``):
     metadata append, page scores, top-k mask, masked attention.
     Returns (o (1, nh, 1, d) fp16, scores, pages)."""
     state.append(k_new, v_new)
     scores, pages = select_pages(state, q, token_budget, fixed, value_aware,
-                                 num_key_value_groups)
+                                 num_key_value_groups, semantics)
     mask = pages_to_token_mask(pages, state.chunk_size, state.kv_len)
     mask = np.repeat(mask, num_key_value_groups, axis=1)
     K = np.repeat(state.K, num_key_value_groups, axis=1)
@@ -445,7 +470,8 @@ def causal_prefill_rows(q: np.ndarray, k: np.ndarray, v: np.ndarray,
 
 
 def selection_matches(sel: np.ndarray, sel_ref: np.ndarray, scores: np.ndarray,
-                      fixed: bool = False, rel_tol: float = 1e-3) -> Tuple[bool, str]:
+                      fixed: bool = False, rel_tol: float = 1e-3,
+                      forced: Optional[set] = None) -> Tuple[bool, str]:
     """Tie-aware comparison of a selected page set with the reference's, for
     one head.
 
@@ -453,7 +479,9 @@ def selection_matches(sel: np.ndarray, sel_ref: np.ndarray, scores: np.ndarray,
     has a reference score within ``rel_tol`` (relative) of the boundary score
     (the smallest score the reference selected, forced pages excluded): the
     sets then differ only among near-ties at the selection boundary.
-    ``scores`` are the reference page scores before fixed forcing."""
+    ``scores`` are the reference page scores before fixed forcing.
+    ``forced`` names the always-selected pages explicitly (default: pages 0
+    and P-1 when ``fixed``; ``{P-1}`` for the quest_kernel convention)."""
     a = set(int(x) for x in np.ravel(sel))
     b = set(int(x) for x in np.ravel(sel_ref))
     if len(a) != len(b):
@@ -461,7 +489,8 @@ def selection_matches(sel: np.ndarray, sel_ref: np.ndarray, scores: np.ndarray,
     if a == b:
         return True, "exact"
     P = scores.shape[-1]
-    forced = {0, P - 1} if fixed else set()
+    if forced is None:
+        forced = {0, P - 1} if fixed else set()
     if not forced <= a:
         return False, f"forced pages {sorted(forced - a)} missing"
     free = [float(scores[i]) for i in b - forced]

@@ -81,8 +81,30 @@ def test_validation_errors_without_gpu():
     assert rc == _lib.AOAKV_ERR_INVALID and b"v_log_norm" in lib.aoakv_last_error()
     # workspace too small
     rc = lib.aoakv_decode_sparse_attn(1, 1, 1, 1, 1, 1, 1, 128, 2048, nul, 1, 16, 1, 2048, 32,
-                                      32, 128, 16, 1, nul)
+                                      32, 128, 16, 1, 0, nul)
     assert rc == _lib.AOAKV_ERR_INVALID and b"workspace" in lib.aoakv_last_error()
+    # the quest_kernel convention forces no page: FIXED with it is an error
+    qk = _lib.FLAG_QUEST_KERNEL
+    rc = lib.aoakv_estimate_attn_score(1, 1, 64, 1, 1, 1, 1, 1, 1, 1, 1, 64, 32, 32, 128, 16, 1,
+                                       qk | _lib.FLAG_FIXED, nul)
+    assert rc == _lib.AOAKV_ERR_INVALID and b"QUEST_KERNEL" in lib.aoakv_last_error()
+    rc = lib.aoakv_topk_filtering(1, 64, 1, 1, 1, 1024, nul, 1, 64, 1, 32, 16,
+                                  qk | _lib.FLAG_FIXED, nul)
+    assert rc == _lib.AOAKV_ERR_INVALID and b"QUEST_KERNEL" in lib.aoakv_last_error()
+    # unknown flag bits
+    rc = lib.aoakv_topk_filtering(1, 64, 1, 1, 1, 1024, nul, 1, 64, 1, 32, 16, 16, nul)
+    assert rc == _lib.AOAKV_ERR_INVALID and b"unknown flags" in lib.aoakv_last_error()
+    rc = lib.aoakv_decode_sparse_attn(1, 1, 1, 1, 1, 1, 1, 128, 2048, nul, 1, 1 << 30, 1, 2048,
+                                      32, 32, 128, 16, 1, 2, nul)
+    assert rc == _lib.AOAKV_ERR_INVALID and b"unknown flags" in lib.aoakv_last_error()
+    # quest_kernel score rows hold P - 1 entries: stride 63 for 64 pages is
+    # accepted up to the next check (missing v_log_norm), stride 62 is not
+    rc = lib.aoakv_estimate_attn_score(1, 1, 63, 1, 1, 1, 1, 1, 1, nul, 1, 64, 32, 32, 128, 16,
+                                       1, qk | _lib.FLAG_VALUE_AWARE, nul)
+    assert rc == _lib.AOAKV_ERR_INVALID and b"v_log_norm" in lib.aoakv_last_error()
+    rc = lib.aoakv_estimate_attn_score(1, 1, 62, 1, 1, 1, 1, 1, 1, 1, 1, 64, 32, 32, 128, 16, 1,
+                                       qk | _lib.FLAG_VALUE_AWARE, nul)
+    assert rc == _lib.AOAKV_ERR_INVALID and b"score_stride" in lib.aoakv_last_error()
     # prefill attention reports its own status
     rc = lib.aoakv_topk_filtering(nul, 64, 1, 1, 1, 1024, nul, 1, 64, 1, 32, 16, 2, nul)
     assert rc == _lib.AOAKV_ERR_INVALID

@@ -243,3 +243,104 @@ def test_causal_prefill_rows_small_bruteforce():
             p /= p.sum()
             ref = sum(p[j] * v[j, hh].astype(np.float64) for j in range(last + 1))
             np.testing.assert_allclose(out[i, hh], ref, rtol=1e-5, atol=1e-6)
+
+
+# --------------------------------------------------------------------------
+# quest_kernel convention: restated from the reference's own test of the
+# kernel path (quest/tests/test_approx_attention.py:17-110), which builds the
+# expected selection from raw keys with the sign trick, not from the page
+# metadata the oracle uses.
+# --------------------------------------------------------------------------
+
+def _reference_kernel_convention(q, K, V, page_size, page_budget):
+    """test_approx_attention.py:38-110 in numpy: plain-Quest page bound from
+    sign(q)*k page maxima (padding with fp16 min), the last page removed,
+    top (page_budget - 1), the last page appended; dense when the sequence
+    has no more pages than the budget.  q (h, d), K/V (h, L, d) fp16.
+    Returns (selected page sets per head or None, o (h, d) float64, the
+    page bounds of the first P - 1 pages (h, P - 1) or None)."""
+    h, L, d = K.shape
+    qf = q.astype(np.float64)
+    s = np.einsum("hd,hld->hl", qf, K.astype(np.float64))
+    s = s.astype(np.float16).astype(np.float64) / math.sqrt(d)   # fp16 matmul, fp16 / sqrt(d)
+    s = s.astype(np.float16).astype(np.float64)
+    P = (L + page_size - 1) // page_size
+    sets = None
+    if P > page_budget:
+        sign = np.where(q > 0, 1.0, -1.0)
+        mk = K.astype(np.float64) * sign[:, None, :]
+        pad = page_size - ((L - 1) % page_size + 1)
+        mk = np.concatenate([mk, np.full((h, pad, d), -65504.0)], axis=1)
+        pmax = mk.reshape(h, P, page_size, d).max(axis=2)
+        approx = np.einsum("hd,hpd->hp", np.abs(qf), pmax)[:, :P - 1]
+        sets = []
+        mask = np.zeros((h, L), bool)
+        for i in range(h):
+            top = np.argsort(-approx[i], kind="stable")[:page_budget - 1]
+            chosen = set(int(x) for x in top) | {P - 1}
+            sets.append(chosen)
+            for p in chosen:
+                mask[i, p * page_size:min(L, (p + 1) * page_size)] = True
+        s = np.where(mask, s, -65504.0)
+    e = np.exp(s - s.max(-1, keepdims=True))
+    p = (e / e.sum(-1, keepdims=True)).astype(np.float16).astype(np.float64)
+    return sets, np.einsum("hl,hld->hd", p, V.astype(np.float64)), approx if sets else None
+
+
+QK_GRID = [(L, pb) for L in (27, 61, 113, 482, 577, 1011, 1541) for pb in (4, 7, 15, 31, 55, 71)]
+
+
+@pytest.mark.parametrize("L,pb", QK_GRID)
+def test_quest_kernel_convention_matches_reference_test_construction(L, pb):
+    H = 4
+    q = randn16(100 + L, (1, H, 1, 128))
+    K = randn16(200 + L + pb, (1, H, L, 128))
+    V = randn16(300 + L + pb, (1, H, L, 128))
+    st = sim.SimLayerState(K[:, :, :L - 1], V[:, :, :L - 1])
+    o, scores, pages = sim.decode_step(st, q, K[:, :, L - 1:], V[:, :, L - 1:], pb * 16,
+                                       fixed=False, value_aware=False, semantics="quest_kernel")
+    ref_sets, ref_o, approx = _reference_kernel_convention(q[0, :, 0], K[0], V[0], 16, pb)
+    P = (L + 15) // 16
+    assert pages.shape[-1] == min(pb, P)
+    for i in range(H):
+        got = pages[0, i, 0]
+        assert got[-1] == P - 1  # the last page is always attended
+        if ref_sets is None:
+            assert list(got) == list(range(P))
+        else:
+            # the reference ranks by its own float64 bound: allow near-ties
+            ok, why = sim.selection_matches(got, np.array(sorted(ref_sets[i])),
+                                            np.append(approx[i], np.inf), forced={P - 1})
+            assert ok, (i, why)
+    # the reference test's tolerance (assert_close, fp16: rtol = atol = 5e-3)
+    np.testing.assert_allclose(o[0, :, 0].astype(np.float64), ref_o, rtol=5e-3, atol=5e-3)
+
+
+def test_quest_kernel_convention_is_not_the_simulation_rule():
+    """The construction above tells the two conventions apart: the
+    simulation's rule (k = max(3, budget/16), first and last page forced)
+    selects other pages on some grid case."""
+    differs = 0
+    for L, pb in QK_GRID:
+        P = (L + 15) // 16
+        if P <= pb:
+            continue
+        q = randn16(100 + L, (1, 4, 1, 128))
+        K = randn16(200 + L + pb, (1, 4, L, 128))
+        V = randn16(300 + L + pb, (1, 4, L, 128))
+        st = sim.SimLayerState(K, V)
+        _, sim_pages = sim.select_pages(st, q, pb * 16, fixed=True, value_aware=False)
+        _, qk_pages = sim.select_pages(st, q, pb * 16, value_aware=False,
+                                       semantics="quest_kernel")
+        differs += int(any(set(sim_pages[0, i, 0]) != set(qk_pages[0, i, 0]) for i in range(4)))
+    assert differs > 0
+
+
+def test_quest_kernel_pages_edge_cases():
+    s = np.array([[3.0, 9, 1, 9, 100.0]], np.float32)  # entry P-1 is never ranked
+    assert list(sim.quest_kernel_pages(s, 1)[0]) == [4]
+    assert list(sim.quest_kernel_pages(s, 0)[0]) == [4]
+    assert list(sim.quest_kernel_pages(s, 2)[0]) == [1, 4]       # tie 9/9: lower index
+    assert list(sim.quest_kernel_pages(s, 3)[0]) == [1, 3, 4]
+    assert list(sim.quest_kernel_pages(s, 99)[0]) == [0, 1, 2, 3, 4]
+    assert list(sim.quest_kernel_pages(np.zeros((1, 1), np.float32), 5)[0]) == [0]
