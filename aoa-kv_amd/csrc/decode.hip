@@ -471,23 +471,41 @@ __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, ui
   return true;
 }
 
-// Top-k of (sequence b, kv head h) from its stored scores, every chunk
-// written; lpl and budget of the sequence are passed in (loaded early).
-template <int GROUP>
-__device__ __forceinline__ void select_item(const EstimateArgs& a, uint32_t b, uint32_t h,
-                                            uint32_t lpl, uint32_t budget, TopkShared& tk) {
-  uint32_t pbeg;
-  uint32_t P = est_pages(a, b, &pbeg);
-  uint32_t k = num_selected_pages((P - 1u) * kPageSize + lpl, budget, kPageSize, P, a.flags);
-  if (a.flags & kFlagQuestKernel) {
+// The shape of one sequence's top-k: candidate pages, how many to select,
+// and whether the decode items will read the handoff rows.  Computed before
+// the wait for the scores, so its page-table loads are off the critical path.
+struct SelPlan {
+  uint32_t P, pbeg, k;
+  bool handoff;
+};
+
+__device__ __forceinline__ SelPlan plan_select(const EstimateArgs& a, uint32_t b) {
+  SelPlan p;
+  const uint32_t lpl = (uint32_t)a.kv_last_page_len[b];
+  const uint32_t budget = a.token_budgets ? (uint32_t)a.token_budgets[b] : a.token_budget;
+  p.P = est_pages(a, b, &p.pbeg);
+  p.k = p.P == 0u ? 0u
+                  : num_selected_pages((p.P - 1u) * kPageSize + lpl, budget, kPageSize, p.P,
+                                       a.flags);
+  if ((a.flags & kFlagQuestKernel) && p.P != 0u) {
     // the last page is attended without selection: k - 1 of the others
-    P -= 1u;
-    k -= 1u;
+    p.P -= 1u;
+    p.k -= 1u;
   }
-  if (k > a.sel_stride) k = a.sel_stride;  // never write past a selection row
+  if (p.k > a.sel_stride) p.k = a.sel_stride;  // never write past a selection row
   // no handoff entries for a sequence the decode items skip (malformed
   // last-page length): nothing would read and clear them
-  const bool handoff = a.hsel != nullptr && lpl >= 1u && lpl <= (uint32_t)kPageSize;
+  p.handoff = a.hsel != nullptr && lpl >= 1u && lpl <= (uint32_t)kPageSize;
+  return p;
+}
+
+// Top-k of (sequence b, kv head h) from its stored scores, every chunk
+// written, as planned by plan_select.
+template <int GROUP>
+__device__ __forceinline__ void select_item(const EstimateArgs& a, uint32_t b, uint32_t h,
+                                            const SelPlan& pl, TopkShared& tk) {
+  const uint32_t P = pl.P, k = pl.k, pbeg = pl.pbeg;
+  const bool handoff = pl.handoff;
   uint32_t* hout = handoff ? a.hsel + ((size_t)b * a.Hq + h * GROUP) * a.hsel_stride : nullptr;
   topk_staged(a.scores + ((size_t)b * a.Hkv + h) * a.score_stride, P, k,
               (a.flags & kFlagFixed) != 0u, a.kv_indices + pbeg,
@@ -499,18 +517,15 @@ __device__ __forceinline__ void select_item(const EstimateArgs& a, uint32_t b, u
 template <int GROUP>
 __device__ __forceinline__ void estimate_item(const EstimateArgs& a, uint32_t b, uint32_t h,
                                               uint32_t chunk, EstShared& sm, TopkShared* tk) {
-  // the selection size of the fused top-k, loaded up front (off the handoff path)
-  uint32_t lpl = 0u, budget = 0u;
-  if (a.sel != nullptr) {
-    lpl = (uint32_t)a.kv_last_page_len[b];
-    budget = a.token_budgets ? (uint32_t)a.token_budgets[b] : a.token_budget;
-  }
+  // the fused top-k's shape, loaded up front (off the handoff path)
+  SelPlan plan{};
+  if (a.sel != nullptr) plan = plan_select(a, b);
   if (!score_item<GROUP>(a, b, h, chunk, sm)) return;
   if (a.sel == nullptr) return;
   uint32_t pbeg;
   const uint32_t nch = (est_pages(a, b, &pbeg) + kEstPagesPerBlock - 1) / kEstPagesPerBlock;
   if (!arrive_last(&a.counters[(b * a.Hkv + h) * kCounterStride], nch, &sm.last)) return;
-  select_item<GROUP>(a, b, h, lpl, budget, *tk);
+  select_item<GROUP>(a, b, h, plan, *tk);
 }
 
 template <int GROUP, bool FUSED>
@@ -945,13 +960,11 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
   } else if (t < la.n_workers + la.n_heads) {
     const uint32_t bh = t - la.n_workers;
     const uint32_t b = bh / la.e.Hkv, h = bh % la.e.Hkv;
-    const uint32_t lpl = (uint32_t)la.e.kv_last_page_len[b];
-    const uint32_t budget =
-        la.e.token_budgets ? (uint32_t)la.e.token_budgets[b] : la.e.token_budget;
     uint32_t pbeg;
     const uint32_t P = est_pages(la.e, b, &pbeg);
     if (P == 0u) return;
     const uint32_t nch = (P + kEstPagesPerBlock - 1) / kEstPagesPerBlock;
+    const SelPlan plan = plan_select(la.e, b);
     if (threadIdx.x == 0) {
       uint32_t it = 0u, ok = 1u;
       while (ld_agent_u32(la.e.counters + bh * kCounterStride) < nch) {
@@ -966,7 +979,7 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
       s_ok = ok;
     }
     __syncthreads();
-    if (s_ok != 0u) select_item<GROUP>(la.e, b, h, lpl, budget, sm.e.tk);
+    if (s_ok != 0u) select_item<GROUP>(la.e, b, h, plan, sm.e.tk);
   } else if (t < la.n_workers + la.n_heads + la.n_dec) {
     const uint32_t u = t - la.n_workers - la.n_heads;
     const uint32_t bh = u / la.d.max_chunks, chunk = u % la.d.max_chunks;
