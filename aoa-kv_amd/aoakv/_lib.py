@@ -23,6 +23,7 @@ _u32 = ctypes.c_uint32
 _p = ctypes.c_void_p
 _sz = ctypes.c_size_t
 _int = ctypes.c_int
+_f32 = ctypes.c_float
 
 # name -> argument types (all return int status unless listed in _RESTYPES)
 SIGNATURES = {
@@ -47,6 +48,9 @@ SIGNATURES = {
                             _sz, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _p],
     "aoakv_prefill_with_paged_kv_cache": [_p, _p, _p, _p, _u32, _u32, _u32, _u32, _u32,
                                           _u32, _u32, _u32, _p],
+    "aoakv_apply_rope_in_place": [_p, _p, _u32, _u32, _u32, _u32, _u32, _f32, _f32, _p],
+    "aoakv_rope_append_kv_cache_decode": [_p, _p, _p, _u32, _u32, _p, _p, _p, _p, _p, _p, _p,
+                                          _p, _p, _u32, _u32, _u32, _u32, _f32, _f32, _p],
 }
 _RESTYPES = {
     "aoakv_last_error": ctypes.c_char_p,

@@ -94,6 +94,48 @@ def append_kv_cache_decode(k, v, kv_data, kv_indptr, kv_indices, kv_last_page_le
               v_log_norm.data_ptr(), v_mean.data_ptr(), H, D, S, layout, _stream())
 
 
+def apply_rope_in_place(q, k, past_kv_len: int, rope_scale: float = 1.0,
+                        rope_theta: float = 1e4):
+    """Reference: quest/ops/csrc/page.cu:224-265.  q [N, Hq, D], k [N, Hkv, D]
+    fp16, rotated in place; token n at position past_kv_len + n."""
+    _need(q, "q", torch.float16)
+    _need(k, "k", torch.float16)
+    if q.dim() != 3 or k.dim() != 3 or q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
+        raise ValueError(f"q / k must be [N, H, D] with the same N and D, got "
+                         f"{tuple(q.shape)} / {tuple(k.shape)}")
+    _lib.call("aoakv_apply_rope_in_place", q.data_ptr(), k.data_ptr(), q.shape[0], past_kv_len,
+              q.shape[1], k.shape[1], q.shape[2], float(rope_scale), float(rope_theta),
+              _stream())
+
+
+def rope_append_kv_cache_decode(q, k, v, kv_data, kv_indptr, kv_indices, kv_last_page_len,
+                                metadata_data, metadata_indptr, metadata_indices, v_log_norm,
+                                v_mean, layout: int, rope_scale: float = 1.0,
+                                rope_theta: float = 1e4):
+    """apply_rope_in_place + append_kv_cache_decode in one launch: q [B, Hq, D]
+    and k [B, H, D] rotated in place at each sequence's new position, then k, v
+    appended with metadata (reference calls QuestAttention.py:98-111)."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (kv_data, "kv_data"),
+                 (metadata_data, "metadata_data"), (v_log_norm, "v_log_norm"), (v_mean, "v_mean")):
+        _need(t, n, torch.float16)
+    for t, n in ((kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"),
+                 (kv_last_page_len, "kv_last_page_len"), (metadata_indptr, "metadata_indptr"),
+                 (metadata_indices, "metadata_indices")):
+        _need(t, n, torch.int32)
+    _, S, H, D = cache_dims(kv_data, layout)
+    B = k.shape[0]
+    if k.shape != (B, H, D) or v.shape != (B, H, D) or q.dim() != 3 or q.shape[0] != B \
+            or q.shape[2] != D:
+        raise ValueError(f"q must be [B, Hq, {D}], k/v [B, {H}, {D}]")
+    if kv_indptr.numel() != B + 1 or kv_last_page_len.numel() != B or metadata_indptr.numel() != B + 1:
+        raise ValueError("indptr / last_page_len sizes do not match the batch")
+    _lib.call("aoakv_rope_append_kv_cache_decode", q.data_ptr(), k.data_ptr(), v.data_ptr(), B,
+              q.shape[1], kv_data.data_ptr(), kv_indptr.data_ptr(), kv_indices.data_ptr(),
+              kv_last_page_len.data_ptr(), metadata_data.data_ptr(), metadata_indptr.data_ptr(),
+              metadata_indices.data_ptr(), v_log_norm.data_ptr(), v_mean.data_ptr(), H, D, S,
+              layout, float(rope_scale), float(rope_theta), _stream())
+
+
 def estimate_attn_score(q, scores, metadata_data, metadata_indptr, metadata_indices, kv_indptr,
                         kv_indices, kv_last_page_len, v_log_norm, max_pages: int, layout: int,
                         flags: int = FLAG_VALUE_AWARE):

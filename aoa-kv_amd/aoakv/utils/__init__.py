@@ -32,13 +32,44 @@ __all__ = [
     "KvCache",
     "KvPool",
     "InferenceController",
+    "apply_rope_in_place",
     "append_kv",
+    "rope_append_kv",
     "prefill_forward",
     "decode_estimate",
     "decode_topk",
     "decode_sparse_attn",
     "decode_layer",
 ]
+
+
+def apply_rope_in_place(q: torch.Tensor, k: torch.Tensor, past_kv_len: int,
+                        rope_scale: Optional[float] = None, rope_theta: Optional[float] = None):
+    """RoPE of q [N, Hq, D] and k [N, Hkv, D] in place, token n at position
+    past_kv_len + n (reference __init__.py:25-52; defaults scale 1, theta 1e4)."""
+    ops.apply_rope_in_place(q, k, past_kv_len, 1.0 if rope_scale is None else rope_scale,
+                            1e4 if rope_theta is None else rope_theta)
+
+
+def rope_append_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                   iController: InferenceController, layer_idx: int,
+                   rope_scale: Optional[float] = None, rope_theta: Optional[float] = None):
+    """apply_rope_in_place(q, k, seqlen - N) then append_kv(k, v) -- the
+    reference's two calls at QuestAttention.py:98-111 -- with the decode step
+    (N == 1) in one launch.  q and k are left rotated, as the reference leaves
+    them.  Call after begin_forward, like append_kv."""
+    c = iController
+    scale = 1.0 if rope_scale is None else rope_scale
+    theta = 1e4 if rope_theta is None else rope_theta
+    if k.size(0) > 1:
+        ops.apply_rope_in_place(q, k, c.kv_cache.seqlen - k.size(0), scale, theta)
+        append_kv(k, v, c, layer_idx)
+        return
+    ops.rope_append_kv_cache_decode(
+        q.view(1, -1, c.head_dim), k, v, c.kv_cache.buf_layer(layer_idx),
+        c.kv_indptr_for_append, c.kv_indices_with_last, c.kv_last_page_len_t,
+        c.metadata_cache.buf_layer(layer_idx), c.metadata_indptr_for_append, c.metadata_indices,
+        c.v_log_norm_layer(layer_idx), c.v_mean_layer(layer_idx), c.layout, scale, theta)
 
 
 def append_kv(k: torch.Tensor, v: torch.Tensor, iController: InferenceController,

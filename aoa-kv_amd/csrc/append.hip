@@ -111,21 +111,38 @@ __global__ __launch_bounds__(256) void append_prefill_kernel(AppendPrefillArgs a
 
 
 // One new token per sequence (update_page_filters / update_mean_page_filters,
-// filter_util.py:681-716, 758-795).
+// filter_util.py:681-716, 758-795).  With ROPE the block rows of grid.y past
+// the kv heads' rotate q in place, and k is rotated (in place, and as stored)
+// before the append: RoPE + append + metadata in one launch, the reference's
+// apply_rope_in_place then append_kv_cache_decode (QuestAttention.py:98-111).
+// The new token sits at position L - 1 of its sequence (L counts it).
+template <bool ROPE>
 __global__ __launch_bounds__(256) void append_decode_kernel(AppendDecodeArgs a) {
   const uint32_t lane = __lane_id();
   const uint32_t wave = threadIdx.x / kWave;
   const uint32_t row = lane / kLanesPerRow;
   const uint32_t l16 = lane % kLanesPerRow;
   const uint32_t b = blockIdx.x;
-  const uint32_t h = blockIdx.y * kHeadsPerBlock + wave * kHeadsPerWave + row;
-  if (h >= a.H) return;
+  const uint32_t kv_blocks = (a.H + kHeadsPerBlock - 1) / kHeadsPerBlock;
+  const bool q_block = ROPE && blockIdx.y >= kv_blocks;  // uniform per block
+  const uint32_t h = (q_block ? blockIdx.y - kv_blocks : blockIdx.y) * kHeadsPerBlock +
+                     wave * kHeadsPerWave + row;
+  if (h >= (q_block ? a.Hq : a.H)) return;
 
   const uint32_t S = a.S;
   const uint32_t pbeg = (uint32_t)a.kv_indptr[b];
   const uint32_t P = (uint32_t)a.kv_indptr[b + 1] - pbeg;
   const uint32_t lpl = (uint32_t)a.kv_last_page_len[b];
   if (P == 0u || lpl == 0u || lpl > S) return;  // malformed page table: nothing to do
+  RopeTable rt;
+  if constexpr (ROPE) {
+    rt = rope_table((P - 1u) * S + lpl - 1u, l16, a.rope_rcp_scale, a.rope_rcp_theta);
+    if (q_block) {
+      f16* qp = a.q + ((size_t)b * a.Hq + h) * kHeadDim + l16 * kVec;
+      st16(qp, rope_row(ld16(qp), rt, l16));
+      return;
+    }
+  }
   const uint32_t e = lpl - 1u;  // entry of the new token
   const uint32_t p = P - 1u;
   const uint32_t phys = (uint32_t)a.kv_indices[pbeg + p];
@@ -140,6 +157,10 @@ __global__ __launch_bounds__(256) void append_decode_kernel(AppendDecodeArgs a) 
   const size_t in_off = ((size_t)b * a.H + h) * kHeadDim + d0;
   H8 kk = ld16(a.k + in_off);
   H8 vv = ld16(a.v + in_off);
+  if constexpr (ROPE) {
+    kk = rope_row(kk, rt, l16);
+    st16(a.k + in_off, kk);
+  }
   H8 kmax, kmin, vbar;
   if (e == 0u) {  // new page: max = min = k, V̄ = v
     kmax = kk;
@@ -176,8 +197,38 @@ hipError_t launch_append_prefill(const AppendPrefillArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_append_decode(const AppendDecodeArgs& a, uint32_t batch, hipStream_t s) {
-  dim3 grid(batch, (a.H + kHeadsPerBlock - 1) / kHeadsPerBlock);
-  hipLaunchKernelGGL(append_decode_kernel, grid, dim3(256), 0, s, a);
+  const uint32_t kv_blocks = (a.H + kHeadsPerBlock - 1) / kHeadsPerBlock;
+  if (a.rope) {
+    const uint32_t q_blocks = (a.Hq + kHeadsPerBlock - 1) / kHeadsPerBlock;
+    hipLaunchKernelGGL(append_decode_kernel<true>, dim3(batch, kv_blocks + q_blocks), dim3(256),
+                       0, s, a);
+  } else {
+    hipLaunchKernelGGL(append_decode_kernel<false>, dim3(batch, kv_blocks), dim3(256), 0, s, a);
+  }
+  return hipGetLastError();
+}
+
+// In-place RoPE of q [N, Hq, D] and k [N, Hkv, D], token n at position
+// past + n (apply_rope_in_place, page.cu:224-265).  A block takes one token:
+// each lane computes the cos / sin of its 8 dims once and its row rotates
+// heads row, row + 16, ... of q then k.
+__global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
+  const uint32_t lane = __lane_id();
+  const uint32_t l16 = lane % kLanesPerRow;
+  const uint32_t r = threadIdx.x / kLanesPerRow;  // 16 rows per block
+  const uint32_t n = blockIdx.x;
+  const RopeTable rt = rope_table(a.past + n, l16, a.rope_rcp_scale, a.rope_rcp_theta);
+  for (uint32_t h = r; h < a.Hq + a.Hkv; h += 16u) {
+    f16* p = h < a.Hq ? a.q + ((size_t)n * a.Hq + h) * kHeadDim
+                      : a.k + ((size_t)n * a.Hkv + (h - a.Hq)) * kHeadDim;
+    p += l16 * kVec;
+    st16(p, rope_row(ld16(p), rt, l16));
+  }
+}
+
+hipError_t launch_rope(const RopeArgs& a, hipStream_t s) {
+  if (a.N == 0u) return hipSuccess;
+  hipLaunchKernelGGL(rope_kernel, dim3(a.N), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -5,6 +5,7 @@
 // Nothing here allocates device memory or synchronises.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <string>
@@ -214,7 +215,8 @@ int aoakv_append_kv_cache_decode(const void* k, const void* v, uint32_t batch_si
   REQUIRE(batch_size >= 1u && batch_size <= 65535u,
           "append_kv_cache_decode: batch_size %u out of range", batch_size);
   aoakv::AppendDecodeArgs a{};
-  a.k = static_cast<const aoakv::f16*>(k);
+  // k is only read without RoPE
+  a.k = static_cast<aoakv::f16*>(const_cast<void*>(k));
   a.v = static_cast<const aoakv::f16*>(v);
   a.kv = static_cast<aoakv::f16*>(kv_data);
   a.kv_indptr = kv_indptr;
@@ -230,6 +232,82 @@ int aoakv_append_kv_cache_decode(const void* k, const void* v, uint32_t batch_si
   a.g = aoakv::make_geom(layout, num_heads, page_size, head_dim);
   return hip_status(aoakv::launch_append_decode(a, batch_size, static_cast<hipStream_t>(stream)),
                     "append_kv_cache_decode");
+}
+
+// RoPE factors as the reference passes them (rope_scale, rope_theta; the
+// kernel uses their reciprocals, decode_page.cuh:855-856).
+static int check_rope(float rope_scale, float rope_theta, const char* fn) {
+  if (!(rope_scale > 0.f) || !(rope_theta > 0.f) || !std::isfinite(rope_scale) ||
+      !std::isfinite(rope_theta))
+    return fail(AOAKV_ERR_INVALID, "%s: rope_scale %g / rope_theta %g must be positive", fn,
+                (double)rope_scale, (double)rope_theta);
+  return AOAKV_OK;
+}
+
+int aoakv_apply_rope_in_place(void* q, void* k, uint32_t seq_len, uint32_t past_kv_len,
+                              uint32_t num_qo_heads, uint32_t num_kv_heads, uint32_t head_dim,
+                              float rope_scale, float rope_theta, void* stream) {
+  if (int e = check_shape(head_dim, aoakv::kPageSize, 0u, num_qo_heads)) return e;
+  REQUIRE(q && k, "apply_rope_in_place: null pointer argument");
+  REQUIRE(num_kv_heads >= 1u && num_kv_heads <= 256u,
+          "apply_rope_in_place: num_kv_heads %u out of range [1, 256]", num_kv_heads);
+  REQUIRE(seq_len <= 0x7FFFFFFFu && (uint64_t)past_kv_len + seq_len <= (1ull << 24),
+          "apply_rope_in_place: positions up to %llu exceed 2^24 (fp32 positions)",
+          (unsigned long long)past_kv_len + seq_len);
+  if (int e = check_rope(rope_scale, rope_theta, "apply_rope_in_place")) return e;
+  aoakv::RopeArgs a{};
+  a.q = static_cast<aoakv::f16*>(q);
+  a.k = static_cast<aoakv::f16*>(k);
+  a.N = seq_len;
+  a.past = past_kv_len;
+  a.Hq = num_qo_heads;
+  a.Hkv = num_kv_heads;
+  a.rope_rcp_scale = 1.0f / rope_scale;
+  a.rope_rcp_theta = 1.0f / rope_theta;
+  return hip_status(aoakv::launch_rope(a, static_cast<hipStream_t>(stream)), "apply_rope_in_place");
+}
+
+int aoakv_rope_append_kv_cache_decode(void* q, void* k, const void* v, uint32_t batch_size,
+                                      uint32_t num_qo_heads, void* kv_data,
+                                      const int32_t* kv_indptr, const int32_t* kv_indices,
+                                      const int32_t* kv_last_page_len, void* metadata_data,
+                                      const int32_t* metadata_indptr,
+                                      const int32_t* metadata_indices, void* v_log_norm,
+                                      void* v_mean, uint32_t num_heads, uint32_t head_dim,
+                                      uint32_t page_size, uint32_t layout, float rope_scale,
+                                      float rope_theta, void* stream) {
+  if (int e = check_shape(head_dim, page_size, layout, num_heads)) return e;
+  REQUIRE(q, "rope_append_kv_cache_decode: null pointer argument");
+  REQUIRE(num_qo_heads >= 1u && num_qo_heads <= 256u,
+          "rope_append_kv_cache_decode: num_qo_heads %u out of range [1, 256]", num_qo_heads);
+  if (int e = check_rope(rope_scale, rope_theta, "rope_append_kv_cache_decode")) return e;
+  REQUIRE(k && v && kv_data && kv_indptr && kv_indices && kv_last_page_len && metadata_data &&
+              metadata_indptr && metadata_indices && v_log_norm && v_mean,
+          "rope_append_kv_cache_decode: null pointer argument");
+  REQUIRE(batch_size >= 1u && batch_size <= 65535u,
+          "rope_append_kv_cache_decode: batch_size %u out of range", batch_size);
+  aoakv::AppendDecodeArgs a{};
+  a.k = static_cast<aoakv::f16*>(k);
+  a.v = static_cast<const aoakv::f16*>(v);
+  a.kv = static_cast<aoakv::f16*>(kv_data);
+  a.kv_indptr = kv_indptr;
+  a.kv_indices = kv_indices;
+  a.kv_last_page_len = kv_last_page_len;
+  a.meta = static_cast<aoakv::f16*>(metadata_data);
+  a.meta_indptr = metadata_indptr;
+  a.meta_indices = metadata_indices;
+  a.v_log_norm = static_cast<aoakv::f16*>(v_log_norm);
+  a.v_mean = static_cast<aoakv::f16*>(v_mean);
+  a.H = num_heads;
+  a.S = page_size;
+  a.g = aoakv::make_geom(layout, num_heads, page_size, head_dim);
+  a.rope = 1u;
+  a.q = static_cast<aoakv::f16*>(q);
+  a.Hq = num_qo_heads;
+  a.rope_rcp_scale = 1.0f / rope_scale;
+  a.rope_rcp_theta = 1.0f / rope_theta;
+  return hip_status(aoakv::launch_append_decode(a, batch_size, static_cast<hipStream_t>(stream)),
+                    "rope_append_kv_cache_decode");
 }
 
 static int fill_estimate(aoakv::EstimateArgs& a, const void* q, float* scores,

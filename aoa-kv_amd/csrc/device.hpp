@@ -155,6 +155,56 @@ __device__ inline f16 log_norm_row(const H8& vbar, uint32_t lane16) {
   return r16((float)ln);
 }
 
+// ---------------------------------------------------------------- RoPE
+// Llama rotary embedding in the rotate-half form (QKApplyRotaryInPlaceKernel,
+// decode_page.cuh:785-840, which the reference tests against HF's
+// apply_rotary_pos_emb, quest/tests/test_rope.py:17-30).  For dim d of a
+// 128-dim vector at position pos, with i = d mod 64:
+//   f_i = rcp_scale * rcp_theta^(i / 64),   a = fp32(pos) * f_i,
+//   out_d = x_d cos a - x_{d+64} sin a   (d < 64)
+//   out_d = x_d cos a + x_{d-64} sin a   (d >= 64),
+// with f_i evaluated in fp64 and rounded to fp32 (so it is the correctly
+// rounded frequency: at position 10^4 one ulp of f_i moves the angle by
+// ~10^-3), the angle and rotation in fp32 with the accurate sincosf, and one
+// rounding to fp16 at the end.  Lane l16
+// of a 16-lane row holds dims 8*l16 .. 8*l16 + 7, so the partner dims d +- 64
+// are in lane l16 ^ 8 of the same row (DPP row_ror:8).
+struct RopeTable {
+  float c[kVec], s[kVec];  // cos / sin of this lane's 8 dims at one position
+};
+
+__device__ inline RopeTable rope_table(uint32_t pos, uint32_t l16, float rcp_scale,
+                                       float rcp_theta) {
+  RopeTable t;
+#pragma unroll
+  for (int j = 0; j < kVec; ++j) {
+    const uint32_t i = (l16 * kVec + (uint32_t)j) % (kHeadDim / 2);
+    const float f =
+        (float)((double)rcp_scale * pow((double)rcp_theta, (double)(2u * i) / (double)kHeadDim));
+    sincosf((float)pos * f, &t.s[j], &t.c[j]);
+  }
+  return t;
+}
+
+__device__ inline H8 rope_row(const H8& x, const RopeTable& t, uint32_t l16) {
+  const uint4 u = __builtin_bit_cast(uint4, x);
+  uint4 pu;  // the partner lane's 8 dims
+  pu.x = (uint32_t)__builtin_amdgcn_mov_dpp((int)u.x, 0x128, 0xF, 0xF, false);  // row_ror:8
+  pu.y = (uint32_t)__builtin_amdgcn_mov_dpp((int)u.y, 0x128, 0xF, 0xF, false);
+  pu.z = (uint32_t)__builtin_amdgcn_mov_dpp((int)u.z, 0x128, 0xF, 0xF, false);
+  pu.w = (uint32_t)__builtin_amdgcn_mov_dpp((int)u.w, 0x128, 0xF, 0xF, false);
+  const H8 p = __builtin_bit_cast(H8, pu);
+  const bool low = l16 < 8u;  // dims < 64: the partner term enters negated
+  H8 y;
+#pragma unroll
+  for (int j = 0; j < kVec; ++j) {
+    const float a = (float)x.v[j] * t.c[j];
+    const float b = (float)p.v[j] * t.s[j];
+    y.v[j] = r16(low ? a - b : a + b);
+  }
+  return y;
+}
+
 // ---------------------------------------------------------------- cross-workgroup handoff
 // gfx950 has one L2 per XCD and the L2s are not coherent with each other.
 // An agent-scope __threadfence() therefore writes back and invalidates the

@@ -24,7 +24,7 @@ struct AppendPrefillArgs {
 };
 
 struct AppendDecodeArgs {
-  const f16* k;  // [B, H, D]
+  f16* k;        // [B, H, D] (rotated in place when rope)
   const f16* v;
   f16* kv;
   const int32_t* kv_indptr;
@@ -37,6 +37,19 @@ struct AppendDecodeArgs {
   f16* v_mean;
   uint32_t H, S;
   PageGeom g;
+  // fused RoPE (rope != 0): q [B, Hq, D] and k rotated in place at each
+  // sequence's new position, k stored rotated
+  uint32_t rope;
+  f16* q;
+  uint32_t Hq;
+  float rope_rcp_scale, rope_rcp_theta;
+};
+
+struct RopeArgs {
+  f16* q;  // [N, Hq, D]
+  f16* k;  // [N, Hkv, D]
+  uint32_t N, past, Hq, Hkv;
+  float rope_rcp_scale, rope_rcp_theta;
 };
 
 struct EstimateArgs {
@@ -125,6 +138,7 @@ struct LayerArgs {
 
 hipError_t launch_append_prefill(const AppendPrefillArgs& a, hipStream_t s);
 hipError_t launch_append_decode(const AppendDecodeArgs& a, uint32_t batch, hipStream_t s);
+hipError_t launch_rope(const RopeArgs& a, hipStream_t s);
 hipError_t launch_estimate(const EstimateArgs& a, uint32_t batch, uint32_t max_pages,
                            hipStream_t s);
 hipError_t launch_topk(const TopkArgs& a, uint32_t batch, hipStream_t s);

@@ -102,8 +102,11 @@ def build_layers(n_layers, layout, dev):
                 append_us=times, k0=k0, v0=v0)
 
 
-def decode_appends(dev, layout, n_app=512):
-    """Config 3b: prefill 4096+7 tokens then 512 single-token appends."""
+def decode_appends(dev, layout, n_app=512, mode="append"):
+    """Config 3b: prefill 4096+7 tokens then 512 single-token appends.
+    mode "append": the decode append alone; "rope_then_append": RoPE of q, k
+    then the append (two launches, the reference's call order); "rope_append":
+    the fused RoPE + append (one launch).  Eager launches, us per step."""
     import torch
     from aoakv import ops
     from aoakv.utils import InferenceController, append_kv
@@ -116,6 +119,7 @@ def decode_appends(dev, layout, n_app=512):
               torch.randn((4103, H, D), generator=g, device=dev).half(), c, 0)
     kn = torch.randn((n_app, 1, H, D), generator=g, device=dev).half()
     vn = torch.randn((n_app, 1, H, D), generator=g, device=dev).half()
+    qn = torch.randn((n_app, 1, H, D), generator=g, device=dev).half()
     # device page tables for all steps are prepared up front; the timed loop
     # is the append kernels only (the host planner's uploads are not timed)
     steps = []
@@ -128,6 +132,13 @@ def decode_appends(dev, layout, n_app=512):
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for i, (ip, ix, lp, mip, mix) in enumerate(steps):
+        if mode == "rope_append":
+            ops.rope_append_kv_cache_decode(qn[i], kn[i], vn[i], c.kv_cache.buf_layer(0), ip, ix,
+                                            lp, c.metadata_cache.buf_layer(0), mip, mix,
+                                            c.v_log_norm[0], c.v_mean[0], layout)
+            continue
+        if mode == "rope_then_append":
+            ops.apply_rope_in_place(qn[i], kn[i], 4103 + i)
         ops.append_kv_cache_decode(kn[i], vn[i], c.kv_cache.buf_layer(0), ip, ix, lp,
                                    c.metadata_cache.buf_layer(0), mip, mix, c.v_log_norm[0],
                                    c.v_mean[0], layout)
@@ -437,6 +448,10 @@ def main():
         extra["bulk_append_32k_GBps"] = round(app_bytes / (np.median(app) * 1e-6) / 1e9, 1)
         extra["bulk_append_bytes"] = app_bytes
         extra["decode_append_us"] = round(decode_appends(dev, layout), 3)
+        extra["decode_rope_then_append_us"] = round(
+            decode_appends(dev, layout, mode="rope_then_append"), 3)
+        extra["decode_rope_append_fused_us"] = round(
+            decode_appends(dev, layout, mode="rope_append"), 3)
         for Lp in (8192, 16384):
             us, tf = prefill_bench(dev, layout, Lp)
             extra[f"prefill_{Lp // 1024}k_us"] = round(us, 1)

@@ -14,9 +14,11 @@
  *     PyTorchWrapper                aoakv_workspace_init,
  *     .begin/forward/end_forward    aoakv_decode_sparse_attn
  *   prefill_with_paged_kv_cache  -> aoakv_prefill_with_paged_kv_cache
+ *   apply_rope_in_place          -> aoakv_apply_rope_in_place
  *
- * plus one fused entry point (aoakv_sparse_decode_layer) that runs
- * estimate + top-k + sparse decode for one layer.
+ * plus fused entry points: aoakv_sparse_decode_layer (estimate + top-k +
+ * sparse decode for one layer), aoakv_estimate_topk, and
+ * aoakv_rope_append_kv_cache_decode (RoPE + decode append).
  *
  * Conventions
  *   - All tensor arguments are device pointers (plain pointers, no torch
@@ -127,6 +129,39 @@ int aoakv_append_kv_cache_decode(const void* k, const void* v, uint32_t batch_si
                                  const int32_t* metadata_indices, void* v_log_norm,
                                  void* v_mean, uint32_t num_heads, uint32_t head_dim,
                                  uint32_t page_size, uint32_t layout, void* stream);
+
+/*
+ * Rotary position embedding of q [seq_len, num_qo_heads, head_dim] and
+ * k [seq_len, num_kv_heads, head_dim] (NHD, fp16), in place; token n is at
+ * position past_kv_len + n.  Replaces apply_rope_in_place (reference
+ * page.cu:224-265, QKApplyRotaryInPlaceKernel decode_page.cuh:785-869): the
+ * Llama rotate-half form with frequency (1/rope_scale) *
+ * (1/rope_theta)^(2i/head_dim) for the dim pair (i, i + head_dim/2),
+ * computed in fp32, rounded once to fp16.  The reference defaults are
+ * rope_scale 1, rope_theta 1e4 (quest/utils/__init__.py:42-45).
+ * Positions up to 2^24.
+ */
+int aoakv_apply_rope_in_place(void* q, void* k, uint32_t seq_len, uint32_t past_kv_len,
+                              uint32_t num_qo_heads, uint32_t num_kv_heads, uint32_t head_dim,
+                              float rope_scale, float rope_theta, void* stream);
+
+/*
+ * The decode step's RoPE and append in one launch: aoakv_apply_rope_in_place
+ * on q [B, num_qo_heads, D] and k [B, num_heads, D] at each sequence's new
+ * position (the token the page table already counts: L_b - 1), then
+ * aoakv_append_kv_cache_decode of the rotated k and v.  Same results, bit
+ * for bit, as the two calls; q and k are rotated in place as the reference's
+ * QuestAttention.forward leaves them (QuestAttention.py:98-111).
+ */
+int aoakv_rope_append_kv_cache_decode(void* q, void* k, const void* v, uint32_t batch_size,
+                                      uint32_t num_qo_heads, void* kv_data,
+                                      const int32_t* kv_indptr, const int32_t* kv_indices,
+                                      const int32_t* kv_last_page_len, void* metadata_data,
+                                      const int32_t* metadata_indptr,
+                                      const int32_t* metadata_indices, void* v_log_norm,
+                                      void* v_mean, uint32_t num_heads, uint32_t head_dim,
+                                      uint32_t page_size, uint32_t layout, float rope_scale,
+                                      float rope_theta, void* stream);
 
 /*
  * Page scores of every page of every sequence.  Replaces estimate_attn_score

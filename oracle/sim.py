@@ -439,6 +439,37 @@ def decode_step(state: SimLayerState, q: np.ndarray, k_new: np.ndarray, v_new: n
 
 
 # --------------------------------------------------------------------------
+# Rotary position embedding (apply_rope_in_place)
+# --------------------------------------------------------------------------
+
+def apply_rope(x: np.ndarray, positions: np.ndarray, rope_scale: float = 1.0,
+               rope_theta: float = 1e4) -> np.ndarray:
+    """Llama RoPE, rotate-half form, as the reference kernel computes it
+    (``QKApplyRotaryInPlaceKernel``, decode_page.cuh:785-840: frequency
+    ``rcp_scale * rcp_theta^(2i/D)`` in fp32, angle = fp32(position) * freq,
+    fp32 arithmetic, one rounding to fp16) and as its test checks it
+    (quest/tests/test_rope.py:17-30, HF ``apply_rotary_pos_emb``).  The fp32
+    frequency is the correctly rounded one.
+
+    x (N, H, D) fp16, positions (N,) ints.  The angle is formed in fp32 as
+    the kernel does; cos / sin and the rotation are evaluated in float64, so
+    the result is the exactly rounded value the fp32 kernel approximates.
+    Returns float64 (N, H, D) (round with ``h()`` for the fp16 result)."""
+    N, H, D = x.shape
+    half = D // 2
+    i = np.arange(D) % half
+    rcp_scale = np.float64(np.float32(1.0) / np.float32(rope_scale))
+    rcp_theta = np.float64(np.float32(1.0) / np.float32(rope_theta))
+    # the correctly rounded fp32 frequency (fp64 evaluation, one rounding)
+    freq = (rcp_scale * np.power(rcp_theta, (2 * i) / D)).astype(np.float32)
+    ang = (np.asarray(positions, np.float32)[:, None] * freq[None, :]).astype(np.float64)
+    c, sn = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    xf = x.astype(np.float64)
+    rot = np.concatenate([-xf[..., half:], xf[..., :half]], axis=-1)   # rotate_half
+    return xf * c + rot * sn
+
+
+# --------------------------------------------------------------------------
 # Dense causal prefill (textbook; quest/tests/test_prefill_attention.py:17-44,
 # kernels/src/include/cpu_reference.h:56-159)
 # --------------------------------------------------------------------------

@@ -135,3 +135,21 @@ def test_kv_cache_page_bookkeeping_on_host():
     assert sorted(s.indicies) == list(range(7)) and s.indicies != list(range(7))
     with pytest.raises(RuntimeError):
         s.append_seq(100)
+
+
+def test_rope_validation_without_gpu():
+    from aoakv import _lib
+    lib = _lib.load()
+    nul = None
+    rc = lib.aoakv_apply_rope_in_place(1, 1, 4, 0, 32, 32, 64, 1.0, 1e4, nul)
+    assert rc == _lib.AOAKV_ERR_UNSUPPORTED and b"head_dim" in lib.aoakv_last_error()
+    rc = lib.aoakv_apply_rope_in_place(1, 1, 4, 0, 32, 32, 128, 0.0, 1e4, nul)
+    assert rc == _lib.AOAKV_ERR_INVALID and b"rope_scale" in lib.aoakv_last_error()
+    rc = lib.aoakv_apply_rope_in_place(1, 1, 4, 1 << 24, 32, 32, 128, 1.0, 1e4, nul)
+    assert rc == _lib.AOAKV_ERR_INVALID and b"2^24" in lib.aoakv_last_error()
+    rc = lib.aoakv_rope_append_kv_cache_decode(nul, 1, 1, 1, 32, 1, 1, 1, 1, 1, 1, 1, 1, 1, 32,
+                                               128, 16, 1, 1.0, 1e4, nul)
+    assert rc == _lib.AOAKV_ERR_INVALID and b"null" in lib.aoakv_last_error()
+    rc = lib.aoakv_rope_append_kv_cache_decode(1, 1, 1, 1, 32, 1, 1, 1, 1, 1, 1, 1, 1, 1, 32,
+                                               128, 16, 1, 1.0, -1.0, nul)
+    assert rc == _lib.AOAKV_ERR_INVALID and b"rope_theta" in lib.aoakv_last_error()

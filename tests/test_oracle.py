@@ -344,3 +344,88 @@ def test_quest_kernel_pages_edge_cases():
     assert list(sim.quest_kernel_pages(s, 3)[0]) == [1, 3, 4]
     assert list(sim.quest_kernel_pages(s, 99)[0]) == [0, 1, 2, 3, 4]
     assert list(sim.quest_kernel_pages(np.zeros((1, 1), np.float32), 5)[0]) == [0]
+
+
+# --------------------------------------------------------------------------
+# RoPE (apply_rope_in_place): pinned against the library routine the
+# reference's test compares with (HF apply_rotary_pos_emb,
+# quest/tests/test_rope.py:17-30), against the complex-rotation form, and
+# by invariants.
+# --------------------------------------------------------------------------
+
+def _rope_angles(positions, D, rope_scale=1.0, rope_theta=1e4):
+    """fp32 angles pos * f_i with f_i = (1/scale) * (1/theta)^(2i/D), the
+    reciprocals in fp32 as the reference kernel forms them
+    (decode_page.cuh:855-856), the power in fp64, rounded to fp32 once.
+    (HF's inv_freq = 1 / theta^(2i/D) differs from this in the last fp32
+    bits; the GPU test compares with HF's fp16 result at the reference
+    test's tolerance.)"""
+    i = np.arange(D // 2)
+    freq = (np.float64(np.float32(1.0) / np.float32(rope_scale)) *
+            np.power(np.float64(np.float32(1.0) / np.float32(rope_theta)), (2 * i) / D)
+            ).astype(np.float32)
+    return (np.asarray(positions, np.float32)[:, None] * freq[None, :]).astype(np.float64)
+
+
+@pytest.mark.parametrize("past,n,scale,theta", [(0, 5, 1.0, 1e4), (1110, 7, 1.0, 1e4),
+                                                (311, 19, 2.0, 5e5)])
+def test_rope_matches_hf_apply_rotary_pos_emb(past, n, scale, theta):
+    from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+    q = randn16(70 + n, (n, 4, 128))
+    k = randn16(71 + n, (n, 2, 128))
+    pos = past + np.arange(n)
+    ang = _rope_angles(pos, 128, scale, theta)
+    emb = np.concatenate([ang, ang], axis=-1)                      # HF: cat(freqs, freqs)
+    cos = torch.from_numpy(np.cos(emb))[None]
+    sin = torch.from_numpy(np.sin(emb))[None]
+    qt = torch.from_numpy(q.astype(np.float64)).transpose(0, 1)[None]   # [1, H, N, D]
+    kt = torch.from_numpy(k.astype(np.float64)).transpose(0, 1)[None]
+    qr, kr = apply_rotary_pos_emb(qt, kt, cos, sin)
+    np.testing.assert_allclose(sim.apply_rope(q, pos, scale, theta),
+                               qr[0].transpose(0, 1).numpy(), rtol=0, atol=1e-12)
+    np.testing.assert_allclose(sim.apply_rope(k, pos, scale, theta),
+                               kr[0].transpose(0, 1).numpy(), rtol=0, atol=1e-12)
+
+
+def test_rope_is_the_complex_rotation_of_dim_pairs():
+    x = randn16(80, (6, 3, 128))
+    pos = np.array([0, 1, 17, 250, 4096, 65535])
+    ang = _rope_angles(pos, 128)
+    z = (x[..., :64].astype(np.float64) + 1j * x[..., 64:].astype(np.float64)) * \
+        np.exp(1j * ang)[:, None, :]
+    out = sim.apply_rope(x, pos)
+    np.testing.assert_allclose(out[..., :64], z.real, atol=1e-12)
+    np.testing.assert_allclose(out[..., 64:], z.imag, atol=1e-12)
+    # position 0 is the identity; each (i, i + 64) pair keeps its length
+    np.testing.assert_array_equal(out[0], x[0].astype(np.float64))
+    r_in = np.hypot(x[..., :64].astype(np.float64), x[..., 64:].astype(np.float64))
+    np.testing.assert_allclose(np.hypot(out[..., :64], out[..., 64:]), r_in, rtol=1e-12)
+
+
+def test_rope_scores_depend_on_relative_position_only():
+    q = randn16(90, (1, 1, 128))
+    k = randn16(91, (1, 1, 128))
+    def score(m, n):
+        return float(np.sum(sim.apply_rope(q, [m])[0, 0] * sim.apply_rope(k, [n])[0, 0]))
+    for m, n, t in ((10, 3, 5), (40, 40, 7), (100, 1, 64)):
+        assert abs(score(m, n) - score(m + t, n + t)) < 1e-3
+
+
+def test_rope_planted_mistakes_fail_the_hf_check():
+    """A wrong partner sign, an unwrapped frequency index, theta instead of
+    1/theta: each moves the result far beyond fp16 noise."""
+    x = randn16(95, (3, 2, 128))
+    pos = np.array([5, 77, 300])
+    good = sim.apply_rope(x, pos)
+    xf = x.astype(np.float64)
+    ang = _rope_angles(pos, 128)[:, None, :]
+    c, s = np.cos(ang), np.sin(ang)
+    wrong_sign = np.concatenate([xf[..., :64] * c + xf[..., 64:] * s,
+                                 xf[..., 64:] * c - xf[..., :64] * s], -1)
+    i = np.arange(128)
+    f_unwrapped = np.power(np.float32(1e-4), (2 * i).astype(np.float32) / np.float32(128))
+    a2 = (pos[:, None].astype(np.float32) * f_unwrapped[None]).astype(np.float64)[:, None, :]
+    rot = np.concatenate([-xf[..., 64:], xf[..., :64]], -1)
+    unwrapped = xf * np.cos(a2) + rot * np.sin(a2)
+    for bad in (wrong_sign, unwrapped, sim.apply_rope(x, pos, 1.0, 1e-4)):
+        assert np.abs(bad - good).max() > 0.05
