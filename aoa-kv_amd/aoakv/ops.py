@@ -272,14 +272,17 @@ def estimate_topk(q, metadata_data, metadata_indptr, metadata_indices, kv_indptr
 
 def prefill_with_paged_kv_cache(q, kv_data, kv_indices, num_kv_pages: int, kv_last_page_len: int,
                                 layout: int, causal: bool = True, o=None):
-    """Reference: quest/ops/csrc/batch_prefill.cu:27-117.  q [L, H, D] -> o."""
+    """Reference: quest/ops/csrc/batch_prefill.cu:27-117.  q [L, Hq, D] -> o;
+    the cache holds Hkv heads, Hq a multiple of Hkv (GQA)."""
     _need(q, "q", torch.float16)
     _need(kv_data, "kv_data", torch.float16)
     _need(kv_indices, "kv_indices", torch.int32)
     _, S, H, D = cache_dims(kv_data, layout)
+    if q.dim() != 3 or q.shape[2] != D:
+        raise ValueError(f"q must be [L, Hq, {D}], got {tuple(q.shape)}")
     if o is None:
         o = torch.empty_like(q)
     _lib.call("aoakv_prefill_with_paged_kv_cache", q.data_ptr(), o.data_ptr(), kv_data.data_ptr(),
-              kv_indices.data_ptr(), num_kv_pages, kv_last_page_len, q.shape[0], int(causal), H,
-              D, S, layout, _stream())
+              kv_indices.data_ptr(), num_kv_pages, kv_last_page_len, q.shape[0], int(causal),
+              q.shape[1], H, D, S, layout, _stream())
     return o

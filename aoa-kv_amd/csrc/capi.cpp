@@ -97,8 +97,9 @@ size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 // [hpart: B*Hq*chunks*stride u32]; every region 256-byte aligned.  The
 // control words sit at offset 0 so a caller can read the error flag (word
 // 2) without knowing the shapes.  All of it starts zeroed
-// (aoakv_workspace_init) and every launch leaves it zeroed again, except
-// the two-launch partials, which are always written before they are read.
+// (aoakv_workspace_init) and every launch leaves all of it zeroed again
+// (the offsets depend on the call's selection size, so a region that must
+// start at zero in one call can lie where another call kept other data).
 size_t ws_layout(uint32_t B, uint32_t hq, uint32_t hkv, uint32_t max_sel_pages, void* base,
                  Workspace* w) {
   const size_t part =
@@ -583,9 +584,14 @@ int aoakv_estimate_topk(const void* q, const void* metadata_data, const int32_t*
 int aoakv_prefill_with_paged_kv_cache(const void* q, void* o, const void* kv_data,
                                       const int32_t* kv_indices, uint32_t num_kv_pages,
                                       uint32_t kv_last_page_len, uint32_t qo_len,
-                                      uint32_t causal, uint32_t num_heads, uint32_t head_dim,
+                                      uint32_t causal, uint32_t num_qo_heads,
+                                      uint32_t num_kv_heads, uint32_t head_dim,
                                       uint32_t page_size, uint32_t layout, void* stream) {
-  if (int e = check_shape(head_dim, page_size, layout, num_heads)) return e;
+  if (int e = check_shape(head_dim, page_size, layout, num_qo_heads)) return e;
+  if (num_kv_heads == 0u || num_qo_heads % num_kv_heads != 0u)
+    return fail(AOAKV_ERR_INVALID,
+                "prefill_with_paged_kv_cache: num_qo_heads %u not a multiple of num_kv_heads %u",
+                num_qo_heads, num_kv_heads);
   REQUIRE(q && o && kv_data && kv_indices, "prefill_with_paged_kv_cache: null pointer argument");
   REQUIRE(num_kv_pages >= 1u, "prefill_with_paged_kv_cache: num_kv_pages must be >= 1");
   REQUIRE(kv_last_page_len >= 1u && kv_last_page_len <= page_size,
@@ -601,12 +607,13 @@ int aoakv_prefill_with_paged_kv_cache(const void* q, void* o, const void* kv_dat
   a.o = static_cast<aoakv::f16*>(o);
   a.kv = static_cast<const aoakv::f16*>(kv_data);
   a.kv_indices = kv_indices;
-  a.H = num_heads;
+  a.H = num_kv_heads;
+  a.Hq = num_qo_heads;
   a.L = (uint32_t)L;
   a.Lq = qo_len;
   a.causal = causal ? 1u : 0u;
   a.sm_scale = 1.0f / aoakv::kSqrtHeadDim;
-  a.g = aoakv::make_geom(layout, num_heads, page_size, head_dim);
+  a.g = aoakv::make_geom(layout, num_kv_heads, page_size, head_dim);
   return hip_status(aoakv::launch_prefill(a, static_cast<hipStream_t>(stream)),
                     "prefill_with_paged_kv_cache");
 }

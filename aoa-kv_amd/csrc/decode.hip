@@ -888,21 +888,24 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   if (half == 1u) s_o[0][d] = acc;
   __syncthreads();
   if (half == 0u) a.o[bh * kHeadDim + d] = r16((acc + s_o[0][d]) / Lsum);
-  if (HANDOFF) {
-    // every thread has read its words (barrier above): clear them for the
-    // next launch -- o words by their reader, m / l words by thread c
-    for (uint32_t g0 = 0; g0 < nch; g0 += 16u) {
-      const size_t gb = base + (size_t)g0 * kPartialStride;
+  // Every thread has read its words (barrier above): clear them -- o words by
+  // their reader, m / l words by thread c.  Handoff words must be zero for
+  // the next launch; the two-launch partials are cleared as well, so the
+  // whole workspace is zero between calls whatever its layout: region
+  // offsets depend on the call's selection size, and a later call with a
+  // smaller one places its handoff words where these partials were.
+  uint32_t* words = HANDOFF ? a.hpart : reinterpret_cast<uint32_t*>(a.partial);
+  for (uint32_t g0 = 0; g0 < nch; g0 += 16u) {
+    const size_t gb = base + (size_t)g0 * kPartialStride;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t c = g0 + half + 2u * i;
-        if (c < nch) st_agent_u32(a.hpart + gb + (half + 2u * i) * kPartialStride + d, 0u);
-      }
-      const uint32_t c = g0 + threadIdx.x;
-      if (threadIdx.x < 16u && c < nch) {
-        st_agent_u32(a.hpart + gb + threadIdx.x * kPartialStride + kHeadDim, 0u);
-        st_agent_u32(a.hpart + gb + threadIdx.x * kPartialStride + kHeadDim + 1, 0u);
-      }
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t c = g0 + half + 2u * i;
+      if (c < nch) st_agent_u32(words + gb + (half + 2u * i) * kPartialStride + d, 0u);
+    }
+    const uint32_t c = g0 + threadIdx.x;
+    if (threadIdx.x < 16u && c < nch) {
+      st_agent_u32(words + gb + threadIdx.x * kPartialStride + kHeadDim, 0u);
+      st_agent_u32(words + gb + threadIdx.x * kPartialStride + kHeadDim + 1, 0u);
     }
   }
 }

@@ -116,11 +116,12 @@ struct DecodeArgs {
 };
 
 struct PrefillArgs {
-  const f16* q;  // [Lq, H, D]
-  f16* o;        // [Lq, H, D]
+  const f16* q;  // [Lq, Hq, D]
+  f16* o;        // [Lq, Hq, D]
   const f16* kv;
   const int32_t* kv_indices;
-  uint32_t H, L, Lq, causal;
+  uint32_t H, L, Lq, causal;  // H: kv heads of the cache
+  uint32_t Hq;                // query heads, a multiple of H
   float sm_scale;
   PageGeom g;
 };

@@ -77,7 +77,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int g = lane / 32;      // lane group
   const int c = lane % 32;      // query column of this lane
-  const uint32_t h = blockIdx.y;
+  const uint32_t h = blockIdx.y;           // query head
+  const uint32_t hkv = h / (a.Hq / a.H);   // its kv head (GQA groups share K/V)
   const uint32_t nqt = gridDim.x;
   const uint32_t qt = nqt - 1u - blockIdx.x;  // heaviest query tiles first
   const uint32_t L = a.L, Lq = a.Lq;
@@ -101,7 +102,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
   half8 qreg[8];
 #pragma unroll
   for (int s = 0; s < 8; ++s)
-    qreg[s] = q_live ? *reinterpret_cast<const half8*>(a.q + ((size_t)q * a.H + h) * kHeadDim +
+    qreg[s] = q_live ? *reinterpret_cast<const half8*>(a.q + ((size_t)q * a.Hq + h) * kHeadDim +
                                                           16 * s + 8 * g)
                      : half8{};
 
@@ -125,7 +126,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * wave + 4 * i + lrow;  // row in the tile; r % 16 = 4i + lrow
-      const size_t e = elem_off(a.g, phys, 0, h, (uint32_t)(r & 15));
+      const size_t e = elem_off(a.g, phys, 0, hkv, (uint32_t)(r & 15));
       __builtin_amdgcn_global_load_lds(a.kv + e + 8 * (lslot ^ k_swz(r)),
                                        buf + (16 * wave + 4 * i) * kPfRowBytes, 16, 0, 0);
       __builtin_amdgcn_global_load_lds(a.kv + e + a.g.kv + 8 * (lslot ^ v_swz(r)),
@@ -297,7 +298,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
   // ---- o = O / l: lane holds its query's dims t*32 + crow(i, g)
   if (!q_live) return;
   const float inv_l = 1.f / l_run;
-  f16* orow = a.o + ((size_t)q * a.H + h) * kHeadDim;
+  f16* orow = a.o + ((size_t)q * a.Hq + h) * kHeadDim;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
 #pragma unroll
@@ -312,7 +313,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
 
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t s) {
   const uint32_t nqt = (a.Lq + kPfQueriesPerBlock - 1) / kPfQueriesPerBlock;
-  hipLaunchKernelGGL(prefill_kernel, dim3(nqt, a.H), dim3(kPfThreads), 0, s, a);
+  hipLaunchKernelGGL(prefill_kernel, dim3(nqt, a.Hq), dim3(kPfThreads), 0, s, a);
   return hipGetLastError();
 }
 

@@ -286,7 +286,9 @@ int aoakv_estimate_topk(const void* q, const void* metadata_data, const int32_t*
  * prefill_with_paged_kv_cache (reference bsk_ops.h:87-95,
  * batch_prefill.cu:27-117, prefill.cuh:688-1115).
  *
- * q, o: [qo_len, num_heads, head_dim] fp16; the queries are the last qo_len
+ * q, o: [qo_len, num_qo_heads, head_dim] fp16; the cache holds num_kv_heads
+ * heads (num_qo_heads a multiple of it: query head h reads kv head
+ * h / (num_qo_heads / num_kv_heads)).  The queries are the last qo_len
  * positions of the L = (num_kv_pages-1)*page_size + kv_last_page_len
  * cached tokens; query i attends keys <= L - qo_len + i when causal.
  * fp16 inputs, fp32 accumulation (MFMA), fp16 output.
@@ -294,7 +296,8 @@ int aoakv_estimate_topk(const void* q, const void* metadata_data, const int32_t*
 int aoakv_prefill_with_paged_kv_cache(const void* q, void* o, const void* kv_data,
                                       const int32_t* kv_indices, uint32_t num_kv_pages,
                                       uint32_t kv_last_page_len, uint32_t qo_len,
-                                      uint32_t causal, uint32_t num_heads, uint32_t head_dim,
+                                      uint32_t causal, uint32_t num_qo_heads,
+                                      uint32_t num_kv_heads, uint32_t head_dim,
                                       uint32_t page_size, uint32_t layout, void* stream);
 
 #ifdef __cplusplus

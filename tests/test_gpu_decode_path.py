@@ -496,3 +496,51 @@ def test_errors_are_reported_not_crashed():
                                     torch.zeros((4, 8), dtype=torch.float16, device=DEV),
                                     torch.zeros((4, 8, 64), dtype=torch.float16, device=DEV),
                                     HND)
+
+
+def test_workspace_shared_across_shrinking_selection_sizes():
+    """Regression: one workspace used by calls of different selection sizes.
+    Region offsets depend on the call's selection size, so a call with a
+    smaller one places its handoff words where an earlier call's split-K
+    partials were; every call must leave the whole workspace zero (a stale
+    partial read as a page id sent a one-launch decode to a wild address)."""
+    from aoakv import ops
+    _say("[workspace reuse]")
+    H, budget = 8, 512
+    ctrls, data = [], []
+    for L, seed in ((9600, 31), (4800, 32)):   # 600 and 300 pages
+        q, K, V = _sim_state(seed, H, L)
+        c = make_ctrl(H, L + 16, HND, budget, shuffle=seed)
+        prefill(c, K, V)
+        c.begin_forward(1)
+        ctrls.append(c)
+        data.append(torch.from_numpy(q[0, :, 0].copy()).to(DEV)[None])
+    big, small = ctrls
+    ws = ops.decode_workspace(1, H, H, 600)
+
+    def layer(c, qd, flags):
+        o = torch.empty_like(qd)
+        sel = torch.zeros((1, H, 300), dtype=torch.int32, device=DEV)
+        P = len(c.kv_cache.indicies)
+        ops.sparse_decode_layer(qd, o, c.kv_cache.buf_layer(0), c.kv_indptr_for_append,
+                                c.kv_indices_with_last, c.kv_last_page_len_t,
+                                c.metadata_cache.buf_layer(0), c.metadata_indptr_for_append,
+                                c.metadata_indices, c.v_log_norm_layer(0), c.scores, sel, budget,
+                                ws, P, HND, flags)
+        return o, sel
+
+    F = ops.FLAG_VALUE_AWARE | ops.FLAG_FIXED
+    o_ref, sel_ref = layer(small, data[1], F)              # two launches
+    for rep in range(3):
+        # dense decode of the 600-page sequence: partials for 75 chunks
+        o_d = torch.empty_like(data[0])
+        ops.decode_sparse_attn(data[0], o_d, big.kv_cache.buf_layer(0), big.kv_indptr_for_append,
+                               big.kv_indices_with_last, big.kv_last_page_len_t, None, budget, ws,
+                               600, H, HND)
+        # one launch on the 300-page sequence: its handoff rows now lie in
+        # that partial region
+        o1, sel1 = layer(small, data[1], F | ops.FLAG_SINGLE_LAUNCH)
+        torch.cuda.synchronize()
+        assert torch.equal(o1, o_ref) and torch.equal(sel1, sel_ref), rep
+        assert int(ws[8:12].view(torch.int32).item()) == 0, "spin-wait error flag set"
+    assert not torch.any(ws[256:].view(torch.int32) != 0), "workspace not left zero"

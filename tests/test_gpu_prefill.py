@@ -104,3 +104,29 @@ def test_prefill_config4_8k_sampled_rows(layout):
     _say(f"   max err {err:.2e}")
     assert err <= 2e-3
     assert np.isfinite(o.astype(np.float32)).all()
+
+
+@pytest.mark.parametrize("layout", [NHD, HND])
+@pytest.mark.parametrize("group", [2, 4])
+def test_prefill_gqa(layout, group):
+    """num_qo_heads = group * num_kv_heads: query head h attends kv head
+    h // group (the reference's prefill kernel takes both head counts,
+    prefill.cuh:688-870)."""
+    from aoakv import ops
+    from aoakv.utils import InferenceController, append_kv
+    _say(f"[prefill] gqa group={group} layout={layout}")
+    L, Lq, Hkv = 500, 300, 2
+    Hq = Hkv * group
+    q = randn16(40 + group, (Lq, Hq, D), 0.5)
+    k = randn16(41 + group, (L, Hkv, D), 0.5)
+    v = randn16(42 + group, (L, Hkv, D), 0.5)
+    c = InferenceController(1, Hq, D, S, 64, L + S, torch.float16, DEV, layout=layout,
+                            num_kv_heads=Hkv, shuffle_seed=3)
+    c.prepare_metadata(L)
+    c.begin_forward(L)
+    append_kv(torch.from_numpy(k).to(DEV), torch.from_numpy(v).to(DEV), c, 0)
+    o = ops.prefill_with_paged_kv_cache(torch.from_numpy(q).to(DEV), c.kv_cache.buf_layer(0),
+                                        c.kv_indices_with_last, len(c.kv_cache.indicies),
+                                        c.kv_cache.last_page_len, layout).cpu().numpy()
+    ref = sim.causal_prefill_rows(q, np.repeat(k, group, axis=1), np.repeat(v, group, axis=1))
+    assert np.abs(o.astype(np.float32) - ref).max() <= 2e-3
