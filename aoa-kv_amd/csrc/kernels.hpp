@@ -153,7 +153,7 @@ uint32_t partial_stride();
 uint32_t decode_max_chunks();  // split-K chunks per head the merge holds
 uint32_t topk_max_pages();     // pages per (sequence, head) top-k supports
 uint32_t fused_topk_max_pages();  // ... and the fused estimate + top-k kernel
-uint32_t layer_score_workers();   // scoring workgroups of the single-launch layer
+uint32_t layer_score_workers(uint32_t n_est, uint32_t est_chunks);  // one-launch layer scorers
 uint32_t counter_stride();        // u32 words between per-head counters (one cache line each)
 
 }  // namespace aoakv
