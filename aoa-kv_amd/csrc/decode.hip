@@ -108,10 +108,12 @@ __device__ __forceinline__ RadixResult radix_select(const uint32_t (&rel)[KPT], 
     const int w = hi < 8 ? hi : 8;
     const int sft = hi - w;
     const uint32_t hmask = hi >= 32 ? 0u : ~0u << hi;
+    // every key adds 1 to its bin if it takes part, else 0: no per-key
+    // branch (keys that do not take part land on scattered bins)
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
-      if (((free_mask >> j) & (Mask)1) && ((rel[j] ^ prefix) & hmask) == 0u)
-        atomicAdd(&sh.hist[buf][(rel[j] >> sft) & ((1u << w) - 1u)], 1u);
+      const bool part = ((free_mask >> j) & (Mask)1) && ((rel[j] ^ prefix) & hmask) == 0u;
+      atomicAdd(&sh.hist[buf][(rel[j] >> sft) & ((1u << w) - 1u)], part ? 1u : 0u);
     }
     const uint32_t nxt = buf == 2u ? 0u : buf + 1u;
     sh.hist[nxt][tid] = 0u;
@@ -196,18 +198,17 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
       sv[m] = ld_agent(scores + i);
       iv[m] = kv_ids[i];
     }
+    // no per-key branch: entries past P (inside the staging arrays, which
+    // hold 256 * KPT) are written too and never read as valid keys
 #pragma unroll
     for (int m = 0; m < KPT; ++m) {
       const uint32_t i = tid + (uint32_t)m * kThreads;
-      if (i < P) {
-        const uint32_t kk = order_key(sv[m]);
-        sh.key[i] = kk;
-        sh.id[i] = iv[m];
-        if (is_free(i)) {
-          kmin = kk < kmin ? kk : kmin;
-          kmax = kk > kmax ? kk : kmax;
-        }
-      }
+      const uint32_t kk = order_key(sv[m]);
+      sh.key[i] = kk;
+      sh.id[i] = iv[m];
+      const bool use = i < P && is_free(i);
+      kmin = use && kk < kmin ? kk : kmin;
+      kmax = use && kk > kmax ? kk : kmax;
     }
   } else {
 #pragma unroll
@@ -251,10 +252,9 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
   for (int j = 0; j < KPT; ++j) {
     const uint32_t i = i0 + j;
     rel[j] = key[j] - kmin;
-    if ((uint32_t)j < kpt && i < P) {
-      valid_mask |= (Mask)1 << j;
-      if (is_free(i)) free_mask |= (Mask)1 << j;
-    }
+    const bool v = (uint32_t)j < kpt && i < P;
+    valid_mask |= (Mask)v << j;
+    free_mask |= (Mask)(v && is_free(i)) << j;
   }
   // >= 1: k == 0 returned above, and with fixed forcing k >= 3 > nforced
   const RadixResult rr = radix_select<KPT, Mask>(rel, free_mask, kmax - kmin, k - nforced, sh);
@@ -266,10 +266,10 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
   Mask above_m = 0, eq_m = 0;
 #pragma unroll
   for (int j = 0; j < KPT; ++j) {
-    if (!((valid_mask >> j) & 1u)) continue;
+    const bool v = (valid_mask >> j) & 1u, f = (free_mask >> j) & 1u;
     const uint32_t r = rel[j] & rr.hmask;
-    if (!((free_mask >> j) & 1u) || r > rr.thr) above_m |= (Mask)1 << j;
-    else if (r == rr.thr) eq_m |= (Mask)1 << j;
+    above_m |= (Mask)(v && (!f || r > rr.thr)) << j;
+    eq_m |= (Mask)(v && f && r == rr.thr) << j;
   }
   // one scan of (pages above, bucket pages) packed in 16-bit halves gives the
   // output position: selected pages before mine = above before + min(bucket
@@ -277,6 +277,19 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
   const uint32_t na = (uint32_t)__builtin_popcountll((uint64_t)above_m);
   const uint32_t ne = (uint32_t)__builtin_popcountll((uint64_t)eq_m);
   const uint32_t packed = na | (ne << 16);
+  // this thread's page ids, read before the barrier below (after it, the id
+  // array takes the discarded writes of the compaction)
+  int32_t myid[kStaged ? KPT : 1];
+  if constexpr (kStaged) {
+#pragma unroll
+    for (int c = 0; c < KPT / 4; ++c) {
+      const int4 v = *reinterpret_cast<const int4*>(&sh.id[i0 + 4u * c]);
+      myid[4 * c + 0] = v.x;
+      myid[4 * c + 1] = v.y;
+      myid[4 * c + 2] = v.z;
+      myid[4 * c + 3] = v.w;
+    }
+  }
   const uint32_t incl = wave_incl_scan(packed);
   if (lane == kWave - 1) sh.s4[wave] = incl;
   __syncthreads();
@@ -287,14 +300,18 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
   uint32_t pos = (before & 0xFFFFu) + (eq_before < rr.kr ? eq_before : rr.kr);
   uint32_t eq_rank = eq_before;
   if constexpr (kStaged) {
-    // every key read from sh.key finished before the barrier above, so
-    // sh.key takes the compacted output
+    // every key and id read from LDS finished before the barrier above, so
+    // sh.key takes the compacted output and sh.id[tid] the discarded writes
+    // (every key writes somewhere: no per-key branch)
     uint32_t* s_out = sh.key;
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
-      bool take = (above_m >> j) & 1u;
-      if ((eq_m >> j) & 1u) take = rr.take_bucket || eq_rank++ < rr.kr;
-      if (take) s_out[pos++] = (uint32_t)sh.id[i0 + j];
+      const bool eq = (eq_m >> j) & 1u;
+      const bool take = ((above_m >> j) & 1u) || (eq && (rr.take_bucket || eq_rank < rr.kr));
+      eq_rank += eq ? 1u : 0u;
+      uint32_t* dst = take ? &s_out[pos] : reinterpret_cast<uint32_t*>(&sh.id[tid]);
+      *dst = (uint32_t)myid[j];
+      pos += take ? 1u : 0u;
     }
     __syncthreads();
     for (uint32_t i = tid; i < k; i += kThreads) put(i, (int32_t)s_out[i]);
