@@ -47,6 +47,7 @@ constexpr int kPfTileKeys = 64;
 constexpr int kPfRowBytes = kHeadDim * 2;                   // one key row
 constexpr int kPfTileBytes = kPfTileKeys * kPfRowBytes;     // 16 KB
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr uint32_t kXcds = 8;  // MI355X: 8 XCDs, workgroups dealt to them round-robin
 
 __device__ inline floatx16 mfma32(const half8& a, const half8& b, const floatx16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -77,11 +78,19 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int g = lane / 32;      // lane group
   const int c = lane % 32;      // query column of this lane
-  const uint32_t h = blockIdx.y;           // query head
-  const uint32_t hkv = h / (a.Hq / a.H);   // its kv head (GQA groups share K/V)
-  const uint32_t nqt = gridDim.x;
-  const uint32_t qt = nqt - 1u - blockIdx.x;  // heaviest query tiles first
   const uint32_t L = a.L, Lq = a.Lq;
+  const uint32_t nqt = (Lq + kPfQueriesPerBlock - 1) / kPfQueriesPerBlock;
+  // XCD-aware work order.  Workgroup b runs on XCD b % 8, and each XCD has
+  // its own L2, so XCD x takes the contiguous range [x * per, (x+1) * per)
+  // of the head-major item list: all query tiles of a head (and of the
+  // query heads that share its kv head) run on one XCD, whose L2 then holds
+  // that head's K/V for all of them.  Within a head, heaviest tiles first.
+  const uint32_t per = (nqt * a.Hq + kXcds - 1) / kXcds;
+  const uint32_t item = (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+  if (item >= nqt * a.Hq) return;  // block-uniform: the last XCD's range is short
+  const uint32_t h = item / nqt;           // query head
+  const uint32_t hkv = h / (a.Hq / a.H);   // its kv head (GQA groups share K/V)
+  const uint32_t qt = nqt - 1u - item % nqt;  // heaviest query tiles first
   const uint32_t off = L - Lq;                 // position of query 0
   const uint32_t npages = (L + kPageSize - 1) / kPageSize;
 
@@ -313,7 +322,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
 
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t s) {
   const uint32_t nqt = (a.Lq + kPfQueriesPerBlock - 1) / kPfQueriesPerBlock;
-  hipLaunchKernelGGL(prefill_kernel, dim3(nqt, a.Hq), dim3(kPfThreads), 0, s, a);
+  const uint32_t per = (nqt * a.Hq + kXcds - 1) / kXcds;
+  hipLaunchKernelGGL(prefill_kernel, dim3(per * kXcds), dim3(kPfThreads), 0, s, a);
   return hipGetLastError();
 }
 
