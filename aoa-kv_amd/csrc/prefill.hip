@@ -53,6 +53,18 @@ __device__ inline floatx16 mfma32(const half8& a, const half8& b, const floatx16
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// This lane's value and lane l^32's, combined: v_permlane32_swap exchanges
+// the two halves of the wave in registers, where __shfl_xor would go through
+// the LDS unit (ds_bpermute) and queue behind the tile reads.
+__device__ inline float pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // row of accumulator register i for lane group g
 __device__ inline int crow(int i, int g) { return 8 * (i / 4) + 4 * g + (i % 4); }
 
@@ -218,7 +230,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
       for (int i = 0; i < 16; ++i) mt = fmaxf(mt, acc_s[ks][i]);
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    mt = pair_max(mt);
     // Lazy rescaling: the reference max m_run moves only when some query's
     // tile max exceeds it by more than 2^8 in probability (the first tile
     // always moves it: every query sees key 0 there).  Otherwise
@@ -239,7 +251,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
         pb[ks][i / 8][i % 8] = (f16)p;
       }
     }
-    lt += __shfl_xor(lt, 32);
+    lt = pair_sum(lt);
     if (move) {  // the reference moved for some query: rescale
       const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale);  // m_run = -inf: 0
       l_run = l_run * alpha;
