@@ -592,6 +592,7 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopkArgs a) {
 struct DecShared {
   float o[4][kHeadDim];
   float ml[4][2];
+  float own[kHeadDim + 2];  // the merging block's own partial (one-launch layer)
   uint32_t sel[kDecPagesPerBlock];
   uint32_t last;
 };
@@ -808,13 +809,17 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
     }
     // slots 0..127: o; slot 128: m; slot 129: l
     const float val = d == (uint32_t)kHeadDim ? M : acc;
-    if (HANDOFF) st_agent_u32(a.hpart + part_off + d, to_word(val));
-    else st_agent(a.partial + part_off + d, val);
+    // the one-launch merging block (the head's last chunk) keeps its own
+    // partial in LDS: no store, no poll of it
+    if (!HANDOFF) st_agent(a.partial + part_off + d, val);
+    else if (chunk == nch - 1u) sm.own[d] = val;
+    else st_agent_u32(a.hpart + part_off + d, to_word(val));
   }
 
   // ---- one block of this (sequence, head) merges the chunks
   if (HANDOFF) {
     if (chunk != nch - 1u) return;  // the head's last chunk
+    __syncthreads();                // its own partial is in LDS
   } else {
     if (!arrive_last(&a.counters[bh * kCounterStride], nch, &sm.last)) return;
   }
@@ -823,10 +828,24 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   // used (one memory round trip per group; handoff words are re-polled until
   // written); thread t sums dim t%128 over the chunks of parity t/128, with
   // the group max folded in online
+  // the head's last chunk (nch - 1) is folded in after the others: in the
+  // one-launch layer it is the merging block's own partial, from LDS
   const uint32_t d = threadIdx.x % kHeadDim, half = threadIdx.x / kHeadDim;
+  const uint32_t nm = nch - 1u;  // chunks merged from memory
+  float lm, ll, lo;              // the last chunk's m, l, o[d]
+  if (HANDOFF) {
+    lm = sm.own[kHeadDim];
+    ll = sm.own[kHeadDim + 1];
+    lo = sm.own[d];
+  } else {
+    const size_t at = base + (size_t)nm * kPartialStride;
+    lm = ld_agent(a.partial + at + kHeadDim);
+    ll = ld_agent(a.partial + at + kHeadDim + 1);
+    lo = ld_agent(a.partial + at + d);
+  }
   float M = -INFINITY, Lsum = 0.f, acc = 0.f;
-  for (uint32_t g0 = 0; g0 < nch; g0 += 16u) {
-    const uint32_t ng = nch - g0 < 16u ? nch - g0 : 16u;
+  for (uint32_t g0 = 0; g0 < nm; g0 += 16u) {
+    const uint32_t ng = nm - g0 < 16u ? nm - g0 : 16u;
     const size_t gb = base + (size_t)g0 * kPartialStride;
     // unconditional loads of clamped chunk indices, masked after
     uint32_t mw[16], lw[16], ow[8];
@@ -901,6 +920,15 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc = acc + mv[half + 2 * i] * ov[i];
     M = Mn;
+  }
+  {  // the last chunk
+    const float Mn = fmaxf(M, lm);
+    const float keep = M == -INFINITY ? 0.f : __expf(M - Mn);
+    Lsum = Lsum * keep;
+    acc = acc * keep;
+    const float w = lm == -INFINITY ? 0.f : __expf(lm - Mn);
+    Lsum = Lsum + w * ll;
+    if (half == (nm & 1u)) acc = acc + w * lo;  // the half that sums its parity
   }
   if (half == 1u) s_o[0][d] = acc;
   __syncthreads();
