@@ -230,22 +230,26 @@ def ragged_batch_bench(dev, layout, reps=20):
     scores = torch.empty((Bn, H, maxP), dtype=torch.float32, device=dev)
     sel = torch.empty((Bn, H, kmax), dtype=torch.int32, device=dev)
     ws = ops.decode_workspace(Bn, H, H, kmax, dev)
-    call = lambda: ops.sparse_decode_layer(q, o, kv, kv_indptr, kv_indices, lpl, meta, m_indptr,
-                                           m_indices, lvn, scores, sel, 0, ws, maxP, layout,
-                                           token_budgets=tb)
-    call()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        call()
-    e1.record()
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / reps
     nbytes = sum(H * Pb * (2 * D * 2 + 2) + H * kb * S * D * 2 * 2 + 2 * H * kb * 4 + 3 * H * D * 2
                  for Pb, kb in zip(Ps, ks))
-    return {"us_per_batch_layer": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
-            "bytes": int(nbytes), "contexts": Ls, "pages_selected": ks}
+    out = {"bytes": int(nbytes), "contexts": Ls, "pages_selected": ks}
+    base = ops.FLAG_VALUE_AWARE | ops.FLAG_FIXED
+    for name, flags in (("two_launch", base), ("one_launch", base | ops.FLAG_SINGLE_LAUNCH)):
+        call = lambda: ops.sparse_decode_layer(q, o, kv, kv_indptr, kv_indices, lpl, meta,
+                                               m_indptr, m_indices, lvn, scores, sel, 0, ws, maxP,
+                                               layout, flags, token_budgets=tb)
+        call()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            call()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        out[f"us_per_batch_layer_{name}"] = round(us, 2)
+        out[f"GBps_{name}"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+    return out
 
 
 def cpu_baseline(k0, v0, q0, reps):
