@@ -541,6 +541,7 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
     la.est_chunks = aoakv::est_chunks(max_pages);
     la.n_est = batch_size * num_kv_heads * la.est_chunks;
     la.n_workers = aoakv::layer_score_workers(la.n_est, la.est_chunks);
+    la.stagger = aoakv::layer_stagger_cycles(la.est_chunks);
     la.n_heads = batch_size * num_kv_heads;
     la.n_dec = batch_size * num_qo_heads * da.max_chunks;
     return hip_status(aoakv::launch_layer(la, s), "sparse_decode_layer");

@@ -992,6 +992,11 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
   __shared__ uint32_t s_ok;
   const uint32_t t = blockIdx.x;
   if (t < la.n_workers) {
+    {  // first item's head bh0 starts bh0 * stagger cycles in (see layer_stagger_cycles)
+      const unsigned long long t0 = clock64();
+      const unsigned long long wait = (unsigned long long)(t / la.est_chunks) * la.stagger;
+      while (clock64() - t0 < wait) __builtin_amdgcn_s_sleep(1);
+    }
     for (uint32_t i = t; i < la.n_est; i += la.n_workers) {
       const uint32_t bh = i / la.est_chunks, chunk = i % la.est_chunks;
       const uint32_t b = bh / la.e.Hkv, h = bh % la.e.Hkv;
@@ -1124,6 +1129,21 @@ uint32_t layer_score_workers(uint32_t n_est, uint32_t est_chunks) {
   uint32_t w = n_est > last_round ? n_est - last_round : 256u;
   w = w < 256u ? 256u : w;
   return w > 448u ? 448u : w;
+}
+// The scoring workers of the first round would otherwise issue all their
+// loads at once, and HBM would finish every head's chunks at about the same
+// time, late (a head is done when its last chunk is).  Starting head h's
+// workers h * stagger cycles in, a little faster than HBM streams one head's
+// metadata (est_chunks * 128 pages * 514 B at 2,800 B per core cycle, ~6.7
+// TB/s at 2.4 GHz, so the memory queue never runs dry), finishes the heads
+// one after another, so the top-k, gathers and merge of the first heads
+// overlap the scoring of the later ones.  Config 2 (16 chunks per head), us
+// per layer by cycles per head: none 24.95, 300: 24.7, 350: 24.42, 376:
+// 24.37, 400: 24.42-24.5, 421: 24.7, 450: 25.2, 700: 26.4.
+uint32_t layer_stagger_cycles(uint32_t est_chunks) {
+  constexpr uint32_t kChunkBytes = kEstPagesPerBlock * (2u * kHeadDim * 2u + 2u);
+  constexpr uint32_t kStreamBytesPerCycle = 2800u;
+  return (uint32_t)((uint64_t)est_chunks * kChunkBytes / kStreamBytesPerCycle);
 }
 uint32_t counter_stride() { return kCounterStride; }
 
