@@ -738,9 +738,11 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
     for (int i = 0; i < 4; ++i) vv[s][i] = ld16(a.kv + vbase + (size_t)(i * 4 + row) * a.g.tok);
   }
   __builtin_amdgcn_sched_barrier(0);
-  float qf[kVec];
+  // q as four fp16 pairs: each logit term pair is one v_dot2_f32_f16
+  // (exact fp16 products, fp32 sum)
+  half2v q2[kVec / 2];
 #pragma unroll
-  for (int j = 0; j < kVec; ++j) qf[j] = (float)qq.v[j];
+  for (int m = 0; m < kVec / 2; ++m) q2[m] = half_pair(qq, m);
   // tokens per page: the sequence's last page holds lpl of them
   if constexpr (!QUEST) last_phys = (uint32_t)a.kv_indices[pbeg + P - 1u];
   uint32_t ntok[kDecPagesPerWave];
@@ -757,7 +759,8 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
     for (int i = 0; i < 4; ++i) {
       float acc = 0.f;
 #pragma unroll
-      for (int j = 0; j < kVec; ++j) acc = acc + qf[j] * (float)kk[s][i].v[j];
+      for (int m = 0; m < kVec / 2; ++m)
+        acc = __builtin_amdgcn_fdot2(q2[m], half_pair(kk[s][i], m), acc, false);
       acc = row_sum16(acc);
       const float lg = (float)r16((float)r16(acc) / kSqrtHeadDim);
       const uint32_t t = i * 4 + row;
@@ -777,8 +780,9 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
       for (int i = 0; i < 4; ++i) {
         const float p = __expf(x[s][i] - m);
         lsum = lsum + p;
+        // one mixed-precision FMA per dim (fp16 V converted in the FMA)
 #pragma unroll
-        for (int j = 0; j < kVec; ++j) o[j] = o[j] + p * (float)vv[s][i].v[j];
+        for (int j = 0; j < kVec; ++j) o[j] = __builtin_fmaf(p, (float)vv[s][i].v[j], o[j]);
       }
     }
   }

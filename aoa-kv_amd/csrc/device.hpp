@@ -65,6 +65,9 @@ __device__ inline H8 ld16(const f16* p) {
 __device__ inline void st16(f16* p, const H8& x) {
   *reinterpret_cast<uint4*>(p) = __builtin_bit_cast(uint4, x);
 }
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+// elements 2m, 2m+1 of x (one 32-bit register)
+__device__ inline half2v half_pair(const H8& x, int m) { return half2v{x.v[2 * m], x.v[2 * m + 1]}; }
 
 // ---------------------------------------------------------------- DPP / shuffles
 
