@@ -410,12 +410,22 @@ __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, ui
   const uint32_t mp0 = (uint32_t)a.meta_indices[mbeg + pl0 / kPageSize];
   const uint32_t mp1 = (uint32_t)a.meta_indices[mbeg + pl1 / kPageSize];
 
-  float qf[GROUP][kVec];
+  // Per dim, the larger of q*Kmax and q*Kmin is q*Kmax where q >= 0 and
+  // q*Kmin where q < 0 (Kmax >= Kmin; fp16 products are exact in fp32).  So
+  // each pair of dims is one byte permute that picks Kmax or Kmin by the
+  // sign of q (a lane-constant selector) and one v_dot2_f32_f16.  Sums start
+  // at +0, so a page whose terms are all zero scores +0 as with fmaxf.
+  half2v q2[GROUP][kVec / 2];
+  uint32_t psel[GROUP][kVec / 2];  // v_perm_b32 selectors: src0 = Kmax, src1 = Kmin
 #pragma unroll
   for (int g = 0; g < GROUP; ++g) {
     const H8 qq = ld16(a.q + ((size_t)b * a.Hq + h * GROUP + g) * kHeadDim + d0);
 #pragma unroll
-    for (int j = 0; j < kVec; ++j) qf[g][j] = (float)qq.v[j];
+    for (int m = 0; m < kVec / 2; ++m) {
+      q2[g][m] = half_pair(qq, m);
+      const bool lo = !((float)qq.v[2 * m] < 0.f), hi = !((float)qq.v[2 * m + 1] < 0.f);
+      psel[g][m] = (lo ? 0x0504u : 0x0100u) | (hi ? 0x07060000u : 0x03020000u);
+    }
   }
 
   constexpr int kSteps = kEstPagesPerWave / 4;
@@ -439,10 +449,11 @@ __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, ui
     for (int g = 0; g < GROUP; ++g) {
       float acc = 0.f;
 #pragma unroll
-      for (int j = 0; j < kVec; ++j) {
-        const float u = qf[g][j] * (float)kmx[s].v[j];
-        const float w = qf[g][j] * (float)kmn[s].v[j];
-        acc = acc + fmaxf(u, w);
+      for (int m = 0; m < kVec / 2; ++m) {
+        const uint32_t kx = __builtin_bit_cast(uint32_t, half_pair(kmx[s], m));
+        const uint32_t kn = __builtin_bit_cast(uint32_t, half_pair(kmn[s], m));
+        const half2v kb = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(kx, kn, psel[g][m]));
+        acc = __builtin_amdgcn_fdot2(q2[g][m], kb, acc, false);
       }
       x[g] = row_sum16(acc);
     }
