@@ -773,7 +773,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
       for (int m = 0; m < kVec / 2; ++m)
         acc = __builtin_amdgcn_fdot2(q2[m], half_pair(kk[s][i], m), acc, false);
       acc = row_sum16(acc);
-      const float lg = (float)r16((float)r16(acc) / kSqrtHeadDim);
+      const float lg = (float)r16(div_sqrt_head_dim_f16((float)r16(acc)));
       const uint32_t t = i * 4 + row;
       x[s][i] = t < ntok[s] ? lg : -INFINITY;
       mloc = fmaxf(mloc, x[s][i]);

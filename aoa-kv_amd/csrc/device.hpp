@@ -23,6 +23,7 @@ constexpr int kVec = 8;            // fp16 elements per lane per vector
 // sqrt(128) rounded to fp32: the simulation divides by math.sqrt(head_dim)
 // as an fp32 true division (filter_util.py:329, quest_attention.py:268).
 constexpr float kSqrtHeadDim = 11.313708498984761f;
+constexpr float kRcpSqrtHeadDim = 1.0f / kSqrtHeadDim;  // fp32(1 / fp32(sqrt(128)))
 
 struct alignas(16) H8 {
   f16 v[8];
@@ -66,6 +67,17 @@ __device__ inline void st16(f16* p, const H8& x) {
   *reinterpret_cast<uint4*>(p) = __builtin_bit_cast(uint4, x);
 }
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// x / sqrt(128) in fp32, correctly rounded for every fp16 value x: the
+// reciprocal product plus one Newton correction gives the rounded quotient
+// for all finite fp16 inputs (exhaustive check in tests/test_oracle.py) but
+// the sign of a zero, which copysign restores; inf and NaN take the product.
+// Three VALU operations where the IEEE division sequence takes about ten.
+__device__ inline float div_sqrt_head_dim_f16(float x) {
+  const float q0 = x * kRcpSqrtHeadDim;
+  const float q1 = __builtin_fmaf(__builtin_fmaf(-q0, kSqrtHeadDim, x), kRcpSqrtHeadDim, q0);
+  return __builtin_isfinite(x) ? __builtin_copysignf(q1, x) : q0;
+}
 // elements 2m, 2m+1 of x (one 32-bit register)
 __device__ inline half2v half_pair(const H8& x, int m) { return half2v{x.v[2 * m], x.v[2 * m + 1]}; }
 

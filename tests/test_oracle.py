@@ -429,3 +429,29 @@ def test_rope_planted_mistakes_fail_the_hf_check():
     unwrapped = xf * np.cos(a2) + rot * np.sin(a2)
     for bad in (wrong_sign, unwrapped, sim.apply_rope(x, pos, 1.0, 1e-4)):
         assert np.abs(bad - good).max() > 0.05
+
+
+def _fma32(a, b, c):
+    """fp32 fused multiply-add: a*b is exact in float64 for fp32 a, b, and
+    for the operands below the float64 sum rounds as the fused result does."""
+    return (a.astype(np.float64) * b.astype(np.float64) + c.astype(np.float64)).astype(np.float32)
+
+
+def test_logit_division_by_sqrt_head_dim_is_exact_for_every_fp16():
+    """The decode kernel divides each fp16 logit by sqrt(128) with a
+    reciprocal product and one Newton step (device.hpp,
+    div_sqrt_head_dim_f16).  Over every finite fp16 value that equals the
+    IEEE fp32 quotient, and so fp16(fp16(q.k)/sqrt(d)) of the simulation
+    (quest_attention.py:265-268), once the sign of a zero is restored."""
+    x = np.arange(65536, dtype=np.uint16).view(np.float16)
+    x = x[np.isfinite(x)].astype(np.float32)
+    c = np.float32(math.sqrt(128.0))
+    assert c == np.float32(11.313708498984761)
+    r = np.float32(1.0) / c
+    q0 = (x * r).astype(np.float32)
+    q1 = _fma32(_fma32(-q0, np.full_like(x, c), x), np.full_like(x, r), q0)
+    q1 = np.copysign(q1, x)
+    ref = (x / c).astype(np.float32)
+    assert np.array_equal(q1.view(np.uint32), ref.view(np.uint32))
+    # a plain reciprocal product is not enough (the step matters)
+    assert not np.array_equal(q0.astype(np.float16).view(np.uint16), ref.astype(np.float16).view(np.uint16))
