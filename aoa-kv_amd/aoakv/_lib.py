@@ -38,6 +38,7 @@ SIGNATURES = {
     "aoakv_topk_filtering": [_p, _u32, _p, _p, _p, _u32, _p, _p, _u32, _u32, _u32, _u32,
                              _u32, _p],
     "aoakv_decode_workspace_size": [_u32, _u32, _u32, _u32, _u32],
+    "aoakv_layer_workspace_size": [_u32, _u32, _u32, _u32, _u32, _u32],
     "aoakv_workspace_init": [_p, _sz, _p],
     "aoakv_decode_sparse_attn": [_p, _p, _p, _p, _p, _p, _p, _u32, _u32, _p, _p, _sz, _u32,
                                  _u32, _u32, _u32, _u32, _u32, _u32, _u32, _p],
@@ -56,6 +57,7 @@ _RESTYPES = {
     "aoakv_last_error": ctypes.c_char_p,
     "aoakv_version": ctypes.c_char_p,
     "aoakv_decode_workspace_size": _sz,
+    "aoakv_layer_workspace_size": _sz,
 }
 
 

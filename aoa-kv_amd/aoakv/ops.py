@@ -181,11 +181,16 @@ def topk_filtering(scores, kv_indptr, kv_indices, kv_last_page_len, token_budget
 
 
 def decode_workspace(batch: int, num_qo_heads: int, num_kv_heads: int, max_sel_pages: int,
-                     device="cuda") -> torch.Tensor:
+                     device="cuda", max_pages: int = 0) -> torch.Tensor:
     """Caller-owned decode workspace (replaces BatchDecodeHandler's buffers,
-    decode_handler.cuh:73-136), counters zeroed."""
-    n = _lib.load().aoakv_decode_workspace_size(batch, num_qo_heads, num_kv_heads, 128,
-                                                 max_sel_pages)
+    decode_handler.cuh:73-136), zeroed.  With max_pages it also holds the
+    one-launch layer's score handoff words (aoakv_layer_workspace_size)."""
+    lib = _lib.load()
+    if max_pages:
+        n = lib.aoakv_layer_workspace_size(batch, num_qo_heads, num_kv_heads, 128, max_sel_pages,
+                                           max_pages)
+    else:
+        n = lib.aoakv_decode_workspace_size(batch, num_qo_heads, num_kv_heads, 128, max_sel_pages)
     ws = torch.empty(n, dtype=torch.uint8, device=device)
     _lib.call("aoakv_workspace_init", ws.data_ptr(), n, _stream())
     return ws

@@ -84,7 +84,7 @@ class InferenceController:
         self._sel = torch.empty((1, self.num_kv_heads, max_kv_pages), dtype=torch.int32,
                                 device=device)
         self.workspace = ops.decode_workspace(1, num_heads, self.num_kv_heads, max_kv_pages,
-                                              device)
+                                              device, max_pages=max_kv_pages)
 
     # ------------------------------------------------------------ budget
     @property

@@ -412,6 +412,19 @@ size_t aoakv_decode_workspace_size(uint32_t batch_size, uint32_t num_qo_heads,
   return ws_layout(batch_size, num_qo_heads, num_kv_heads, max_sel_pages, nullptr, nullptr);
 }
 
+// The one-launch layer's score handoff words follow the decode workspace's
+// regions: B * Hkv * max_pages words, 256-byte aligned.
+static size_t score_words_offset(size_t decode_bytes) { return round_up(decode_bytes, 256); }
+
+size_t aoakv_layer_workspace_size(uint32_t batch_size, uint32_t num_qo_heads,
+                                  uint32_t num_kv_heads, uint32_t head_dim,
+                                  uint32_t max_sel_pages, uint32_t max_pages) {
+  (void)head_dim;
+  const size_t dec = ws_layout(batch_size, num_qo_heads, num_kv_heads, max_sel_pages, nullptr,
+                               nullptr);
+  return score_words_offset(dec) + (size_t)batch_size * num_kv_heads * max_pages * 4u;
+}
+
 int aoakv_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
   REQUIRE(workspace, "workspace_init: null workspace");
   REQUIRE(workspace_bytes % 4u == 0u, "workspace_init: size not a multiple of 4");
@@ -538,6 +551,13 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
     la.d.hsel_stride = max_sel;
     la.d.hpart = w.hpart;
     la.d.error = w.ctl + 2;
+    // with room for them (aoakv_layer_workspace_size), the scores also go to
+    // the top-k as handoff words, polled directly (no arrival counter)
+    const size_t words_off = score_words_offset(w.bytes);
+    if (workspace_bytes >= words_off + (size_t)batch_size * num_kv_heads * max_pages * 4u) {
+      la.e.hscore = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + words_off);
+      la.e.hscore_stride = max_pages;
+    }
     la.est_chunks = aoakv::est_chunks(max_pages);
     la.n_est = batch_size * num_kv_heads * la.est_chunks;
     la.n_workers = aoakv::layer_score_workers(la.n_est, la.est_chunks);

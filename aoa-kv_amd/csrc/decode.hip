@@ -68,6 +68,31 @@ __device__ inline uint32_t wave_reduce_u32(uint32_t v) {
 // top-k selection for one (sequence, kv head), one 256-thread block
 // ======================================================================
 
+// Bound on polls of a handoff word before a wait gives up (it then sets the
+// error flag and goes on with stand-in data, so every wave still exits).
+constexpr uint32_t kSpinLimit = 1u << 18;
+
+// Polls an agent-coherent handoff word until it is written (non-zero);
+// returns the value - 1, or 0 after kSpinLimit polls with *error set.
+__device__ inline uint32_t wait_word(const uint32_t* p, uint32_t* error) {
+  uint32_t v, it = 0u;
+  while ((v = ld_agent_u32(p)) == 0u) {
+    __builtin_amdgcn_s_sleep(1);
+    if (++it > kSpinLimit) {
+      atomicOr(error, 1u);
+      return 0u;
+    }
+  }
+  return v - 1u;
+}
+
+// A float as a handoff word: bits + 1, never 0 (the all-ones NaN pattern,
+// which arithmetic never produces, is stored as the canonical NaN).
+__device__ inline uint32_t to_word(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  return (u == 0xFFFFFFFFu ? 0x7FC00000u : u) + 1u;
+}
+
 // Pages whose scores and page ids are staged in LDS (16 per thread); longer
 // rows are read straight from global memory.
 constexpr uint32_t kStageMaxPages = 16u * kThreads;
@@ -159,7 +184,8 @@ template <int KPT>
 __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uint32_t P, uint32_t k,
                                            bool fixed, const int32_t* __restrict__ kv_ids,
                                            int32_t* __restrict__ out, TopkShared& sh,
-                                           uint32_t* hout, uint32_t hstride, uint32_t hcopies) {
+                                           uint32_t* hout, uint32_t hstride, uint32_t hcopies,
+                                           uint32_t* hwords = nullptr) {
   // page i of the output, also as id + 1 into the hcopies handoff rows
   auto put = [&](uint32_t i, int32_t id) {
     st_agent_i32(out + i, id);
@@ -172,6 +198,14 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = __lane_id();
   const uint32_t wave = tid / kWave;
+  if (hwords != nullptr && (k == 0u || k >= P)) {
+    // the scores are not needed, but their handoff words must be consumed
+    for (uint32_t i = tid; i < P; i += kThreads) {
+      for (uint32_t it = 0u; ld_agent_u32(hwords + i) == 0u && it < kSpinLimit; ++it)
+        __builtin_amdgcn_s_sleep(1);
+      st_agent_u32(hwords + i, 0u);
+    }
+  }
   if (k == 0u) return;  // (quest_kernel convention with a budget of one page)
   if (k >= P) {  // everything selected
     for (uint32_t i = tid; i < P; i += kThreads) put(i, kv_ids[i]);
@@ -191,12 +225,52 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
     // coalesced copy: all loads issued before any is used
     float sv[KPT];
     int32_t iv[KPT];
+    if (hwords == nullptr) {
 #pragma unroll
-    for (int m = 0; m < KPT; ++m) {  // unconditional loads of clamped indices
-      uint32_t i = tid + (uint32_t)m * kThreads;
-      i = i < P ? i : P - 1u;
-      sv[m] = ld_agent(scores + i);
-      iv[m] = kv_ids[i];
+      for (int m = 0; m < KPT; ++m) {  // unconditional loads of clamped indices
+        uint32_t i = tid + (uint32_t)m * kThreads;
+        i = i < P ? i : P - 1u;
+        sv[m] = ld_agent(scores + i);
+        iv[m] = kv_ids[i];
+      }
+    } else {
+      // page ids first, then this thread's score words, polled until the
+      // scoring items have written them, then cleared for the next launch
+      // (only the thread owning a word clears it; clamped reads of another
+      // thread's word are not used)
+      uint32_t w[KPT];
+#pragma unroll
+      for (int m = 0; m < KPT; ++m) {
+        uint32_t i = tid + (uint32_t)m * kThreads;
+        i = i < P ? i : P - 1u;
+        iv[m] = kv_ids[i];
+      }
+      auto load_words = [&]() {
+#pragma unroll
+        for (int m = 0; m < KPT; ++m) {
+          uint32_t i = tid + (uint32_t)m * kThreads;
+          i = i < P ? i : P - 1u;
+          w[m] = ld_agent_u32(hwords + i);
+        }
+      };
+      auto missing = [&]() {
+        bool z = false;
+#pragma unroll
+        for (int m = 0; m < KPT; ++m) z |= tid + (uint32_t)m * kThreads < P && w[m] == 0u;
+        return z;
+      };
+      load_words();
+      for (uint32_t it = 0u; missing(); ++it) {
+        if (it >= kSpinLimit) break;  // stand-in scores (the decode items' waits flag it)
+        __builtin_amdgcn_s_sleep(1);
+        load_words();
+      }
+#pragma unroll
+      for (int m = 0; m < KPT; ++m) {
+        const uint32_t i = tid + (uint32_t)m * kThreads;
+        if (i < P) st_agent_u32(hwords + i, 0u);
+        sv[m] = __builtin_bit_cast(float, w[m] - 1u);
+      }
     }
     // no per-key branch: entries past P (inside the staging arrays, which
     // hold 256 * KPT) are written too and never read as valid keys
@@ -330,13 +404,13 @@ __device__ __forceinline__ void topk_staged(const float* __restrict__ scores, ui
                                             bool fixed, const int32_t* __restrict__ kv_ids,
                                             int32_t* __restrict__ out, TopkShared& sh,
                                             uint32_t* hout = nullptr, uint32_t hstride = 0u,
-                                            uint32_t hcopies = 0u) {
+                                            uint32_t hcopies = 0u, uint32_t* hwords = nullptr) {
   if (P <= 4u * kThreads)
-    topk_block<4>(scores, P, k, fixed, kv_ids, out, sh, hout, hstride, hcopies);
+    topk_block<4>(scores, P, k, fixed, kv_ids, out, sh, hout, hstride, hcopies, hwords);
   else if (P <= 8u * kThreads)
-    topk_block<8>(scores, P, k, fixed, kv_ids, out, sh, hout, hstride, hcopies);
+    topk_block<8>(scores, P, k, fixed, kv_ids, out, sh, hout, hstride, hcopies, hwords);
   else
-    topk_block<16>(scores, P, k, fixed, kv_ids, out, sh, hout, hstride, hcopies);
+    topk_block<16>(scores, P, k, fixed, kv_ids, out, sh, hout, hstride, hcopies, hwords);
 }
 
 // Pages per head the fused estimate + top-k kernel selects from (16 keys per
@@ -492,8 +566,12 @@ __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, ui
   {
     const uint32_t p = chunk * kEstPagesPerBlock + threadIdx.x;
     const uint32_t nstore = (a.flags & kFlagQuestKernel) ? P - 1u : P;
-    if (threadIdx.x < (uint32_t)kEstPagesPerBlock && p < nstore)
+    if (threadIdx.x < (uint32_t)kEstPagesPerBlock && p < nstore) {
       st_agent(out + p, s_sc[threadIdx.x]);
+      if (a.hscore != nullptr)
+        st_agent_u32(a.hscore + ((size_t)b * a.Hkv + h) * a.hscore_stride + p,
+                     to_word(s_sc[threadIdx.x]));
+    }
   }
 
   return true;
@@ -535,9 +613,12 @@ __device__ __forceinline__ void select_item(const EstimateArgs& a, uint32_t b, u
   const uint32_t P = pl.P, k = pl.k, pbeg = pl.pbeg;
   const bool handoff = pl.handoff;
   uint32_t* hout = handoff ? a.hsel + ((size_t)b * a.Hq + h * GROUP) * a.hsel_stride : nullptr;
+  uint32_t* hwords =
+      a.hscore ? a.hscore + ((size_t)b * a.Hkv + h) * a.hscore_stride : nullptr;
   topk_staged(a.scores + ((size_t)b * a.Hkv + h) * a.score_stride, P, k,
               (a.flags & kFlagFixed) != 0u, a.kv_indices + pbeg,
-              a.sel + ((size_t)b * a.Hkv + h) * a.sel_stride, tk, hout, a.hsel_stride, GROUP);
+              a.sel + ((size_t)b * a.Hkv + h) * a.sel_stride, tk, hout, a.hsel_stride, GROUP,
+              hwords);
 }
 
 // Scores one chunk; with a.sel set, the last block of the head to finish
@@ -607,31 +688,6 @@ struct DecShared {
   uint32_t sel[kDecPagesPerBlock];
   uint32_t last;
 };
-
-// Bound on polls of a handoff word before a wait gives up (it then sets the
-// error flag and goes on with stand-in data, so every wave still exits).
-constexpr uint32_t kSpinLimit = 1u << 18;
-
-// Polls an agent-coherent handoff word until it is written (non-zero);
-// returns the value - 1, or 0 after kSpinLimit polls with *error set.
-__device__ inline uint32_t wait_word(const uint32_t* p, uint32_t* error) {
-  uint32_t v, it = 0u;
-  while ((v = ld_agent_u32(p)) == 0u) {
-    __builtin_amdgcn_s_sleep(1);
-    if (++it > kSpinLimit) {
-      atomicOr(error, 1u);
-      return 0u;
-    }
-  }
-  return v - 1u;
-}
-
-// A float as a handoff word: bits + 1, never 0 (the all-ones NaN pattern,
-// which arithmetic never produces, is stored as the canonical NaN).
-__device__ inline uint32_t to_word(float x) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, x);
-  return (u == 0xFFFFFFFFu ? 0x7FC00000u : u) + 1u;
-}
 
 // Attends pages [8*chunk, 8*chunk + 8) of the selection of (sequence b,
 // query head hq) and merges the head's chunks.
@@ -1016,13 +1072,19 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
       const uint32_t bh = i / la.est_chunks, chunk = i % la.est_chunks;
       const uint32_t b = bh / la.e.Hkv, h = bh % la.e.Hkv;
       if (score_item<GROUP>(la.e, b, h, chunk, sm.e.e)) {
-        // the scores are stored once the memory counter drains; the barrier
-        // also ends this item's use of LDS before the next item's
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (threadIdx.x == 0)
-          __hip_atomic_fetch_add(la.e.counters + bh * kCounterStride, 1u, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
+        if (la.e.hscore != nullptr) {
+          // the scores went out as handoff words: only end this item's use
+          // of LDS before the next item's
+          __syncthreads();
+        } else {
+          // the scores are stored once the memory counter drains; the
+          // barrier also ends this item's use of LDS before the next item's
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          __syncthreads();
+          if (threadIdx.x == 0)
+            __hip_atomic_fetch_add(la.e.counters + bh * kCounterStride, 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
     }
   } else if (t < la.n_workers + la.n_heads) {
@@ -1033,6 +1095,10 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
     if (P == 0u) return;
     const uint32_t nch = (P + kEstPagesPerBlock - 1) / kEstPagesPerBlock;
     const SelPlan plan = plan_select(la.e, b);
+    if (la.e.hscore != nullptr) {  // the top-k polls the score words itself
+      select_item<GROUP>(la.e, b, h, plan, sm.e.tk);
+      return;
+    }
     if (threadIdx.x == 0) {
       uint32_t it = 0u, ok = 1u;
       while (ld_agent_u32(la.e.counters + bh * kCounterStride) < nch) {

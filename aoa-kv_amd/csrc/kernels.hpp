@@ -76,6 +76,11 @@ struct EstimateArgs {
   // (0 = not yet written), for the decode items of the same launch
   uint32_t* hsel;      // [B, Hq, hsel_stride] or nullptr
   uint32_t hsel_stride;
+  // single launch only, optional: the scores again as handoff words (bits +
+  // 1, 0 = not yet written), [B, Hkv, hscore_stride]; the top-k polls these
+  // instead of an arrival counter and clears them
+  uint32_t* hscore;
+  uint32_t hscore_stride;
 };
 
 struct TopkArgs {

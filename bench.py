@@ -229,7 +229,7 @@ def ragged_batch_bench(dev, layout, reps=20):
     o = torch.empty_like(q)
     scores = torch.empty((Bn, H, maxP), dtype=torch.float32, device=dev)
     sel = torch.empty((Bn, H, kmax), dtype=torch.int32, device=dev)
-    ws = ops.decode_workspace(Bn, H, H, kmax, dev)
+    ws = ops.decode_workspace(Bn, H, H, kmax, dev, max_pages=maxP)
     nbytes = sum(H * Pb * (2 * D * 2 + 2) + H * kb * S * D * 2 * 2 + 2 * H * kb * 4 + 3 * H * D * 2
                  for Pb, kb in zip(Ps, ks))
     out = {"bytes": int(nbytes), "contexts": Ls, "pages_selected": ks}
@@ -341,7 +341,7 @@ def main():
     scores = torch.zeros((n_layers, 1, H, P), dtype=torch.float32, device=dev)
     sel = torch.zeros((n_layers, 1, H, K_SEL), dtype=torch.int32, device=dev)
     o = torch.zeros((n_layers, 1, H, D), dtype=torch.float16, device=dev)
-    ws = ops.decode_workspace(1, H, H, K_SEL, dev)
+    ws = ops.decode_workspace(1, H, H, K_SEL, dev, max_pages=P)
     flags = ops.FLAG_VALUE_AWARE | ops.FLAG_FIXED
 
     def layer(l):

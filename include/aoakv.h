@@ -217,6 +217,19 @@ size_t aoakv_decode_workspace_size(uint32_t batch_size, uint32_t num_qo_heads,
                                    uint32_t max_sel_pages);
 
 /*
+ * Workspace bytes for aoakv_sparse_decode_layer with AOAKV_FLAG_SINGLE_LAUNCH
+ * at its fastest: the decode workspace plus one word per (sequence, kv head,
+ * page) through which the launch's scoring items hand their scores to its
+ * top-k (polled directly, no arrival counter).  A workspace of only
+ * aoakv_decode_workspace_size bytes still works (counter handoff).  No
+ * counterpart in the reference (its decode handler sizes its own buffers,
+ * decode_handler.cuh:73-136).
+ */
+size_t aoakv_layer_workspace_size(uint32_t batch_size, uint32_t num_qo_heads,
+                                  uint32_t num_kv_heads, uint32_t head_dim,
+                                  uint32_t max_sel_pages, uint32_t max_pages);
+
+/*
  * Zero the workspace's arrival counters.  Call once after allocating a
  * workspace (the kernels leave the counters at zero on exit).
  */

@@ -358,16 +358,24 @@ def _single_launch_matches(args, kwargs, o_ref, sel_ref, ws, reps=3):
     """The one-launch layer (FLAG_SINGLE_LAUNCH) repeats the two-launch result
     bit for bit, launch after launch, without its spin-wait error flag."""
     from aoakv import ops
-    o, sel = args[1], args[11]
-    for rep in range(reps):
-        o.fill_(0)
-        sel.fill_(-1)
-        ops.sparse_decode_layer(*args, **kwargs,
-                                flags=ops.FLAG_VALUE_AWARE | ops.FLAG_FIXED | ops.FLAG_SINGLE_LAUNCH)
-        torch.cuda.synchronize()
-        assert np.array_equal(bits(o.cpu().numpy()), bits(o_ref)), rep
-        assert np.array_equal(sel.cpu().numpy(), sel_ref), rep
-        assert int(ws[8:12].view(torch.int32).item()) == 0, "spin-wait error flag set"
+    o, sel, scores = args[1], args[11], args[10]
+    # the caller's workspace (scores handed over through an arrival counter)
+    # and one with room for the score handoff words
+    wsw = ops.decode_workspace(o.shape[0], o.shape[1], scores.shape[1], sel.shape[-1],
+                               max_pages=args[14])
+    for wsx in (ws, wsw):
+        argx = args[:13] + (wsx,) + args[14:]
+        for rep in range(reps):
+            o.fill_(0)
+            sel.fill_(-1)
+            ops.sparse_decode_layer(*argx, **kwargs,
+                                    flags=ops.FLAG_VALUE_AWARE | ops.FLAG_FIXED | ops.FLAG_SINGLE_LAUNCH)
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(o.cpu().numpy()), bits(o_ref)), rep
+            assert np.array_equal(sel.cpu().numpy(), sel_ref), rep
+            assert int(wsx[8:12].view(torch.int32).item()) == 0, "spin-wait error flag set"
+        # every launch leaves the whole workspace zeroed
+        assert int(wsx.count_nonzero().item()) == 0
 
 
 def test_batched_ragged_decode_matches_simulation():
