@@ -1199,17 +1199,18 @@ uint32_t topk_max_pages() { return kTopkMaxPages; }
 uint32_t fused_topk_max_pages() { return kFusedTopkMaxPages; }
 // Scoring workgroups of the one-launch layer.  Items are scored head by head
 // in rounds of n_workers; the heads of the last round finish last and their
-// top-k, gather and merge are exposed, so the last round is kept to about 4
-// heads (measured at config 2, 32 heads x 16 items: 256 workers 26.6 us,
-// 384 25.7, 448 25.4, 480 25.5, 512 27.4).  Between 256 (one per CU) and 448
-// (with the 32 top-k and 512 decode workgroups of config 2, 992 of the 1024
-// workgroups four per CU allow are resident together).
+// top-k, gather and merge are exposed, so the last round is kept to about 2
+// heads.  Measured at config 2 (32 heads x 16 items, staggered start, score
+// handoff words), us per layer by workers: 416: 23.41, 448: 23.32, 464:
+// 23.24, 480: 23.16, 496: 24.01, 512: 23.71.  Between 256 (one per CU) and
+// 480 (with the 32 top-k and 512 decode workgroups of config 2, all 1024
+// workgroups that four per CU allow are resident together).
 uint32_t layer_score_workers(uint32_t n_est, uint32_t est_chunks) {
   if (n_est <= 256u) return n_est;
-  const uint32_t last_round = 4u * est_chunks;
+  const uint32_t last_round = 2u * est_chunks;
   uint32_t w = n_est > last_round ? n_est - last_round : 256u;
   w = w < 256u ? 256u : w;
-  return w > 448u ? 448u : w;
+  return w > 480u ? 480u : w;
 }
 // The scoring workers of the first round would otherwise issue all their
 // loads at once, and HBM would finish every head's chunks at about the same
