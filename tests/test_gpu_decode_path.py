@@ -552,3 +552,47 @@ def test_workspace_shared_across_shrinking_selection_sizes():
         assert torch.equal(o1, o_ref) and torch.equal(sel1, sel_ref), rep
         assert int(ws[8:12].view(torch.int32).item()) == 0, "spin-wait error flag set"
     assert not torch.any(ws[256:].view(torch.int32) != 0), "workspace not left zero"
+
+
+@pytest.mark.parametrize("case", ["all_selected", "quest_one_page", "plain"])
+def test_one_launch_score_words_every_selection_shape(case):
+    """The one-launch layer with a workspace sized by
+    aoakv_layer_workspace_size hands its scores to the top-k as handoff
+    words.  The top-k must consume (wait for and clear) them whatever it
+    selects: nothing (the quest_kernel convention with a budget of one page),
+    everything (budget at or above the context), or a proper subset.
+    Outputs match the two-launch path bit for bit, no wait gives up, and the
+    whole workspace is zero again after every call."""
+    from aoakv import ops
+    _say(f"[score words] {case}")
+    # k = min(max(3, min(L, budget) // 16), P) reaches P only for L a multiple of 16
+    H, L = 8, (2016 if case == "all_selected" else 2000 + 7)
+    budget = {"all_selected": 4096, "quest_one_page": 16, "plain": 512}[case]
+    F = ops.FLAG_VALUE_AWARE | (ops.FLAG_QUEST_KERNEL if case == "quest_one_page" else ops.FLAG_FIXED)
+    q, K, V = _sim_state(77, H, L)
+    c = make_ctrl(H, L + 16, HND, budget, shuffle=77)
+    prefill(c, K, V)
+    c.begin_forward(1)
+    qd = torch.from_numpy(q[0, :, 0].copy()).to(DEV)[None]
+    P = len(c.kv_cache.indicies)
+    kcols = P
+    ws_words = ops.decode_workspace(1, H, H, kcols, max_pages=P)
+    ws_plain = ops.decode_workspace(1, H, H, kcols)
+
+    def layer(ws, flags):
+        o = torch.empty_like(qd)
+        sel = torch.full((1, H, kcols), -1, dtype=torch.int32, device=DEV)
+        ops.sparse_decode_layer(qd, o, c.kv_cache.buf_layer(0), c.kv_indptr_for_append,
+                                c.kv_indices_with_last, c.kv_last_page_len_t,
+                                c.metadata_cache.buf_layer(0), c.metadata_indptr_for_append,
+                                c.metadata_indices, c.v_log_norm_layer(0), c.scores, sel, budget,
+                                ws, P, HND, flags)
+        torch.cuda.synchronize()
+        return o, sel
+
+    o_ref, sel_ref = layer(ws_plain, F)  # two launches
+    for rep in range(3):
+        o1, sel1 = layer(ws_words, F | ops.FLAG_SINGLE_LAUNCH)
+        assert torch.equal(o1, o_ref) and torch.equal(sel1, sel_ref), rep
+        assert int(ws_words[8:12].view(torch.int32).item()) == 0, "spin-wait error flag set"
+        assert int(ws_words.count_nonzero().item()) == 0, "workspace not left zero"
