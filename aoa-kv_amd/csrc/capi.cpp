@@ -562,7 +562,10 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
     la.n_est = batch_size * num_kv_heads * la.est_chunks;
     la.n_workers = aoakv::layer_score_workers(la.n_est, la.est_chunks);
     la.stagger = aoakv::layer_stagger_cycles(la.est_chunks);
-    la.n_heads = batch_size * num_kv_heads;
+    // one query head per kv head and score words: each decode item selects
+    // its head's pages itself (no top-k workgroups, no selection handoff)
+    la.self_select = la.e.hscore != nullptr && num_qo_heads == num_kv_heads ? 1u : 0u;
+    la.n_heads = la.self_select ? 0u : batch_size * num_kv_heads;
     la.n_dec = batch_size * num_qo_heads * da.max_chunks;
     return hip_status(aoakv::launch_layer(la, s), "sparse_decode_layer");
   }

@@ -180,12 +180,18 @@ __device__ __forceinline__ RadixResult radix_select(const uint32_t (&rel)[KPT], 
 // with coalesced loads and the output is compacted in LDS and stored
 // coalesced; with KPT = 64 (rows up to 16384 pages) keys are read and the
 // output written per thread.
-template <int KPT>
+//
+// SELF (one-launch layer, one query head per kv head): every decode
+// workgroup of the head runs this same selection on the same score words.
+// The words are only read (the head's merging workgroup clears them), their
+// wait starts with one sentinel word per scoring chunk, and the output stays
+// in sh.key[0, k) for the caller (nothing is stored).
+template <int KPT, bool SELF = false>
 __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uint32_t P, uint32_t k,
                                            bool fixed, const int32_t* __restrict__ kv_ids,
                                            int32_t* __restrict__ out, TopkShared& sh,
                                            uint32_t* hout, uint32_t hstride, uint32_t hcopies,
-                                           uint32_t* hwords = nullptr) {
+                                           uint32_t* hwords = nullptr, uint32_t* error = nullptr) {
   // page i of the output, also as id + 1 into the hcopies handoff rows
   auto put = [&](uint32_t i, int32_t id) {
     st_agent_i32(out + i, id);
@@ -198,7 +204,7 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = __lane_id();
   const uint32_t wave = tid / kWave;
-  if (hwords != nullptr && (k == 0u || k >= P)) {
+  if (!SELF && hwords != nullptr && (k == 0u || k >= P)) {
     // the scores are not needed, but their handoff words must be consumed
     for (uint32_t i = tid; i < P; i += kThreads) {
       for (uint32_t it = 0u; ld_agent_u32(hwords + i) == 0u && it < kSpinLimit; ++it)
@@ -245,6 +251,20 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
         i = i < P ? i : P - 1u;
         iv[m] = kv_ids[i];
       }
+      if constexpr (SELF) {
+        // first the head's last score word alone, so that the workgroups
+        // waiting for a head poll one cache line each, not the whole row
+        // (512 workgroups polling every word, or one word per scoring chunk,
+        // cost 1.2 or 0.2 us per layer in memory traffic at config 2)
+        if (wave == 0u) {
+          const uint32_t* sw = hwords + (P - 1u);
+          for (uint32_t it = 0u; it < kSpinLimit; ++it) {
+            if (__builtin_amdgcn_ballot_w64(ld_agent_u32(sw) == 0u) == 0u) break;
+            __builtin_amdgcn_s_sleep(1);
+          }
+        }
+        __syncthreads();
+      }
       auto load_words = [&]() {
 #pragma unroll
         for (int m = 0; m < KPT; ++m) {
@@ -260,15 +280,20 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
         return z;
       };
       load_words();
-      for (uint32_t it = 0u; missing(); ++it) {
-        if (it >= kSpinLimit) break;  // stand-in scores (the decode items' waits flag it)
+      uint32_t it = 0u;
+      for (; missing(); ++it) {
+        if (it >= kSpinLimit) break;  // stand-in scores
         __builtin_amdgcn_s_sleep(1);
         load_words();
       }
+      // a wait that gave up is flagged here (SELF) or by the decode items'
+      // waits for this selection; the flag is set outside the poll loop (an
+      // atomic inside it made this loop's code 0.4 us per layer slower)
+      if (SELF && it >= kSpinLimit) atomicOr(error, 1u);
 #pragma unroll
       for (int m = 0; m < KPT; ++m) {
         const uint32_t i = tid + (uint32_t)m * kThreads;
-        if (i < P) st_agent_u32(hwords + i, 0u);
+        if (!SELF && i < P) st_agent_u32(hwords + i, 0u);
         sv[m] = __builtin_bit_cast(float, w[m] - 1u);
       }
     }
@@ -388,7 +413,8 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
       pos += take ? 1u : 0u;
     }
     __syncthreads();
-    for (uint32_t i = tid; i < k; i += kThreads) put(i, (int32_t)s_out[i]);
+    if (!SELF)
+      for (uint32_t i = tid; i < k; i += kThreads) put(i, (int32_t)s_out[i]);
   } else {
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
@@ -400,17 +426,22 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
 }
 
 // top-k of a row of P <= kStageMaxPages pages with the fewest keys per thread
+template <bool SELF = false>
 __device__ __forceinline__ void topk_staged(const float* __restrict__ scores, uint32_t P, uint32_t k,
                                             bool fixed, const int32_t* __restrict__ kv_ids,
                                             int32_t* __restrict__ out, TopkShared& sh,
                                             uint32_t* hout = nullptr, uint32_t hstride = 0u,
-                                            uint32_t hcopies = 0u, uint32_t* hwords = nullptr) {
+                                            uint32_t hcopies = 0u, uint32_t* hwords = nullptr,
+                                            uint32_t* error = nullptr) {
   if (P <= 4u * kThreads)
-    topk_block<4>(scores, P, k, fixed, kv_ids, out, sh, hout, hstride, hcopies, hwords);
+    topk_block<4, SELF>(scores, P, k, fixed, kv_ids, out, sh, hout, hstride, hcopies, hwords,
+                          error);
   else if (P <= 8u * kThreads)
-    topk_block<8>(scores, P, k, fixed, kv_ids, out, sh, hout, hstride, hcopies, hwords);
+    topk_block<8, SELF>(scores, P, k, fixed, kv_ids, out, sh, hout, hstride, hcopies, hwords,
+                          error);
   else
-    topk_block<16>(scores, P, k, fixed, kv_ids, out, sh, hout, hstride, hcopies, hwords);
+    topk_block<16, SELF>(scores, P, k, fixed, kv_ids, out, sh, hout, hstride, hcopies, hwords,
+                          error);
 }
 
 // Pages per head the fused estimate + top-k kernel selects from (16 keys per
@@ -699,12 +730,19 @@ struct DecShared {
 //     written; partials go to handoff words and the head's last chunk
 //     polls them and merges.  Every block only waits on blocks with smaller
 //     indices, which were dispatched before it.
+//   SELF (one launch, one query head per kv head): instead of polling a
+//     selection, the workgroup runs the head's top-k itself from the score
+//     words (every chunk of the head computes the same selection) and keeps
+//     its entries; the merging chunk clears the score words at the end.
 // QUEST (quest_kernel convention): the selection rows hold the pages chosen
 // besides the last page, which is always attended as the final entry
 // (quest/utils/__init__.py:237, approx_attn.cu:68-151).
-template <bool HANDOFF, bool QUEST>
+template <bool HANDOFF, bool QUEST, bool SELF = false>
 __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uint32_t hq,
-                                            uint32_t chunk, DecShared& sm) {
+                                            uint32_t chunk, DecShared& sm,
+                                            const EstimateArgs* ea = nullptr,
+                                            TopkShared* tk = nullptr) {
+  static_assert(!SELF || HANDOFF, "self-selection is a one-launch mode");
   float (*s_o)[kHeadDim] = sm.o;
   float (*s_ml)[2] = sm.ml;
   const uint32_t lane = __lane_id();
@@ -742,7 +780,25 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   }
   const H8 qq = ld16(a.q + bh * kHeadDim + d0);
   __builtin_amdgcn_sched_barrier(0);  // keep the issue order written here
-  if (P == 0u || lpl == 0u || lpl > S) return;  // malformed page table
+  // SELF: the head's top-k shape and its score words
+  SelPlan pl{};
+  uint32_t* words = nullptr;
+  if constexpr (SELF) {
+    pl = plan_select(*ea, b);
+    words = ea->hscore + ((size_t)b * ea->Hkv + hkv) * ea->hscore_stride;
+  }
+  // waits until the score words [0, pl.P) are written, then clears them
+  auto consume_words = [&]() {
+    for (uint32_t i = threadIdx.x; i < pl.P; i += kThreads) {
+      for (uint32_t it = 0u; ld_agent_u32(words + i) == 0u && it < kSpinLimit; ++it)
+        __builtin_amdgcn_s_sleep(1);
+      st_agent_u32(words + i, 0u);
+    }
+  };
+  if (P == 0u || lpl == 0u || lpl > S) {  // malformed page table
+    if (SELF && chunk == 0u) consume_words();  // the words were written all the same
+    return;
+  }
   // physical id of the sequence's last page (the one holding lpl tokens)
   uint32_t last_phys = 0u;
   if constexpr (QUEST) last_phys = (uint32_t)a.kv_indices[pbeg + P - 1u];
@@ -762,7 +818,36 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   // entries [0, nsel) come from the selection; with QUEST the entry after
   // them is the last page
   const uint32_t nsel = (QUEST && a.sel != nullptr) ? npages - 1u : npages;
-  if (HANDOFF) {
+  bool self_topk = false;  // SELF: the entries came from this workgroup's top-k
+  if constexpr (SELF) {
+    // the head's selection, computed here: entries [0, nout), in page order
+    const EstimateArgs& e = *ea;
+    const int32_t* ids = e.kv_indices + pl.pbeg;
+    self_topk = pl.k != 0u && pl.k < pl.P;
+    if (self_topk)
+      topk_staged<true>(nullptr, pl.P, pl.k, (e.flags & kFlagFixed) != 0u, ids, nullptr, *tk,
+                        nullptr, 0u, 0u, words, a.error);
+    const uint32_t nout = self_topk ? pl.k : (pl.k == 0u ? 0u : pl.P);
+    // entry i (page 0 past the selection; an entry the top-k did not yield
+    // means the shapes disagree: flagged like a wait that gave up)
+    auto entry = [&](uint32_t i) -> uint32_t {
+      if (i >= nsel) return 0u;
+      if (i >= nout) {
+        atomicOr(a.error, 1u);
+        return 0u;
+      }
+      return self_topk ? tk->key[i] : (uint32_t)ids[i];
+    };
+    sel_ch = entry(ich);
+#pragma unroll
+    for (int s = 0; s < kDecPagesPerWave; ++s) selv[s] = entry(idx0 + s);
+    // this chunk's entries of the selection output (the last chunk also
+    // writes any the decode does not cover)
+    int32_t* sel_out = e.sel + ((size_t)b * e.Hkv + hkv) * e.sel_stride;
+    const uint32_t o_end = chunk == nch - 1u ? nout : (ich + kDecPagesPerBlock < nout ? ich + kDecPagesPerBlock : nout);
+    for (uint32_t i = ich + threadIdx.x; i < o_end; i += kThreads)
+      sel_out[i] = (int32_t)(self_topk ? tk->key[i] : (uint32_t)ids[i]);
+  } else if (HANDOFF) {
     // this chunk's entries of the head's selection, each polled until the
     // top-k of this launch has written it, then cleared for the next launch
     uint32_t* hrow = a.hsel + bh * a.hsel_stride;
@@ -1010,18 +1095,28 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   // whole workspace is zero between calls whatever its layout: region
   // offsets depend on the call's selection size, and a later call with a
   // smaller one places its handoff words where these partials were.
-  uint32_t* words = HANDOFF ? a.hpart : reinterpret_cast<uint32_t*>(a.partial);
+  uint32_t* pwords = HANDOFF ? a.hpart : reinterpret_cast<uint32_t*>(a.partial);
   for (uint32_t g0 = 0; g0 < nch; g0 += 16u) {
     const size_t gb = base + (size_t)g0 * kPartialStride;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const uint32_t c = g0 + half + 2u * i;
-      if (c < nch) st_agent_u32(words + gb + (half + 2u * i) * kPartialStride + d, 0u);
+      if (c < nch) st_agent_u32(pwords + gb + (half + 2u * i) * kPartialStride + d, 0u);
     }
     const uint32_t c = g0 + threadIdx.x;
     if (threadIdx.x < 16u && c < nch) {
-      st_agent_u32(words + gb + threadIdx.x * kPartialStride + kHeadDim, 0u);
-      st_agent_u32(words + gb + threadIdx.x * kPartialStride + kHeadDim + 1, 0u);
+      st_agent_u32(pwords + gb + threadIdx.x * kPartialStride + kHeadDim, 0u);
+      st_agent_u32(pwords + gb + threadIdx.x * kPartialStride + kHeadDim + 1, 0u);
+    }
+  }
+  if constexpr (SELF) {
+    // every chunk's partial arrived, and each chunk stored its partial after
+    // its top-k had read the score words: clear them (without a top-k no one
+    // waited for them, so wait first)
+    if (self_topk) {
+      for (uint32_t i = threadIdx.x; i < pl.P; i += kThreads) st_agent_u32(words + i, 0u);
+    } else {
+      consume_words();
     }
   }
 }
@@ -1118,6 +1213,22 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
     const uint32_t u = t - la.n_workers - la.n_heads;
     const uint32_t bh = u / la.d.max_chunks, chunk = u % la.d.max_chunks;
     const uint32_t b = bh / la.d.Hq, hq = bh % la.d.Hq;
+    if constexpr (GROUP == 1) {
+      if (la.self_select != 0u) {
+        // start when the head's scoring workers start (their staggered
+        // schedule; heads of later rounds: the last first-round start):
+        // earlier, the head's decode items only add page-table loads and
+        // polls to the memory traffic of the first heads' scoring (23.0 vs
+        // 24.15 us per layer at config 2)
+        const uint32_t first_round = (la.n_workers - 1u) / la.est_chunks;
+        const unsigned long long t0 = clock64();
+        const unsigned long long wait =
+            (unsigned long long)(bh < first_round ? bh : first_round) * la.stagger;
+        while (clock64() - t0 < wait) __builtin_amdgcn_s_sleep(8);
+        decode_item<true, QUEST, true>(la.d, b, hq, chunk, sm.d, &la.e, &sm.e.tk);
+        return;
+      }
+    }
     decode_item<true, QUEST>(la.d, b, hq, chunk, sm.d);
   }
 }

@@ -141,6 +141,7 @@ struct LayerArgs {
   uint32_t n_heads;    // top-k workgroups: B * Hkv
   uint32_t n_dec;      // decode items: B * Hq * d.max_chunks
   uint32_t stagger;    // core cycles between the scoring starts of consecutive heads
+  uint32_t self_select;  // decode items run their head's top-k themselves (n_heads = 0)
 };
 
 hipError_t launch_append_prefill(const AppendPrefillArgs& a, hipStream_t s);
