@@ -136,7 +136,7 @@ __global__ __launch_bounds__(256) void append_decode_kernel(AppendDecodeArgs a) 
   if (P == 0u || lpl == 0u || lpl > S) return;  // malformed page table: nothing to do
   RopeTable rt;
   if constexpr (ROPE) {
-    rt = rope_table((P - 1u) * S + lpl - 1u, l16, a.rope_rcp_scale, a.rope_rcp_theta);
+    rt = rope_table((P - 1u) * S + lpl - 1u, l16, a.rope_f.f);
     if (q_block) {
       f16* qp = a.q + ((size_t)b * a.Hq + h) * kHeadDim + l16 * kVec;
       st16(qp, rope_row(ld16(qp), rt, l16));
@@ -217,7 +217,7 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   const uint32_t l16 = lane % kLanesPerRow;
   const uint32_t r = threadIdx.x / kLanesPerRow;  // 16 rows per block
   const uint32_t n = blockIdx.x;
-  const RopeTable rt = rope_table(a.past + n, l16, a.rope_rcp_scale, a.rope_rcp_theta);
+  const RopeTable rt = rope_table(a.past + n, l16, a.rope_f.f);
   for (uint32_t h = r; h < a.Hq + a.Hkv; h += 16u) {
     f16* p = h < a.Hq ? a.q + ((size_t)n * a.Hq + h) * kHeadDim
                       : a.k + ((size_t)n * a.Hkv + (h - a.Hq)) * kHeadDim;

@@ -13,6 +13,17 @@
 #include "../../include/aoakv.h"
 #include "kernels.hpp"
 
+namespace aoakv {
+RopeFreqs rope_freqs(float rope_scale, float rope_theta) {
+  RopeFreqs r;
+  const float rcp_scale = 1.0f / rope_scale, rcp_theta = 1.0f / rope_theta;
+  for (int i = 0; i < kHeadDim / 2; ++i)
+    r.f[i] = (float)((double)rcp_scale *
+                     std::pow((double)rcp_theta, (double)(2 * i) / (double)kHeadDim));
+  return r;
+}
+}  // namespace aoakv
+
 namespace {
 
 thread_local std::string g_err;
@@ -35,6 +46,24 @@ int ok() {
 int hip_status(hipError_t e, const char* what) {
   if (e != hipSuccess) return fail(AOAKV_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
   return ok();
+}
+
+// Workgroups of the one-launch layer the current device holds at once: four
+// per CU (its 36 KB of LDS per workgroup and 113 VGPRs per lane allow four).
+// 0 if the device cannot be queried.  Cached per device (benign races: every
+// writer stores the same value).
+uint32_t resident_layer_workgroups() {
+  static uint32_t cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0u;
+  if (cache[dev] == 0u) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      return 0u;
+    cache[dev] = 4u * (uint32_t)cus;
+  }
+  return cache[dev];
 }
 
 #define REQUIRE(cond, ...)                                  \
@@ -263,8 +292,7 @@ int aoakv_apply_rope_in_place(void* q, void* k, uint32_t seq_len, uint32_t past_
   a.past = past_kv_len;
   a.Hq = num_qo_heads;
   a.Hkv = num_kv_heads;
-  a.rope_rcp_scale = 1.0f / rope_scale;
-  a.rope_rcp_theta = 1.0f / rope_theta;
+  a.rope_f = aoakv::rope_freqs(rope_scale, rope_theta);
   return hip_status(aoakv::launch_rope(a, static_cast<hipStream_t>(stream)), "apply_rope_in_place");
 }
 
@@ -305,8 +333,7 @@ int aoakv_rope_append_kv_cache_decode(void* q, void* k, const void* v, uint32_t 
   a.rope = 1u;
   a.q = static_cast<aoakv::f16*>(q);
   a.Hq = num_qo_heads;
-  a.rope_rcp_scale = 1.0f / rope_scale;
-  a.rope_rcp_theta = 1.0f / rope_theta;
+  a.rope_f = aoakv::rope_freqs(rope_scale, rope_theta);
   return hip_status(aoakv::launch_append_decode(a, batch_size, static_cast<hipStream_t>(stream)),
                     "rope_append_kv_cache_decode");
 }
@@ -562,11 +589,17 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
     la.n_est = batch_size * num_kv_heads * la.est_chunks;
     la.n_workers = aoakv::layer_score_workers(la.n_est, la.est_chunks);
     la.stagger = aoakv::layer_stagger_cycles(la.est_chunks);
-    // one query head per kv head and score words: each decode item selects
-    // its head's pages itself (no top-k workgroups, no selection handoff)
-    la.self_select = la.e.hscore != nullptr && num_qo_heads == num_kv_heads ? 1u : 0u;
-    la.n_heads = la.self_select ? 0u : batch_size * num_kv_heads;
     la.n_dec = batch_size * num_qo_heads * da.max_chunks;
+    // one query head per kv head, score words, and the whole launch resident
+    // at once: each decode item selects its head's pages itself (no top-k
+    // workgroups, no selection handoff).  With more workgroups than the GPU
+    // holds, the 16 copies of every top-k cost more than the handoff they
+    // save (config 5, 512 heads: 316 vs 250 us per layer).
+    la.self_select = la.e.hscore != nullptr && num_qo_heads == num_kv_heads &&
+                             la.n_workers + la.n_dec <= resident_layer_workgroups()
+                         ? 1u
+                         : 0u;
+    la.n_heads = la.self_select ? 0u : batch_size * num_kv_heads;
     return hip_status(aoakv::launch_layer(la, s), "sparse_decode_layer");
   }
   if (int e = launch_estimate_topk(ea, w, sel_pages, sel_stride, token_budget, token_budgets,

@@ -1149,8 +1149,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
 // and handoff words are cleared by their readers, so the workspace is zero
 // again for the next launch.  No counter is shared by all workgroups
 // (same-address device atomics serialize at ~12 ns each).
-template <int GROUP, bool QUEST>
+// SELF (GROUP 1, la.self_select): the decode items select for themselves; a
+// separate instantiation, so the other path keeps its own register budget.
+template <int GROUP, bool QUEST, bool SELF>
 __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
+  static_assert(!SELF || GROUP == 1, "self-selection needs one query head per kv head");
   __shared__ union {
     EstTopkShared e;
     DecShared d;
@@ -1213,23 +1216,21 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
     const uint32_t u = t - la.n_workers - la.n_heads;
     const uint32_t bh = u / la.d.max_chunks, chunk = u % la.d.max_chunks;
     const uint32_t b = bh / la.d.Hq, hq = bh % la.d.Hq;
-    if constexpr (GROUP == 1) {
-      if (la.self_select != 0u) {
-        // start when the head's scoring workers start (their staggered
-        // schedule; heads of later rounds: the last first-round start):
-        // earlier, the head's decode items only add page-table loads and
-        // polls to the memory traffic of the first heads' scoring (23.0 vs
-        // 24.15 us per layer at config 2)
-        const uint32_t first_round = (la.n_workers - 1u) / la.est_chunks;
-        const unsigned long long t0 = clock64();
-        const unsigned long long wait =
-            (unsigned long long)(bh < first_round ? bh : first_round) * la.stagger;
-        while (clock64() - t0 < wait) __builtin_amdgcn_s_sleep(8);
-        decode_item<true, QUEST, true>(la.d, b, hq, chunk, sm.d, &la.e, &sm.e.tk);
-        return;
-      }
+    if constexpr (SELF) {
+      // start when the head's scoring workers start (their staggered
+      // schedule; heads of later rounds: the last first-round start):
+      // earlier, the head's decode items only add page-table loads and
+      // polls to the memory traffic of the first heads' scoring (23.0 vs
+      // 24.15 us per layer at config 2)
+      const uint32_t first_round = (la.n_workers - 1u) / la.est_chunks;
+      const unsigned long long t0 = clock64();
+      const unsigned long long wait =
+          (unsigned long long)(bh < first_round ? bh : first_round) * la.stagger;
+      while (clock64() - t0 < wait) __builtin_amdgcn_s_sleep(8);
+      decode_item<true, QUEST, true>(la.d, b, hq, chunk, sm.d, &la.e, &sm.e.tk);
+    } else {
+      decode_item<true, QUEST>(la.d, b, hq, chunk, sm.d);
     }
-    decode_item<true, QUEST>(la.d, b, hq, chunk, sm.d);
   }
 }
 
@@ -1263,11 +1264,17 @@ hipError_t launch_estimate(const EstimateArgs& a, uint32_t batch, uint32_t max_p
 hipError_t launch_layer(const LayerArgs& la, hipStream_t s) {
   const uint32_t grid = la.n_workers + la.n_heads + la.n_dec;
   const bool quest = (la.e.flags & kFlagQuestKernel) != 0u;
+  if (la.self_select != 0u) {
+    if (la.e.Hq != la.e.Hkv) return hipErrorInvalidValue;
+    if (quest) hipLaunchKernelGGL((layer_kernel<1, true, true>), dim3(grid), dim3(kThreads), 0, s, la);
+    else hipLaunchKernelGGL((layer_kernel<1, false, true>), dim3(grid), dim3(kThreads), 0, s, la);
+    return hipGetLastError();
+  }
   switch (la.e.Hq / la.e.Hkv) {
 #define AOAKV_LAYER(G)                                                                       \
   case G:                                                                                    \
-    if (quest) hipLaunchKernelGGL((layer_kernel<G, true>), dim3(grid), dim3(kThreads), 0, s, la); \
-    else hipLaunchKernelGGL((layer_kernel<G, false>), dim3(grid), dim3(kThreads), 0, s, la);      \
+    if (quest) hipLaunchKernelGGL((layer_kernel<G, true, false>), dim3(grid), dim3(kThreads), 0, s, la); \
+    else hipLaunchKernelGGL((layer_kernel<G, false, false>), dim3(grid), dim3(kThreads), 0, s, la);      \
     break;
     AOAKV_LAYER(1)
     AOAKV_LAYER(2)

@@ -180,23 +180,22 @@ __device__ inline f16 log_norm_row(const H8& vbar, uint32_t lane16) {
 //   out_d = x_d cos a + x_{d-64} sin a   (d >= 64),
 // with f_i evaluated in fp64 and rounded to fp32 (so it is the correctly
 // rounded frequency: at position 10^4 one ulp of f_i moves the angle by
-// ~10^-3), the angle and rotation in fp32 with the accurate sincosf, and one
-// rounding to fp16 at the end.  Lane l16
+// ~10^-3; the host computes the 64 of them once per launch, rope_freqs), the
+// angle and rotation in fp32 with the accurate sincosf, and one rounding to
+// fp16 at the end.  Lane l16
 // of a 16-lane row holds dims 8*l16 .. 8*l16 + 7, so the partner dims d +- 64
 // are in lane l16 ^ 8 of the same row (DPP row_ror:8).
 struct RopeTable {
   float c[kVec], s[kVec];  // cos / sin of this lane's 8 dims at one position
 };
 
-__device__ inline RopeTable rope_table(uint32_t pos, uint32_t l16, float rcp_scale,
-                                       float rcp_theta) {
+// freqs: the 64 frequencies f_i (kernel argument)
+__device__ inline RopeTable rope_table(uint32_t pos, uint32_t l16, const float* freqs) {
   RopeTable t;
 #pragma unroll
   for (int j = 0; j < kVec; ++j) {
     const uint32_t i = (l16 * kVec + (uint32_t)j) % (kHeadDim / 2);
-    const float f =
-        (float)((double)rcp_scale * pow((double)rcp_theta, (double)(2u * i) / (double)kHeadDim));
-    sincosf((float)pos * f, &t.s[j], &t.c[j]);
+    sincosf((float)pos * freqs[i], &t.s[j], &t.c[j]);
   }
   return t;
 }

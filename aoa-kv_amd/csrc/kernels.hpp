@@ -10,6 +10,14 @@ namespace aoakv {
 // line slow each other's atomics and polls.
 constexpr uint32_t kCounterStride = 32;
 
+// RoPE frequencies f_i = rcp_scale * rcp_theta^(2i / 128), i < 64: fixed by
+// (rope_scale, rope_theta), so computed once on the host (rope_freqs) and
+// passed with the launch instead of per lane on the device.
+struct RopeFreqs {
+  float f[kHeadDim / 2];
+};
+RopeFreqs rope_freqs(float rope_scale, float rope_theta);
+
 struct AppendPrefillArgs {
   const f16* k;            // [N, H, D]
   const f16* v;            // [N, H, D]
@@ -42,14 +50,14 @@ struct AppendDecodeArgs {
   uint32_t rope;
   f16* q;
   uint32_t Hq;
-  float rope_rcp_scale, rope_rcp_theta;
+  RopeFreqs rope_f;
 };
 
 struct RopeArgs {
   f16* q;  // [N, Hq, D]
   f16* k;  // [N, Hkv, D]
   uint32_t N, past, Hq, Hkv;
-  float rope_rcp_scale, rope_rcp_theta;
+  RopeFreqs rope_f;
 };
 
 struct EstimateArgs {

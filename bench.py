@@ -102,11 +102,12 @@ def build_layers(n_layers, layout, dev):
                 append_us=times, k0=k0, v0=v0)
 
 
-def decode_appends(dev, layout, n_app=512, mode="append"):
+def decode_appends(dev, layout, n_app=512, mode="append", graph=True):
     """Config 3b: prefill 4096+7 tokens then 512 single-token appends.
     mode "append": the decode append alone; "rope_then_append": RoPE of q, k
     then the append (two launches, the reference's call order); "rope_append":
-    the fused RoPE + append (one launch).  Eager launches, us per step."""
+    the fused RoPE + append (one launch).  Returns us per step, eager
+    launches and (graph=True) the steps replayed from a HIP graph."""
     import torch
     from aoakv import ops
     from aoakv.utils import InferenceController, append_kv
@@ -129,22 +130,48 @@ def decode_appends(dev, layout, n_app=512, mode="append"):
         steps.append((c.kv_indptr_for_append, c.kv_indices_with_last, c.kv_last_page_len_t,
                       c.metadata_indptr_for_append, c.metadata_indices))
     torch.cuda.synchronize()
+
+    def run_steps():
+        for i, (ip, ix, lp, mip, mix) in enumerate(steps):
+            if mode == "rope_append":
+                ops.rope_append_kv_cache_decode(qn[i], kn[i], vn[i], c.kv_cache.buf_layer(0), ip, ix,
+                                                lp, c.metadata_cache.buf_layer(0), mip, mix,
+                                                c.v_log_norm[0], c.v_mean[0], layout)
+                continue
+            if mode == "rope_then_append":
+                ops.apply_rope_in_place(qn[i], kn[i], 4103 + i)
+            ops.append_kv_cache_decode(kn[i], vn[i], c.kv_cache.buf_layer(0), ip, ix, lp,
+                                       c.metadata_cache.buf_layer(0), mip, mix, c.v_log_norm[0],
+                                       c.v_mean[0], layout)
+
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for i, (ip, ix, lp, mip, mix) in enumerate(steps):
-        if mode == "rope_append":
-            ops.rope_append_kv_cache_decode(qn[i], kn[i], vn[i], c.kv_cache.buf_layer(0), ip, ix,
-                                            lp, c.metadata_cache.buf_layer(0), mip, mix,
-                                            c.v_log_norm[0], c.v_mean[0], layout)
-            continue
-        if mode == "rope_then_append":
-            ops.apply_rope_in_place(qn[i], kn[i], 4103 + i)
-        ops.append_kv_cache_decode(kn[i], vn[i], c.kv_cache.buf_layer(0), ip, ix, lp,
-                                   c.metadata_cache.buf_layer(0), mip, mix, c.v_log_norm[0],
-                                   c.v_mean[0], layout)
+    run_steps()
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / n_app
+    eager = e0.elapsed_time(e1) * 1e3 / n_app
+    if not graph:
+        return eager
+    # the same 512 steps captured in a HIP graph and replayed: the kernels
+    # back to back, as a decode loop replays them, without the host's per-call
+    # dispatch (a replay appends the same tokens again: same work, and the
+    # buffers belong to this measurement only)
+    gr = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run_steps()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(gr):
+        run_steps()
+    gr.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    gr.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return eager, e0.elapsed_time(e1) * 1e3 / n_app
 
 
 def prefill_bench(dev, layout, L, reps=5):
@@ -451,11 +478,12 @@ def main():
         extra["bulk_append_32k_us"] = round(float(np.median(app)), 2)
         extra["bulk_append_32k_GBps"] = round(app_bytes / (np.median(app) * 1e-6) / 1e9, 1)
         extra["bulk_append_bytes"] = app_bytes
-        extra["decode_append_us"] = round(decode_appends(dev, layout), 3)
-        extra["decode_rope_then_append_us"] = round(
-            decode_appends(dev, layout, mode="rope_then_append"), 3)
-        extra["decode_rope_append_fused_us"] = round(
-            decode_appends(dev, layout, mode="rope_append"), 3)
+        for key, mode in (("decode_append", "append"),
+                          ("decode_rope_then_append", "rope_then_append"),
+                          ("decode_rope_append_fused", "rope_append")):
+            eager, graphed = decode_appends(dev, layout, mode=mode)
+            extra[key + "_us"] = round(eager, 3)
+            extra[key + "_graph_us"] = round(graphed, 3)
         for Lp in (8192, 16384):
             us, tf = prefill_bench(dev, layout, Lp)
             extra[f"prefill_{Lp // 1024}k_us"] = round(us, 1)

@@ -598,37 +598,34 @@ def test_one_launch_score_words_every_selection_shape(case):
         assert int(ws_words.count_nonzero().item()) == 0, "workspace not left zero"
 
 
-def test_one_launch_malformed_sequence_still_clears_score_words():
-    """A batch whose second sequence has a last-page length of 0 (malformed:
-    no decode item attends it).  The one-launch layer still scores its pages
-    and hands the scores over as words; its first decode item must wait for
-    and clear them, so the whole workspace is zero again after every call.
-    The well-formed sequence's output and selection equal the two-launch
-    path's bit for bit and no wait gives up."""
+def _repeated_batch_one_launch(H, L, budget, lpls, seed):
+    """One sequence's cache read by len(lpls) sequences of a batch (the same
+    pages, last-page lengths lpls).  Runs the one-launch layer with score
+    words three times and checks it against the two-launch path: outputs
+    and selections of the well-formed sequences bit for bit, no wait given
+    up, and the whole workspace zero after every call."""
     from aoakv import ops
-    _say("[malformed sequence, score words]")
-    H, L, budget = 8, 2007, 512
-    q, K, V = _sim_state(91, H, L)
-    c = make_ctrl(H, L + 16, HND, budget, shuffle=91)
+    B = len(lpls)
+    q, K, V = _sim_state(seed, H, L)
+    c = make_ctrl(H, L + 16, HND, budget, shuffle=seed)
     prefill(c, K, V)
     c.begin_forward(1)
     P = len(c.kv_cache.indicies)
     mP = int(c.metadata_indices.numel())
-    qd = torch.from_numpy(q[0, :, 0].copy()).to(DEV)[None].repeat(2, 1, 1)
-    # both sequences read the same pages; only the second one's last-page length is bad
-    indptr = torch.tensor([0, P, 2 * P], dtype=torch.int32, device=DEV)
-    idx = c.kv_indices_with_last[:P].repeat(2)
-    lpl = torch.tensor([(L - 1) % S + 1, 0], dtype=torch.int32, device=DEV)
-    mindptr = torch.tensor([0, mP, 2 * mP], dtype=torch.int32, device=DEV)
-    midx = c.metadata_indices.repeat(2)
-    scores = torch.zeros((2, H, P), dtype=torch.float32, device=DEV)
+    qd = torch.from_numpy(q[0, :, 0].copy()).to(DEV)[None].repeat(B, 1, 1)
+    indptr = torch.arange(0, (B + 1) * P, P, dtype=torch.int32, device=DEV)
+    idx = c.kv_indices_with_last[:P].repeat(B)
+    lpl = torch.tensor(lpls, dtype=torch.int32, device=DEV)
+    mindptr = torch.arange(0, (B + 1) * mP, mP, dtype=torch.int32, device=DEV)
+    midx = c.metadata_indices.repeat(B)
+    scores = torch.zeros((B, H, P), dtype=torch.float32, device=DEV)
     kcols = sim.num_selected_pages(min(L, budget), S, P)
-    ws_words = ops.decode_workspace(2, H, H, kcols, max_pages=P)
-    ws_plain = ops.decode_workspace(2, H, H, kcols)
+    ws_words = ops.decode_workspace(B, H, H, kcols, max_pages=P)
+    ws_plain = ops.decode_workspace(B, H, H, kcols)
 
     def layer(ws, flags):
         o = torch.zeros_like(qd)
-        sel = torch.full((2, H, kcols), -1, dtype=torch.int32, device=DEV)
+        sel = torch.full((B, H, kcols), -1, dtype=torch.int32, device=DEV)
         ops.sparse_decode_layer(qd, o, c.kv_cache.buf_layer(0), indptr, idx, lpl,
                                 c.metadata_cache.buf_layer(0), mindptr, midx,
                                 c.v_log_norm_layer(0), scores, sel, budget, ws, P, HND, flags)
@@ -636,9 +633,29 @@ def test_one_launch_malformed_sequence_still_clears_score_words():
         return o, sel
 
     F = ops.FLAG_VALUE_AWARE | ops.FLAG_FIXED
+    good = [b for b, x in enumerate(lpls) if 1 <= x <= S]
     o_ref, sel_ref = layer(ws_plain, F)  # two launches
     for rep in range(3):
         o1, sel1 = layer(ws_words, F | ops.FLAG_SINGLE_LAUNCH)
-        assert torch.equal(o1[0], o_ref[0]) and torch.equal(sel1[0], sel_ref[0]), rep
+        assert torch.equal(o1[good], o_ref[good]) and torch.equal(sel1[good], sel_ref[good]), rep
         assert int(ws_words[8:12].view(torch.int32).item()) == 0, "spin-wait error flag set"
         assert int(ws_words.count_nonzero().item()) == 0, "workspace not left zero"
+
+
+def test_one_launch_malformed_sequence_still_clears_score_words():
+    """A batch whose second sequence has a last-page length of 0 (malformed:
+    no decode item attends it).  The one-launch layer still scores its pages
+    and hands the scores over as words; its first decode item must wait for
+    and clear them, so the whole workspace is zero again after every call."""
+    _say("[malformed sequence, score words]")
+    L = 2007
+    _repeated_batch_one_launch(8, L, 512, [(L - 1) % S + 1, 0], 91)
+
+
+def test_one_launch_more_workgroups_than_resident():
+    """8 sequences x 32 heads x 8 decode chunks: more workgroups than the GPU
+    holds at once, so the one-launch layer keeps its top-k workgroups and the
+    selection handoff (the decode items do not select for themselves)."""
+    _say("[one launch, 2048 decode items]")
+    L = 2007
+    _repeated_batch_one_launch(32, L, 1024, [(L - 1) % S + 1] * 8, 93)
