@@ -332,8 +332,9 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this build measures one GPU only: the AOA-KV decode path "
-                          "is single-GPU (multi-GPU sharding by heads is a design note in "
-                          "DESIGN.md); run with --gpus 1"}))
+                          "is single-GPU (across GPUs it would shard by heads, each GPU "
+                          "taking H/N heads with no exchange inside the path); run with "
+                          "--gpus 1"}))
         sys.exit(2)
 
     import numpy as np
