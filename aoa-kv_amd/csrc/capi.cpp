@@ -48,10 +48,10 @@ int hip_status(hipError_t e, const char* what) {
   return ok();
 }
 
-// Workgroups of the one-launch layer the current device holds at once: four
-// per CU (its 36 KB of LDS per workgroup and 113 VGPRs per lane allow four).
-// 0 if the device cannot be queried.  Cached per device (benign races: every
-// writer stores the same value).
+// Workgroups of the self-selecting one-launch layer the current device holds
+// at once: CUs times the kernel's occupancy per CU (four at 36 KB of LDS and
+// 112 VGPRs).  0 if the device cannot be queried.  Cached per device (benign
+// races: every writer stores the same value).
 uint32_t resident_layer_workgroups() {
   static uint32_t cache[64];
   int dev = 0;
@@ -61,7 +61,7 @@ uint32_t resident_layer_workgroups() {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         cus <= 0)
       return 0u;
-    cache[dev] = 4u * (uint32_t)cus;
+    cache[dev] = aoakv::layer_self_blocks_per_cu() * (uint32_t)cus;
   }
   return cache[dev];
 }

@@ -1346,5 +1346,15 @@ uint32_t layer_stagger_cycles(uint32_t est_chunks) {
   return (uint32_t)((uint64_t)est_chunks * kChunkBytes / kStreamBytesPerCycle);
 }
 uint32_t counter_stride() { return kCounterStride; }
+// Workgroups of the self-selecting layer kernel one CU holds at once (its LDS
+// and registers decide); 0 if the runtime cannot tell.
+uint32_t layer_self_blocks_per_cu() {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, layer_kernel<1, false, true>, kThreads, 0) !=
+          hipSuccess ||
+      n < 0)
+    return 0u;
+  return (uint32_t)n;
+}
 
 }  // namespace aoakv

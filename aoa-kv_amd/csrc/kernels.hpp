@@ -171,5 +171,6 @@ uint32_t fused_topk_max_pages();  // ... and the fused estimate + top-k kernel
 uint32_t layer_score_workers(uint32_t n_est, uint32_t est_chunks);  // one-launch layer scorers
 uint32_t layer_stagger_cycles(uint32_t est_chunks);  // one-launch scoring start offset per head
 uint32_t counter_stride();        // u32 words between per-head counters (one cache line each)
+uint32_t layer_self_blocks_per_cu();  // self-selecting layer workgroups resident per CU
 
 }  // namespace aoakv
