@@ -712,6 +712,19 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopkArgs a) {
 // sparse decode attention, split-K over pages with a fused merge
 // ======================================================================
 
+// out[u] = v of lane u of this lane's 16-lane row, u < 8 (DPP row_newbcast)
+__device__ __forceinline__ void row_bcast8(float v, float (&out)[8]) {
+  const int x = __builtin_bit_cast(int, v);
+  out[0] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x150, 0xF, 0xF, false));
+  out[1] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x151, 0xF, 0xF, false));
+  out[2] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x152, 0xF, 0xF, false));
+  out[3] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x153, 0xF, 0xF, false));
+  out[4] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x154, 0xF, 0xF, false));
+  out[5] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x155, 0xF, 0xF, false));
+  out[6] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x156, 0xF, 0xF, false));
+  out[7] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x157, 0xF, 0xF, false));
+}
+
 struct DecShared {
   float o[4][kHeadDim];
   float ml[4][2];
@@ -902,9 +915,14 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   for (int s = 0; s < kDecPagesPerWave; ++s)
     ntok[s] = live[s] ? (phys[s] == last_phys ? lpl : S) : 0u;
 
-  // ---- logits: fp16(q.k), then fp16(. / sqrt(d))  (quest_attention.py:265-268)
-  float x[kDecPagesPerWave][4];
-  float mloc = -INFINITY;
+  // ---- logits: fp16(q.k), then fp16(. / sqrt(d))  (quest_attention.py:265-268).
+  // The 16 lanes of a row hold the same 8 dot sums (tokens i*4 + row of the
+  // wave's two pages, u = 4s + i); lane l16 % 8 rounds and exponentiates
+  // token u = l16 % 8 only, and the row takes each token's value from its
+  // lane with DPP row_newbcast (the same arithmetic per token, once).
+  constexpr int kTok = kDecPagesPerWave * 4;
+  static_assert(kTok == 8, "one rounding lane per token of a row");
+  float raw[kTok];
 #pragma unroll
   for (int s = 0; s < kDecPagesPerWave; ++s) {
 #pragma unroll
@@ -913,29 +931,35 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
 #pragma unroll
       for (int m = 0; m < kVec / 2; ++m)
         acc = __builtin_amdgcn_fdot2(q2[m], half_pair(kk[s][i], m), acc, false);
-      acc = row_sum16(acc);
-      const float lg = (float)r16(div_sqrt_head_dim_f16((float)r16(acc)));
-      const uint32_t t = i * 4 + row;
-      x[s][i] = t < ntok[s] ? lg : -INFINITY;
-      mloc = fmaxf(mloc, x[s][i]);
+      raw[s * 4 + i] = row_sum16(acc);
     }
   }
+  const uint32_t um = l16 % (uint32_t)kTok;  // this lane's token
+  float pick = raw[0];
+#pragma unroll
+  for (int u = 1; u < kTok; ++u) pick = um == (uint32_t)u ? raw[u] : pick;
+  float xm = (float)r16(div_sqrt_head_dim_f16((float)r16(pick)));
+  xm = (um % 4u) * 4u + row < (um < 4u ? ntok[0] : ntok[1]) ? xm : -INFINITY;
+  float x[kTok];
+  row_bcast8(xm, x);
+  float mloc = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < kTok; ++u) mloc = fmaxf(mloc, x[u]);
   const float m = cross_row_max(mloc);
   float lsum = 0.f;
   float o[kVec];
 #pragma unroll
   for (int j = 0; j < kVec; ++j) o[j] = 0.f;
   if (m != -INFINITY) {
+    float pv[kTok];
+    row_bcast8(__expf(xm - m), pv);
 #pragma unroll
-    for (int s = 0; s < kDecPagesPerWave; ++s) {
+    for (int u = 0; u < kTok; ++u) {
+      const float p = pv[u];
+      lsum = lsum + p;
+      // one mixed-precision FMA per dim (fp16 V converted in the FMA)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float p = __expf(x[s][i] - m);
-        lsum = lsum + p;
-        // one mixed-precision FMA per dim (fp16 V converted in the FMA)
-#pragma unroll
-        for (int j = 0; j < kVec; ++j) o[j] = __builtin_fmaf(p, (float)vv[s][i].v[j], o[j]);
-      }
+      for (int j = 0; j < kVec; ++j) o[j] = __builtin_fmaf(p, (float)vv[u / 4][u % 4].v[j], o[j]);
     }
   }
   lsum = cross_row_sum(lsum);
