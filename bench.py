@@ -319,7 +319,9 @@ def main():
     ap.add_argument("--steps", type=int, default=3200, help="layers timed (multiple of 32)")
     ap.add_argument("--warmup", type=int, default=320)
     ap.add_argument("--layout", choices=["hnd", "nhd"], default="hnd")
-    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--cpu-reps", type=int, default=20,
+                    help="timed oracle passes over layer 0 (about 0.5 s each on 16 host threads: "
+                         "a bounded sample of about 10 s of CPU work)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip appends / eager timings")
     ap.add_argument("--prefill-pass", action="store_true",
