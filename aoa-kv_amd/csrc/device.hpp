@@ -164,7 +164,12 @@ __device__ inline f16 log_norm_row(const H8& vbar, uint32_t lane16) {
     // hand the running sum to the next lane of the row
     acc = __shfl(acc, (int)((__lane_id() & ~15u) | (uint32_t)src), kWave);
   }
-  f16 nrm = r16(__fsqrt_rn(acc));
+  // the correctly rounded fp32 root (torch's sqrtf): the fp64 root rounded
+  // once to fp32 is exactly that (53 >= 2 * 24 + 2 bits).  __fsqrt_rn is not
+  // used: this toolchain's header maps it to the native approximation, whose
+  // last bit can differ, and an fp32 root on an fp16 midpoint then rounds to
+  // the other fp16 neighbour (seen at one page-head of 65,536 at config 3a).
+  f16 nrm = r16((float)__builtin_sqrt((double)acc));
   nrm = r16((float)nrm + 1e-8f);
   double ln = log((double)(float)nrm);
   return r16((float)ln);

@@ -114,6 +114,39 @@ def test_decode_append_trace_bit_exact(layout):
             check_metadata(ctrl, st)
 
 
+def test_prefill_append_config3a_full_size_bit_exact():
+    """BASELINE config 3a at its full size: the bulk metadata build of a
+    32768-token sequence over 32 heads (the bench's layout, HND).  K/V
+    storage, Kmax/Kmin, page means and log-norms all bit-exact."""
+    _say("[prefill-append] config 3a, 32 heads x 32768 tokens")
+    H, L = 32, 32768
+    K = randn16(300, (1, H, L, D))
+    V = randn16(301, (1, H, L, D))
+    ctrl = make_ctrl(H, L + 64, HND, shuffle=3)
+    prefill(ctrl, K, V)
+    check_metadata(ctrl, sim.SimLayerState(K, V))
+
+
+def test_decode_append_config3b_full_trace_bit_exact():
+    """BASELINE config 3b at its full size: 4096+7 tokens, then 512
+    single-token appends over 32 heads (32 page boundaries crossed, partial
+    pages updated by the running mean); metadata checked every 128 appends."""
+    _say("[decode-append] config 3b, 32 heads, 512 appends")
+    H, L0, steps = 32, 4096 + 7, 512
+    K = randn16(11, (1, H, L0, D))
+    V = randn16(12, (1, H, L0, D))
+    kn = randn16(13, (steps, 1, H, 1, D))
+    vn = randn16(14, (steps, 1, H, 1, D))
+    ctrl = make_ctrl(H, L0 + steps + 16, HND, shuffle=11)
+    prefill(ctrl, K, V)
+    st = sim.SimLayerState(K, V)
+    for s in range(steps):
+        decode_append(ctrl, kn[s], vn[s])
+        st.append(kn[s], vn[s])
+        if s % 128 == 127:
+            check_metadata(ctrl, st)
+
+
 @pytest.mark.parametrize("layout", [NHD, HND])
 def test_chunked_prefill_append(layout):
     """A second bulk append: the page already holding tokens continues the
