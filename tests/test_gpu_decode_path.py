@@ -330,14 +330,17 @@ def test_fused_estimate_topk_long_rows(L):
 # ------------------------------------------------------------------ attention
 
 @pytest.mark.parametrize("layout", [NHD, HND])
-@pytest.mark.parametrize("L", [4096, 4096 + 9, 1000])
-def test_full_decode_step_matches_simulation(layout, L):
-    """Config-1 shape: prefill L-1 tokens, append one, then estimate / top-k /
-    sparse decode; o within 2e-3 of the simulation's masked attention."""
+@pytest.mark.parametrize("L,budget,outlier", [(4096, 1024, False), (4096 + 9, 1024, False),
+                                              (1000, 1024, False), (32768, 2048, True)])
+def test_full_decode_step_matches_simulation(layout, L, budget, outlier):
+    """Config-1 shape, and config 2 at its full size (32768 tokens, budget
+    2048, 4 key channels x8): prefill L-1 tokens, append one, then estimate /
+    top-k / sparse decode; o within 2e-3 of the simulation's masked
+    attention; the two fused layer paths give the same bits."""
     from aoakv.utils import decode_estimate, decode_sparse_attn, decode_topk, decode_layer
-    _say(f"[decode-step] layout={layout} L={L}")
-    H, budget = 32, 1024
-    q, K, V = _sim_state(11, H, L)
+    _say(f"[decode-step] layout={layout} L={L} budget={budget} outlier={outlier}")
+    H = 32
+    q, K, V = _sim_state(11, H, L, outlier)
     ctrl = make_ctrl(H, L + 16, layout, budget, shuffle=5)
     prefill(ctrl, K[:, :, :-1], V[:, :, :-1])
     decode_append(ctrl, K[:, :, -1:], V[:, :, -1:])
