@@ -91,14 +91,14 @@ def test_prefill_forward_via_controller():
     assert np.abs(o.astype(np.float32) - ref).max() <= 2e-3
 
 
-@pytest.mark.parametrize("layout", [NHD, HND])
-def test_prefill_config4_8k_sampled_rows(layout):
-    """BASELINE config 4 shape (32 heads, 8192 tokens); rows sampled across the
-    causal range, including tile and page boundaries."""
-    _say(f"[prefill] config-4 8k layout={layout}")
-    L = 8192
+@pytest.mark.parametrize("layout,L", [(NHD, 8192), (HND, 8192), (HND, 16384)])
+def test_prefill_config4_8k_sampled_rows(layout, L):
+    """BASELINE config 4 shapes (32 heads, 8192 and 16384 tokens); rows
+    sampled across the causal range, including tile and page boundaries."""
+    _say(f"[prefill] config-4 L={L} layout={layout}")
     q, k, v, o = _run(L, L, 32, layout, seed=0, shuffle=4)
-    rows = np.array([0, 1, 15, 16, 63, 64, 127, 128, 129, 1000, 4095, 4096, 6000, 8126, 8190, 8191])
+    rows = np.array([0, 1, 15, 16, 63, 64, 127, 128, 129, 1000, 4095, 4096, 6000,
+                     L - 66, L - 2, L - 1])
     ref = _ref_rows(q, k, v, rows, True)
     err = np.abs(o[rows].astype(np.float32) - ref).max()
     _say(f"   max err {err:.2e}")
