@@ -486,18 +486,19 @@ def test_batched_ragged_decode_matches_simulation():
     assert differs_from_quest >= 1, "value term never changed a selection"
 
 
-def test_gqa_selection_and_decode():
-    """GQA (2 query heads per kv head): group-consistent logsumexp selection
-    (filter_util.py:351-368) and decode over the shared pages."""
+@pytest.mark.parametrize("Hq,Hkv,L,budget", [(8, 4, 1500, 256), (32, 8, 32768, 2048)])
+def test_gqa_selection_and_decode(Hq, Hkv, L, budget):
+    """GQA: group-consistent logsumexp selection (filter_util.py:351-368)
+    and decode over the shared pages; 2 query heads per kv head at 1500
+    tokens, and 4 per kv head at the config-2 length and budget."""
     from aoakv import ops
-    _say("[gqa]")
-    Hq, Hkv, L, budget = 8, 4, 1500, 256
+    _say(f"[gqa] Hq={Hq} Hkv={Hkv} L={L} budget={budget}")
     K = randn16(13, (1, Hkv, L, D))
     V = randn16(14, (1, Hkv, L, D))
     q = randn16(15, (1, Hq, 1, D))
     P = num_pages(L)
     st = sim.SimLayerState(K, V)
-    scores_ref, pages_ref = sim.select_pages(st, q, budget, True, True, 2)
+    scores_ref, pages_ref = sim.select_pages(st, q, budget, True, True, Hq // Hkv)
     kv = torch.zeros((P, 2, Hkv, S, D), dtype=torch.float16, device=DEV)
     meta = torch.zeros((math.ceil(P / S), 2, Hkv, S, D), dtype=torch.float16, device=DEV)
     lvn = torch.zeros((P, Hkv), dtype=torch.float16, device=DEV)
@@ -523,8 +524,9 @@ def test_gqa_selection_and_decode():
     np.testing.assert_allclose(sc, scores_ref[0, :, 0], rtol=1e-5, atol=1e-4)
     sl = sel.cpu().numpy()[0]
     _selection_ok(sl, pages_ref, scores_ref, True)
-    mask = np.repeat(sim.pages_to_token_mask(sl[None, :, None], S, L), 2, axis=1)
-    ref = sim.masked_decode_attention(q, np.repeat(K, 2, 1), np.repeat(V, 2, 1), mask)
+    grp = Hq // Hkv
+    mask = np.repeat(sim.pages_to_token_mask(sl[None, :, None], S, L), grp, axis=1)
+    ref = sim.masked_decode_attention(q, np.repeat(K, grp, 1), np.repeat(V, grp, 1), mask)
     assert np.abs(o.cpu().numpy()[0].astype(np.float32) - ref[0, :, 0].astype(np.float32)).max() <= 2e-3
 
 
