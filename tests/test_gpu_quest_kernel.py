@@ -56,7 +56,7 @@ def _to_dev(x):
 
 
 @pytest.mark.parametrize("value_aware", [False, True])
-@pytest.mark.parametrize("L,pb", GRID)
+@pytest.mark.parametrize("L,pb", GRID + [(32768, 128)])  # + config 2's length and budget
 def test_quest_kernel_decode_matches_oracle(L, pb, value_aware):
     from aoakv.utils import (append_kv, decode_estimate, decode_layer, decode_sparse_attn,
                              decode_topk)
