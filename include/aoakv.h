@@ -73,7 +73,11 @@ extern "C" {
 #define AOAKV_FLAG_FIXED 2u       /* force first and last page (sim `fixed`) */
 /* aoakv_sparse_decode_layer only: run scoring, top-k and decode in ONE launch
  * (scoring workers, per-head top-k and decode items handing over through
- * the workspace) instead of two launches. */
+ * the workspace) instead of two launches.  Workgroups wait on lower-indexed
+ * workgroups of the launch, each wait bounded; if one gives up, 32-bit word
+ * 2 of the workspace becomes non-zero, the output is invalid and handoff
+ * words may be left set: call aoakv_workspace_init on the workspace before
+ * using it again. */
 #define AOAKV_FLAG_SINGLE_LAUNCH 4u
 /* The reference KERNEL's selection convention instead of the simulation's
  * (controller.py:113-124, quest/utils/__init__.py:196-246,
