@@ -196,6 +196,19 @@ def decode_workspace(batch: int, num_qo_heads: int, num_kv_heads: int, max_sel_p
     return ws
 
 
+def workspace_wait_failed(workspace: torch.Tensor) -> bool:
+    """True when a one-launch layer call on this workspace had a bounded wait
+    give up (32-bit word 2 of the workspace; reads it back, so it
+    synchronizes).  The output of that call is invalid and the workspace
+    must be re-initialized (``workspace_init``) before it is used again."""
+    return bool(int(workspace[8:12].view(torch.int32).item()))
+
+
+def workspace_init(workspace: torch.Tensor) -> None:
+    """Zero a decode workspace (aoakv_workspace_init) on the current stream."""
+    _lib.call("aoakv_workspace_init", workspace.data_ptr(), workspace.numel(), _stream())
+
+
 def decode_sparse_attn(q, o, kv_data, kv_indptr, kv_indices, kv_last_page_len, sel_pages,
                        token_budget: int, workspace, max_pages: int, num_kv_heads: int,
                        layout: int, token_budgets=None, flags: int = 0):

@@ -153,3 +153,17 @@ def test_rope_validation_without_gpu():
     rc = lib.aoakv_rope_append_kv_cache_decode(1, 1, 1, 1, 32, 1, 1, 1, 1, 1, 1, 1, 1, 1, 32,
                                                128, 16, 1, 1.0, -1.0, nul)
     assert rc == _lib.AOAKV_ERR_INVALID and b"rope_theta" in lib.aoakv_last_error()
+
+
+def test_workspace_wait_flag_reads_word_2():
+    """ops.workspace_wait_failed reads 32-bit word 2 of a workspace (host
+    tensor here: no GPU needed)."""
+    import torch
+    from aoakv import ops
+    ws = torch.zeros(64, dtype=torch.uint8)
+    assert not ops.workspace_wait_failed(ws)
+    ws[8:12].view(torch.int32).fill_(1)
+    assert ops.workspace_wait_failed(ws)
+    ws[8:12].view(torch.int32).fill_(0)
+    ws[12:16].view(torch.int32).fill_(7)   # other words do not count
+    assert not ops.workspace_wait_failed(ws)
