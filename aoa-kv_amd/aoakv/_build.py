@@ -6,6 +6,8 @@
 from __future__ import annotations
 
 import concurrent.futures as cf
+import hashlib
+import json
 import os
 import shutil
 import subprocess
@@ -15,7 +17,10 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 SRC_DIR = os.path.join(os.path.dirname(PKG_DIR), "csrc")
 OBJ_DIR = os.path.join(os.path.dirname(PKG_DIR), "_build")
 LIB = os.path.join(PKG_DIR, "libaoakv.so")
+# build record beside the library (travels with it; the GPU box has no .git)
+BUILDINFO = os.path.join(PKG_DIR, "libaoakv.buildinfo.json")
 SOURCES = ["append.hip", "decode.hip", "prefill.hip", "capi.cpp"]
+REPO_DIR = os.path.dirname(os.path.dirname(PKG_DIR))
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -42,6 +47,50 @@ def _compile(src: str) -> str:
     return obj
 
 
+def source_files() -> list:
+    """Every file the library is compiled from (kernels, headers, the C ABI)."""
+    out = [os.path.join(SRC_DIR, f) for f in sorted(os.listdir(SRC_DIR))
+           if f.endswith((".hip", ".hpp", ".cpp", ".h"))]
+    return out + [os.path.join(REPO_DIR, "include", "aoakv.h")]
+
+
+def source_md5() -> str:
+    """md5 over the library's source files (names and contents, in order)."""
+    h = hashlib.md5()
+    for p in source_files():
+        h.update(os.path.basename(p).encode())
+        with open(p, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
+def file_md5(path: str) -> str:
+    with open(path, "rb") as f:
+        return hashlib.md5(f.read()).hexdigest()
+
+
+def _git(*args) -> str:
+    try:
+        r = subprocess.run(["git", "-C", REPO_DIR, *args], capture_output=True, text=True,
+                           timeout=10)
+        return r.stdout.strip() if r.returncode == 0 else ""
+    except (OSError, subprocess.SubprocessError):
+        return ""
+
+
+def write_buildinfo() -> dict:
+    """Record what the library was built from: the git HEAD of the tree, whether
+    its sources differed from HEAD, the source and library md5s."""
+    head = _git("rev-parse", "HEAD") or None
+    dirty = bool(_git("status", "--porcelain", "--", "aoa-kv_amd/csrc", "include")) \
+        if head else None
+    info = {"git_head": head, "sources_differ_from_head": dirty, "src_md5": source_md5(),
+            "so_md5": file_md5(LIB), "arch": ARCH}
+    with open(BUILDINFO, "w") as f:
+        json.dump(info, f, indent=1)
+    return info
+
+
 def build(verbose: bool = True) -> str:
     """Compile every source for gfx950 and link libaoakv.so.  Always rebuilds."""
     if not os.path.exists(HIPCC):
@@ -57,6 +106,7 @@ def build(verbose: bool = True) -> str:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
     shutil.rmtree(OBJ_DIR, ignore_errors=True)
+    write_buildinfo()
     if verbose:
         print(f"built {LIB} ({os.path.getsize(LIB)} bytes)")
     return LIB

@@ -7,7 +7,10 @@ from __future__ import annotations
 import ctypes
 import os
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libaoakv.so")
+# the package's own build; AOAKV_LIB names another build of the library to
+# load instead (how a driver picks the tree it measures)
+LIB_PATH = os.environ.get("AOAKV_LIB") or os.path.join(
+    os.path.dirname(os.path.abspath(__file__)), "libaoakv.so")
 
 AOAKV_OK = 0
 AOAKV_ERR_INVALID = 1
@@ -70,11 +73,12 @@ class AoakvError(RuntimeError):
 
 
 _lib = None
+_loaded_path = None
 
 
 def load(path: str = LIB_PATH) -> ctypes.CDLL:
     """Load libaoakv.so once and declare every entry point's signature."""
-    global _lib
+    global _lib, _loaded_path
     if _lib is not None:
         return _lib
     if not os.path.exists(path):
@@ -87,7 +91,14 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         fn.argtypes = argtypes
         fn.restype = _RESTYPES.get(name, _int)
     _lib = lib
+    _loaded_path = os.path.abspath(path)
     return lib
+
+
+def loaded_path() -> str:
+    """Path of the library this process loaded."""
+    load()
+    return _loaded_path
 
 
 def call(name: str, *args) -> None:

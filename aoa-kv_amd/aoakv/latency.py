@@ -4,25 +4,32 @@ runs on libaoakv.so, with the reference latency driver's CSV row
 was loaded, GPU, model, context, budget, page size, mean and std of the
 prefill time and of the per-token decode time.
 
-    python -m aoakv.latency --model longchat-7b-v1.5-32k --context_len 8192 \\
-        --decode_len 256 --token_budget 1024 --out results.csv
+    python -m aoakv.latency --kernel aoa_kv --model longchat-7b-v1.5-32k \\
+        --context_len 8192 --decode_len 256 --token_budget 1024 --out results.csv
 
-``--method AOA_KV`` is the value-aware score (the reference's aoa_kv tree),
-``--method QUEST`` the plain Quest bound (its quest_orig tree); both use the
+``--kernel`` picks the tree as the reference driver's flag does
+(bench_latency.py:27-32,49-64): ``aoa_kv`` is the value-aware score (CSV
+method AOA_KV), ``quest_orig`` the plain Quest bound (method QUEST); both
+run on libaoakv.so -- the package's own build, or the one the environment
+variable AOAKV_LIB names -- and the md5 of the library loaded goes into every
+row.  ``--method`` is the older spelling of the same choice.  Both use the
 simulation's selection unless ``--semantics quest_kernel`` asks for the
 reference kernels' convention.  Weights are random and seeded (no checkpoint
 is loaded; latency does not depend on weight values), inputs are random
 embeddings as in the reference driver, and timing uses events with a
-synchronize on both sides after ``--warmup`` discarded iterations.
+synchronize on both sides after ``--warmup`` discarded iterations.  The
+decode workspace's error word is read once per iteration (every step with
+``--debug_checks``); a flagged error ends the run.
 """
 from __future__ import annotations
 
 import argparse
 import csv
 import hashlib
-import sys
 import time
 from pathlib import Path
+
+KERNELS = {"aoa_kv": "AOA_KV", "quest_orig": "QUEST"}   # tree -> CSV method label
 
 CSV_FIELDS = [
     "method", "kernel_md5", "gpu", "model", "context_len", "token_budget",
@@ -34,7 +41,13 @@ CSV_FIELDS = [
 def parse_args(argv=None):
     from .shim import MODEL_SHAPES
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    p.add_argument("--method", choices=["AOA_KV", "QUEST"], default="AOA_KV")
+    p.add_argument("--kernel", choices=sorted(KERNELS), default=None,
+                   help="which tree to measure: aoa_kv (value-aware) or quest_orig (plain Quest)")
+    p.add_argument("--method", choices=sorted(KERNELS.values()), default=None,
+                   help="the same choice by CSV label (AOA_KV / QUEST)")
+    p.add_argument("--debug_checks", action="store_true",
+                   help="read the decode workspace error word after every decode step "
+                        "(synchronizes; off: once per iteration)")
     p.add_argument("--semantics", choices=["sim", "quest_kernel"], default="sim")
     p.add_argument("--model", choices=sorted(MODEL_SHAPES), default="longchat-7b-v1.5-32k")
     p.add_argument("--layers", type=int, default=None,
@@ -48,7 +61,11 @@ def parse_args(argv=None):
     p.add_argument("--three_call", action="store_true",
                    help="decode with the reference's three calls instead of one launch")
     p.add_argument("--out", default=None, help="CSV to append to (optional)")
-    return p.parse_args(argv)
+    args = p.parse_args(argv)
+    if args.kernel and args.method and KERNELS[args.kernel] != args.method:
+        p.error(f"--kernel {args.kernel} and --method {args.method} disagree")
+    args.method = KERNELS[args.kernel] if args.kernel else (args.method or "AOA_KV")
+    return args
 
 
 def main(argv=None):
@@ -59,7 +76,7 @@ def main(argv=None):
     from . import _lib
     from .shim import MODEL_SHAPES, QuestLlamaModel
 
-    lib_path = Path(_lib.LIB_PATH).resolve()
+    lib_path = Path(_lib.loaded_path()).resolve()
     md5 = hashlib.md5(lib_path.read_bytes()).hexdigest()
     device = torch.device("cuda:0")
     dtype = torch.float16
@@ -104,11 +121,11 @@ def main(argv=None):
                 torch.cuda.synchronize()
                 if measured:
                     decode_ms.append(start.elapsed_time(end))
+                if args.debug_checks:
+                    model.iController.check_errors()
+            model.iController.check_errors()  # once per iteration (raises on a flagged error)
             model.quest_clear()
             print(f"iteration {it} done ({'measured' if measured else 'warmup'})", flush=True)
-    err = int(model.iController.workspace[8:12].view(torch.int32).item())
-    if err:
-        sys.exit("a one-launch decode layer timed out waiting (workspace error flag set)")
 
     row = {
         "method": args.method + ("" if args.semantics == "sim" else "_quest_kernel"),

@@ -196,12 +196,27 @@ def decode_workspace(batch: int, num_qo_heads: int, num_kv_heads: int, max_sel_p
     return ws
 
 
+# bits of the workspace error word (aoakv.h AOAKV_WS_ERR_*)
+WS_ERR_WAIT = 1
+WS_ERR_TRUNCATED = 2
+
+
+def workspace_error(workspace: torch.Tensor) -> int:
+    """The workspace's error bits (32-bit word 2, aoakv.h AOAKV_WS_ERR_WORD):
+    WS_ERR_WAIT when a one-launch layer call had a bounded wait give up (its
+    output is invalid; later one-launch calls write NaN until
+    ``workspace_init``), WS_ERR_TRUNCATED when a device page table held more
+    pages than a call was sized for.  Reads the word back, so it
+    synchronizes with the stream."""
+    return int(workspace[8:12].view(torch.int32).item())
+
+
 def workspace_wait_failed(workspace: torch.Tensor) -> bool:
     """True when a one-launch layer call on this workspace had a bounded wait
-    give up (32-bit word 2 of the workspace; reads it back, so it
-    synchronizes).  The output of that call is invalid and the workspace
-    must be re-initialized (``workspace_init``) before it is used again."""
-    return bool(int(workspace[8:12].view(torch.int32).item()))
+    give up (WS_ERR_WAIT; reads the word back, so it synchronizes).  The
+    workspace must be re-initialized (``workspace_init``) before it is used
+    again."""
+    return bool(workspace_error(workspace) & WS_ERR_WAIT)
 
 
 def workspace_init(workspace: torch.Tensor) -> None:

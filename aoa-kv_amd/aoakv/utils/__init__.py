@@ -33,6 +33,7 @@ __all__ = [
     "KvPool",
     "InferenceController",
     "apply_rope_in_place",
+    "rms_norm_forward",
     "append_kv",
     "rope_append_kv",
     "prefill_forward",
@@ -49,6 +50,17 @@ def apply_rope_in_place(q: torch.Tensor, k: torch.Tensor, past_kv_len: int,
     past_kv_len + n (reference __init__.py:25-52; defaults scale 1, theta 1e4)."""
     ops.apply_rope_in_place(q, k, past_kv_len, 1.0 if rope_scale is None else rope_scale,
                             1e4 if rope_theta is None else rope_theta)
+
+
+def rms_norm_forward(input: torch.Tensor, weight: torch.Tensor, epsilon: float) -> torch.Tensor:
+    """RMSNorm of the last dim (reference __init__.py:54-67, which calls the
+    rms_norm kernel of ops/csrc/rms_norm.cu): s = 1/sqrt(mean(x^2) + eps) in
+    fp32 over the fp32 values of x, then x * s * weight in fp32, rounded once
+    to x's dtype.  RMSNorm is outside the decode path, so this is torch on
+    the GPU (hipBLASLt / elementwise), not a libaoakv kernel."""
+    xf = input.float()
+    s = torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + epsilon)
+    return (xf * s * weight.float()).to(input.dtype)
 
 
 def rope_append_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
@@ -162,7 +174,10 @@ def decode_sparse_attn(q: torch.Tensor, iController: InferenceController, layer_
 def decode_layer(q: torch.Tensor, iController: InferenceController, layer_idx: int,
                  single_launch: bool = False) -> torch.Tensor:
     """estimate + top-k + sparse decode in two launches (or one, with
-    ``single_launch``)."""
+    ``single_launch``).  A one-launch call whose wait gave up leaves NaN
+    outputs from then on until the workspace is re-initialized;
+    ``iController.check_errors()`` reports it (and re-initializes), and with
+    ``iController.debug_checks`` it runs after every call."""
     c = iController
     q3 = q.view(1, c.num_heads, c.head_dim)
     o = torch.empty_like(q3)
@@ -172,4 +187,6 @@ def decode_layer(q: torch.Tensor, iController: InferenceController, layer_idx: i
         c.metadata_indptr_for_append, c.metadata_indices, c.v_log_norm_layer(layer_idx),
         c.scores, c._sel, c.token_budget, c.workspace, len(c.kv_cache.indicies), c.layout,
         c.flags | (ops.FLAG_SINGLE_LAUNCH if single_launch else 0))
+    if c.debug_checks:
+        c.check_errors()
     return o.view_as(q)

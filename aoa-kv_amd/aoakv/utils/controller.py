@@ -85,6 +85,9 @@ class InferenceController:
                                 device=device)
         self.workspace = ops.decode_workspace(1, num_heads, self.num_kv_heads, max_kv_pages,
                                               device, max_pages=max_kv_pages)
+        # check the workspace error word after every fused decode layer call
+        # (synchronizes: for debugging; check_errors() once per token is cheap)
+        self.debug_checks = False
 
     # ------------------------------------------------------------ budget
     @property
@@ -154,6 +157,23 @@ class InferenceController:
         if self.quest_kernel:
             return min(max(1, self._page_budget), P)
         return min(max(3, min(L, self.token_budget) // self.page_size), P)
+
+    def check_errors(self):
+        """Raise if a decode call on this controller's workspace flagged an
+        error: a one-launch layer's wait gave up (the workspace is
+        re-initialized, so the next call runs normally again) or a page
+        table exceeded what a call was sized for.  Reads the workspace error
+        word back, so it synchronizes: call it once per generated token, not
+        per layer."""
+        err = ops.workspace_error(self.workspace)
+        if err:
+            ops.workspace_init(self.workspace)
+            what = []
+            if err & ops.WS_ERR_WAIT:
+                what.append("a one-launch decode layer's wait gave up (its outputs are invalid)")
+            if err & ops.WS_ERR_TRUNCATED:
+                what.append("a page table held more pages than the call was sized for")
+            raise RuntimeError("aoakv decode workspace error: " + "; ".join(what))
 
     def clean_states(self):
         self.kv_cache.release()

@@ -110,7 +110,7 @@ int check_group(uint32_t hq, uint32_t hkv) {
 }
 
 struct Workspace {
-  uint32_t* ctl;  // [2] error flag of the single-launch layer
+  uint32_t* ctl;  // word 2 (kErrWord): error bits kErrWait, kErrTruncated
   uint32_t* est_counters;
   uint32_t* dec_counters;
   float* partial;
@@ -182,6 +182,7 @@ int launch_estimate_topk(aoakv::EstimateArgs ea, const Workspace& w, int32_t* se
   ta.Hkv = ea.Hkv;
   ta.S = page_size;
   ta.flags = flags & kSelectFlags;
+  ta.error = ea.error;
   return hip_status(aoakv::launch_topk(ta, batch_size, s), "topk");
 }
 
@@ -415,6 +416,12 @@ int aoakv_topk_filtering(const float* scores, uint32_t score_stride,
   if (int e = check_flags(flags, kSelectFlags, "topk_filtering")) return e;
   REQUIRE(sel_stride >= min_sel_stride(flags), "topk_filtering: sel_stride %u < %u", sel_stride,
           min_sel_stride(flags));
+  // a score row is the candidate set; its length bounds the pages selected from
+  const uint32_t max_row =
+      aoakv::topk_max_pages() - ((flags & AOAKV_FLAG_QUEST_KERNEL) ? 1u : 0u);
+  REQUIRE(score_stride >= 1u && score_stride <= max_row,
+          "topk_filtering: score_stride %u not in [1, %u] (pages per row the top-k holds)",
+          score_stride, max_row);
   aoakv::TopkArgs a{};
   a.scores = scores;
   a.score_stride = score_stride;
@@ -505,8 +512,10 @@ static int fill_decode(aoakv::DecodeArgs& a, Workspace& w, const void* q, void* 
   a.Hkv = num_kv_heads;
   a.S = page_size;
   a.max_chunks = aoakv::decode_chunks(max_sel);
+  a.max_pages = max_pages;
   a.flags = flags & AOAKV_FLAG_QUEST_KERNEL;
   a.g = aoakv::make_geom(layout, num_kv_heads, page_size, head_dim);
+  a.error = w.ctl + aoakv::kErrWord;
   return AOAKV_OK;
 }
 
@@ -561,6 +570,7 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
     return e;
   hipStream_t s = static_cast<hipStream_t>(stream);
   ea.flags &= kSelectFlags;
+  ea.error = da.error;
   if ((flags & AOAKV_FLAG_SINGLE_LAUNCH) && max_pages <= aoakv::fused_topk_max_pages()) {
     // one launch: scoring, top-k and decode items of every head
     aoakv::LayerArgs la{};
@@ -577,7 +587,6 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
     la.d.hsel = w.hsel;
     la.d.hsel_stride = max_sel;
     la.d.hpart = w.hpart;
-    la.d.error = w.ctl + 2;
     // with room for them (aoakv_layer_workspace_size), the scores also go to
     // the top-k as handoff words, polled directly (no arrival counter)
     const size_t words_off = score_words_offset(w.bytes);
@@ -633,6 +642,7 @@ int aoakv_estimate_topk(const void* q, const void* metadata_data, const int32_t*
   const size_t need = ws_layout(batch_size, num_qo_heads, num_kv_heads, max_sel, workspace, &w);
   REQUIRE(workspace_bytes >= need, "estimate_topk: workspace of %zu bytes < %zu needed",
           workspace_bytes, need);
+  ea.error = w.ctl + aoakv::kErrWord;
   return launch_estimate_topk(ea, w, sel_pages, sel_stride, token_budget, token_budgets,
                               batch_size, max_pages, page_size, flags,
                               static_cast<hipStream_t>(stream));

@@ -79,7 +79,7 @@ __device__ inline uint32_t wait_word(const uint32_t* p, uint32_t* error) {
   while ((v = ld_agent_u32(p)) == 0u) {
     __builtin_amdgcn_s_sleep(1);
     if (++it > kSpinLimit) {
-      atomicOr(error, 1u);
+      flag_error(error, kErrWait);
       return 0u;
     }
   }
@@ -207,8 +207,10 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
   if (!SELF && hwords != nullptr && (k == 0u || k >= P)) {
     // the scores are not needed, but their handoff words must be consumed
     for (uint32_t i = tid; i < P; i += kThreads) {
-      for (uint32_t it = 0u; ld_agent_u32(hwords + i) == 0u && it < kSpinLimit; ++it)
-        __builtin_amdgcn_s_sleep(1);
+      uint32_t it = 0u;
+      for (; ld_agent_u32(hwords + i) == 0u && it < kSpinLimit; ++it) __builtin_amdgcn_s_sleep(1);
+      // a word written after this gave up would be left set
+      if (it >= kSpinLimit) flag_error(error, kErrWait);
       st_agent_u32(hwords + i, 0u);
     }
   }
@@ -258,10 +260,12 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
         // cost 1.2 or 0.2 us per layer in memory traffic at config 2)
         if (wave == 0u) {
           const uint32_t* sw = hwords + (P - 1u);
-          for (uint32_t it = 0u; it < kSpinLimit; ++it) {
+          uint32_t it = 0u;
+          for (; it < kSpinLimit; ++it) {
             if (__builtin_amdgcn_ballot_w64(ld_agent_u32(sw) == 0u) == 0u) break;
             __builtin_amdgcn_s_sleep(1);
           }
+          if (it >= kSpinLimit && lane == 0u) flag_error(error, kErrWait);
         }
         __syncthreads();
       }
@@ -286,10 +290,11 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
         __builtin_amdgcn_s_sleep(1);
         load_words();
       }
-      // a wait that gave up is flagged here (SELF) or by the decode items'
-      // waits for this selection; the flag is set outside the poll loop (an
-      // atomic inside it made this loop's code 0.4 us per layer slower)
-      if (SELF && it >= kSpinLimit) atomicOr(error, 1u);
+      // a wait that gave up is flagged here, outside the poll loop (an atomic
+      // inside it made this loop's code 0.4 us per layer slower): words
+      // written after it are left set, and the next launch must not run on
+      // them
+      if (it >= kSpinLimit) flag_error(error, kErrWait);
 #pragma unroll
       for (int m = 0; m < KPT; ++m) {
         const uint32_t i = tid + (uint32_t)m * kThreads;
@@ -467,9 +472,12 @@ struct EstTopkShared {
 
 // Pages of sequence b the scoring covers: never past a score row or the
 // max_pages the grid covers, and within the fused top-k's limit when fused.
-__device__ inline uint32_t est_pages(const EstimateArgs& a, uint32_t b, uint32_t* pbeg_out) {
+// *clamped (if given) tells whether the page table held more.
+__device__ inline uint32_t est_pages(const EstimateArgs& a, uint32_t b, uint32_t* pbeg_out,
+                                     bool* clamped = nullptr) {
   const uint32_t pbeg = (uint32_t)a.kv_indptr[b];
-  uint32_t P = (uint32_t)a.kv_indptr[b + 1] - pbeg;
+  const uint32_t P0 = (uint32_t)a.kv_indptr[b + 1] - pbeg;
+  uint32_t P = P0;
   // a score row holds a score per page, or per page but the last with the
   // quest_kernel convention (the last page is not scored)
   const uint32_t rowcap = a.score_stride + ((a.flags & kFlagQuestKernel) ? 1u : 0u);
@@ -477,23 +485,33 @@ __device__ inline uint32_t est_pages(const EstimateArgs& a, uint32_t b, uint32_t
   if (P > a.max_pages) P = a.max_pages;
   if (P > kFusedTopkMaxPages && a.sel != nullptr) P = kFusedTopkMaxPages;
   *pbeg_out = pbeg;
+  if (clamped != nullptr) *clamped = P != P0;
   return P;
 }
 
 // Scores pages [128*chunk, 128*chunk + 128) of (sequence b, kv head h) and
 // stores them (agent-coherent).  Returns false, uniformly, when the chunk
-// holds no page.
+// holds no page.  A sequence whose page table exceeds what the call covers
+// sets kErrTruncated (once, from its first chunk).
+// One-launch layer: err0 is the error word as read at the workgroup's start,
+// s_err an LDS word it passes through so that the workgroup branches alike;
+// with kErrWait set nothing is stored (handoff words left set by a wait that
+// gave up must not be mixed with this launch's) and the item returns true.
+// Two launches: s_err = nullptr.
 template <int GROUP>
 __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, uint32_t h,
-                                           uint32_t chunk, EstShared& sm) {
+                                           uint32_t chunk, EstShared& sm,
+                                           uint32_t* s_err = nullptr, uint32_t err0 = 0u) {
   float* s_sc = sm.sc;
   const uint32_t lane = __lane_id();
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t row = lane / kLanesPerRow;
   const uint32_t l16 = lane % kLanesPerRow;
   uint32_t pbeg;
-  const uint32_t P = est_pages(a, b, &pbeg);
+  bool clamped;
+  const uint32_t P = est_pages(a, b, &pbeg, &clamped);
   if (chunk * kEstPagesPerBlock >= P) return false;  // uniform per block
+  if (clamped && chunk == 0u && threadIdx.x == 0u) flag_error(a.error, kErrTruncated);
   const uint32_t mbeg = (uint32_t)a.meta_indptr[b];
   const uint32_t d0 = l16 * kVec;
   const bool value_aware = (a.flags & kFlagValueAware) != 0u;
@@ -592,7 +610,10 @@ __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, ui
     if (value_aware) score = score + 2.0f * __shfl(lvn_lane, s * 4 + (int)row);
     if (l16 == 0u) s_sc[wave * kEstPagesPerWave + s * 4 + row] = score;
   }
+  // the snapshot is written here, after every load of the item was issued
+  if (s_err != nullptr && threadIdx.x == 0u) *s_err = err0;
   __syncthreads();
+  if (s_err != nullptr && (*s_err & kErrWait) != 0u) return true;
   float* out = a.scores + ((size_t)b * a.Hkv + h) * a.score_stride;
   {
     const uint32_t p = chunk * kEstPagesPerBlock + threadIdx.x;
@@ -649,7 +670,7 @@ __device__ __forceinline__ void select_item(const EstimateArgs& a, uint32_t b, u
   topk_staged(a.scores + ((size_t)b * a.Hkv + h) * a.score_stride, P, k,
               (a.flags & kFlagFixed) != 0u, a.kv_indices + pbeg,
               a.sel + ((size_t)b * a.Hkv + h) * a.sel_stride, tk, hout, a.hsel_stride, GROUP,
-              hwords);
+              hwords, a.error);
 }
 
 // Scores one chunk; with a.sel set, the last block of the head to finish
@@ -688,8 +709,13 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopkArgs a) {
   if (P == 0u) return;
   const bool quest = (a.flags & kFlagQuestKernel) != 0u;
   const uint32_t rowcap = a.score_stride + (quest ? 1u : 0u);  // see est_pages
+  // candidates are the pages the score row holds (as the reference's top-k
+  // over an [H, n] row); a longer page table is flagged where there is a
+  // workspace (the entry point checks score_stride against kTopkMaxPages)
+  const uint32_t P0 = P;
   if (P > rowcap) P = rowcap;
   if (P > kTopkMaxPages) P = kTopkMaxPages;
+  if (P != P0 && h == 0u && threadIdx.x == 0u) flag_error(a.error, kErrTruncated);
   const uint32_t L = (P - 1u) * a.S + (uint32_t)a.kv_last_page_len[b];
   const uint32_t budget = a.token_budgets ? (uint32_t)a.token_budgets[b] : a.token_budget;
   uint32_t k = num_selected_pages(L, budget, a.S, P, a.flags);
@@ -750,11 +776,15 @@ struct DecShared {
 // QUEST (quest_kernel convention): the selection rows hold the pages chosen
 // besides the last page, which is always attended as the final entry
 // (quest/utils/__init__.py:237, approx_attn.cu:68-151).
+// One launch: err0 is the error word as read at the workgroup's start and
+// s_err an LDS word for it; with kErrWait set no handoff word is touched and
+// the head's output is NaN (written by its chunk 0).
 template <bool HANDOFF, bool QUEST, bool SELF = false>
 __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uint32_t hq,
                                             uint32_t chunk, DecShared& sm,
                                             const EstimateArgs* ea = nullptr,
-                                            TopkShared* tk = nullptr) {
+                                            TopkShared* tk = nullptr, uint32_t* s_err = nullptr,
+                                            uint32_t err0 = 0u) {
   static_assert(!SELF || HANDOFF, "self-selection is a one-launch mode");
   float (*s_o)[kHeadDim] = sm.o;
   float (*s_ml)[2] = sm.ml;
@@ -775,7 +805,11 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   // for it before issuing the next).  The page-table words, the selection
   // entries and q need no earlier load, so they are all issued first.
   const uint32_t pbeg = (uint32_t)a.kv_indptr[b];
-  const uint32_t P = (uint32_t)a.kv_indptr[b + 1] - pbeg;
+  const uint32_t P_table = (uint32_t)a.kv_indptr[b + 1] - pbeg;
+  // a page table longer than the call was sized for is cut where the
+  // scoring cuts it (est_pages), so the selection's size and the decode's
+  // agree; flagged once per (sequence, head)
+  const uint32_t P = P_table < a.max_pages ? P_table : a.max_pages;
   const uint32_t lpl = (uint32_t)a.kv_last_page_len[b];
   const int32_t tbv = *(a.token_budgets ? a.token_budgets + b : a.kv_indptr + b);
   const uint32_t budget = a.token_budgets ? (uint32_t)tbv : a.token_budget;
@@ -803,11 +837,22 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   // waits until the score words [0, pl.P) are written, then clears them
   auto consume_words = [&]() {
     for (uint32_t i = threadIdx.x; i < pl.P; i += kThreads) {
-      for (uint32_t it = 0u; ld_agent_u32(words + i) == 0u && it < kSpinLimit; ++it)
-        __builtin_amdgcn_s_sleep(1);
+      uint32_t it = 0u;
+      for (; ld_agent_u32(words + i) == 0u && it < kSpinLimit; ++it) __builtin_amdgcn_s_sleep(1);
+      if (it >= kSpinLimit) flag_error(a.error, kErrWait);  // a late word would be left set
       st_agent_u32(words + i, 0u);
     }
   };
+  if constexpr (HANDOFF) {
+    if (threadIdx.x == 0u) *s_err = err0;
+    __syncthreads();
+    if ((*s_err & kErrWait) != 0u) {
+      if (chunk == 0u && threadIdx.x < (uint32_t)kHeadDim)
+        a.o[bh * kHeadDim + threadIdx.x] = (f16)__builtin_nanf("");
+      return;
+    }
+  }
+  if (P != P_table && chunk == 0u && threadIdx.x == 0u) flag_error(a.error, kErrTruncated);
   if (P == 0u || lpl == 0u || lpl > S) {  // malformed page table
     if (SELF && chunk == 0u) consume_words();  // the words were written all the same
     return;
@@ -825,7 +870,10 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   // the grid holds max_chunks blocks per head; never index partials past it
   const uint32_t cap =
       a.max_chunks < (uint32_t)kMergeMaxChunks ? a.max_chunks : (uint32_t)kMergeMaxChunks;
-  if (npages > cap * kDecPagesPerBlock) npages = cap * kDecPagesPerBlock;
+  if (npages > cap * kDecPagesPerBlock) {  // more pages than the call was sized for
+    npages = cap * kDecPagesPerBlock;
+    if (chunk == 0u && threadIdx.x == 0u) flag_error(a.error, kErrTruncated);
+  }
   const uint32_t nch = (npages + kDecPagesPerBlock - 1) / kDecPagesPerBlock;
   if (chunk >= nch) return;  // uniform per block
   // entries [0, nsel) come from the selection; with QUEST the entry after
@@ -846,7 +894,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
     auto entry = [&](uint32_t i) -> uint32_t {
       if (i >= nsel) return 0u;
       if (i >= nout) {
-        atomicOr(a.error, 1u);
+        flag_error(a.error, kErrWait);
         return 0u;
       }
       return self_topk ? tk->key[i] : (uint32_t)ids[i];
@@ -1064,7 +1112,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
       uint32_t it = 0u;
       while (missing()) {
         if (++it > kSpinLimit) {
-          atomicOr(a.error, 1u);
+          flag_error(a.error, kErrWait);
           break;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -1183,6 +1231,14 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
     DecShared d;
   } sm;
   __shared__ uint32_t s_ok;
+  // The error word as it stands when the workgroup starts: kErrWait there
+  // means an earlier launch's wait gave up and may have left handoff words
+  // set, so no workgroup touches one (every role checks the snapshot, passed
+  // through s_err, before its first handoff access) and the output is NaN
+  // until the caller re-initialises the workspace.  Read here, checked once
+  // the role's first loads are in flight.
+  __shared__ uint32_t s_err;
+  const uint32_t err0 = ld_agent_u32(la.d.error);
   const uint32_t t = blockIdx.x;
   if (t < la.n_workers) {
     {  // first item's head bh0 starts bh0 * stagger cycles in (see layer_stagger_cycles)
@@ -1193,7 +1249,8 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
     for (uint32_t i = t; i < la.n_est; i += la.n_workers) {
       const uint32_t bh = i / la.est_chunks, chunk = i % la.est_chunks;
       const uint32_t b = bh / la.e.Hkv, h = bh % la.e.Hkv;
-      if (score_item<GROUP>(la.e, b, h, chunk, sm.e.e)) {
+      if (score_item<GROUP>(la.e, b, h, chunk, sm.e.e, &s_err, err0)) {
+        if ((s_err & kErrWait) != 0u) return;  // uniform: read after score_item's barrier
         if (la.e.hscore != nullptr) {
           // the scores went out as handoff words: only end this item's use
           // of LDS before the next item's
@@ -1217,6 +1274,9 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
     if (P == 0u) return;
     const uint32_t nch = (P + kEstPagesPerBlock - 1) / kEstPagesPerBlock;
     const SelPlan plan = plan_select(la.e, b);
+    if (threadIdx.x == 0u) s_err = err0;
+    __syncthreads();
+    if ((s_err & kErrWait) != 0u) return;
     if (la.e.hscore != nullptr) {  // the top-k polls the score words itself
       select_item<GROUP>(la.e, b, h, plan, sm.e.tk);
       return;
@@ -1226,7 +1286,7 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
       while (ld_agent_u32(la.e.counters + bh * kCounterStride) < nch) {
         __builtin_amdgcn_s_sleep(1);
         if (++it > kSpinLimit) {
-          atomicOr(la.d.error, 1u);
+          flag_error(la.d.error, kErrWait);
           ok = 0u;
           break;
         }
@@ -1251,9 +1311,9 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
       const unsigned long long wait =
           (unsigned long long)(bh < first_round ? bh : first_round) * la.stagger;
       while (clock64() - t0 < wait) __builtin_amdgcn_s_sleep(8);
-      decode_item<true, QUEST, true>(la.d, b, hq, chunk, sm.d, &la.e, &sm.e.tk);
+      decode_item<true, QUEST, true>(la.d, b, hq, chunk, sm.d, &la.e, &sm.e.tk, &s_err, err0);
     } else {
-      decode_item<true, QUEST>(la.d, b, hq, chunk, sm.d);
+      decode_item<true, QUEST>(la.d, b, hq, chunk, sm.d, nullptr, nullptr, &s_err, err0);
     }
   }
 }

@@ -10,6 +10,23 @@ namespace aoakv {
 // line slow each other's atomics and polls.
 constexpr uint32_t kCounterStride = 32;
 
+// Bits of the workspace error word (32-bit word 2 of a workspace):
+//   kErrWait       a bounded wait of the one-launch layer gave up; its output
+//                  is invalid and handoff words may be left set
+//   kErrTruncated  a sequence's device page table holds more pages than the
+//                  call was sized for (max_pages, a score or selection row,
+//                  or a kernel limit); that sequence was computed on a
+//                  truncated page list
+constexpr uint32_t kErrWait = 1u;
+constexpr uint32_t kErrTruncated = 2u;
+// Workspace word that holds the error bits.
+constexpr uint32_t kErrWord = 2u;
+
+// Sets error bits (a no-op for entry points without a workspace).
+__device__ inline void flag_error(uint32_t* error, uint32_t bits) {
+  if (error != nullptr) atomicOr(error, bits);
+}
+
 // RoPE frequencies f_i = rcp_scale * rcp_theta^(2i / 128), i < 64: fixed by
 // (rope_scale, rope_theta), so computed once on the host (rope_freqs) and
 // passed with the launch instead of per lane on the device.
@@ -89,6 +106,7 @@ struct EstimateArgs {
   // instead of an arrival counter and clears them
   uint32_t* hscore;
   uint32_t hscore_stride;
+  uint32_t* error;  // workspace error word, or nullptr (no workspace)
 };
 
 struct TopkArgs {
@@ -102,6 +120,7 @@ struct TopkArgs {
   int32_t* sel;
   uint32_t sel_stride;
   uint32_t Hkv, S, flags;
+  uint32_t* error;  // workspace error word, or nullptr (no workspace)
 };
 
 struct DecodeArgs {
@@ -118,6 +137,7 @@ struct DecodeArgs {
   float* partial;      // [B*Hq, max_chunks, kPartialStride]
   uint32_t* counters;  // [B*Hq]
   uint32_t Hq, Hkv, S, max_chunks;
+  uint32_t max_pages;  // pages per sequence the call is sized for (as the scoring's)
   uint32_t flags;      // kFlagQuestKernel: the quest_kernel selection convention
   PageGeom g;
   // single launch only: handoff buffers whose words hold value + 1 (0 = not
@@ -125,7 +145,7 @@ struct DecodeArgs {
   uint32_t* hsel;      // [B, Hq, hsel_stride] selection of this launch
   uint32_t hsel_stride;
   uint32_t* hpart;     // [B*Hq, max_chunks, kPartialStride] split-K partials
-  uint32_t* error;     // set when a wait gave up
+  uint32_t* error;     // workspace error word (kErrWait, kErrTruncated)
 };
 
 struct PrefillArgs {

@@ -205,11 +205,12 @@ def prefill_bench(dev, layout, L, reps=5):
     return us, flops / (us * 1e-6) / 1e12
 
 
-def ragged_batch_bench(dev, layout, reps=20):
-    """Config 5: batch 16, L_i ~ U[8192, 65536] (seeded), budget min(2048, L/8),
-    keys with 4 channels x8, values of 10% of the pages x4.  One fused layer
-    call for the whole batch; algorithmic bytes summed per sequence."""
-    import numpy as np
+def ragged_batch_inputs(dev, layout, keep_kv=False):
+    """Config 5's seeded batch: 16 sequences, L_i ~ U[8192, 65536], budget
+    min(2048, L/8), keys with 4 channels x8, values of 10% of the pages x4,
+    written into one paged cache (shuffled pages) through the library's bulk
+    append.  With keep_kv, each sequence's K and V also come back as CPU
+    fp16 tensors [H, L, D] (for the oracle)."""
     import torch
     from aoakv import ops
     Bn = 16
@@ -232,6 +233,7 @@ def ragged_batch_bench(dev, layout, reps=20):
         indptr.append(indptr[-1] + Pb)
         mindptr.append(mindptr[-1] + Pm)
     g = torch.Generator(device=dev).manual_seed(6)
+    kept = []
     for b, Lb in enumerate(Ls):
         kk = torch.randn((Lb, H, D), generator=g, device=dev)
         ch = torch.randperm(D, generator=gen)[:4].to(dev)
@@ -240,19 +242,33 @@ def ragged_batch_bench(dev, layout, reps=20):
         pages4 = torch.rand(Ps[b], generator=gen) < 0.1
         tok4 = pages4.repeat_interleave(S)[:Lb].to(dev)
         vv[tok4] *= 4.0
+        kk, vv = kk.half(), vv.half()
         idx_b = perm[indptr[b]:indptr[b + 1]].to(dev)
         midx_b = torch.arange(mindptr[b], mindptr[b + 1], dtype=torch.int32, device=dev)
-        ops.append_kv_cache_prefill(kk.half(), vv.half(), kv, idx_b, Ps[b], (Lb - 1) % S + 1,
+        ops.append_kv_cache_prefill(kk, vv, kv, idx_b, Ps[b], (Lb - 1) % S + 1,
                                     meta, midx_b, lvn, vmean, layout)
+        if keep_kv:
+            kept.append((kk.permute(1, 0, 2).contiguous().cpu(),
+                         vv.permute(1, 0, 2).contiguous().cpu()))
         del kk, vv
     t = lambda x: torch.tensor(x, dtype=torch.int32, device=dev)
-    kv_indptr, m_indptr = t(indptr), t(mindptr)
-    kv_indices, m_indices = perm.to(dev), torch.arange(totm, dtype=torch.int32, device=dev)
-    lpl = t([(Lb - 1) % S + 1 for Lb in Ls])
-    tb = t(budgets)
     ks = [min(max(3, min(Lb, bb) // S), Pb) for Lb, bb, Pb in zip(Ls, budgets, Ps)]
-    maxP, kmax = max(Ps), max(ks)
     q = torch.randn((Bn, H, D), generator=g, device=dev).half()
+    return dict(Ls=Ls, budgets=budgets, Ps=Ps, ks=ks, kv=kv, meta=meta, lvn=lvn, vmean=vmean,
+                kv_indptr=t(indptr), m_indptr=t(mindptr), kv_indices=perm.to(dev),
+                m_indices=torch.arange(totm, dtype=torch.int32, device=dev),
+                lpl=t([(Lb - 1) % S + 1 for Lb in Ls]), tb=t(budgets), q=q, kept=kept)
+
+
+def ragged_batch_bench(dev, layout, reps=20):
+    """Config 5: one fused layer call for the whole batch (ragged_batch_inputs);
+    algorithmic bytes summed per sequence."""
+    import torch
+    from aoakv import ops
+    R = ragged_batch_inputs(dev, layout)
+    Ls, Ps, ks = R["Ls"], R["Ps"], R["ks"]
+    Bn, maxP, kmax = len(Ls), max(Ps), max(ks)
+    q = R["q"]
     o = torch.empty_like(q)
     scores = torch.empty((Bn, H, maxP), dtype=torch.float32, device=dev)
     sel = torch.empty((Bn, H, kmax), dtype=torch.int32, device=dev)
@@ -262,9 +278,10 @@ def ragged_batch_bench(dev, layout, reps=20):
     out = {"bytes": int(nbytes), "contexts": Ls, "pages_selected": ks}
     base = ops.FLAG_VALUE_AWARE | ops.FLAG_FIXED
     for name, flags in (("two_launch", base), ("one_launch", base | ops.FLAG_SINGLE_LAUNCH)):
-        call = lambda: ops.sparse_decode_layer(q, o, kv, kv_indptr, kv_indices, lpl, meta,
-                                               m_indptr, m_indices, lvn, scores, sel, 0, ws, maxP,
-                                               layout, flags, token_budgets=tb)
+        call = lambda: ops.sparse_decode_layer(q, o, R["kv"], R["kv_indptr"], R["kv_indices"],
+                                               R["lpl"], R["meta"], R["m_indptr"],
+                                               R["m_indices"], R["lvn"], scores, sel, 0, ws, maxP,
+                                               layout, flags, token_budgets=R["tb"])
         call()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -279,6 +296,25 @@ def ragged_batch_bench(dev, layout, reps=20):
     return out
 
 
+def _threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+        return max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:
+        return 1
+
+
+def _median_time(fn, reps: int, warm: int = 1) -> float:
+    times = []
+    for r in range(reps + warm):
+        t0 = time.perf_counter()
+        fn()
+        if r >= warm:
+            times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2]
+
+
 def cpu_baseline(k0, v0, q0, reps):
     """The oracle's sparse decode of one config-2 layer on the host cores:
     page scores of all 2048 pages, top-k mask, masked attention over all
@@ -289,35 +325,126 @@ def cpu_baseline(k0, v0, q0, reps):
     V = v0.numpy().transpose(1, 0, 2)[None]
     q = q0.cpu().numpy()[0][:, None, :][None]
     st = sim.SimLayerState(K, V)
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:
-        threads = 1
-    times = []
-    o = None
-    for r in range(reps + 1):
-        t0 = time.perf_counter()
+    threads = _threads()
+    res = {}
+
+    def run():
         scores, pages = sim.select_pages(copy.copy(st), q, BUDGET, True, True)
         mask = sim.pages_to_token_mask(pages, S, L)
-        o = sim.masked_decode_attention(q, K, V, mask)
-        t1 = time.perf_counter()
-        if r > 0:
-            times.append(t1 - t0)
-    times.sort()
-    med = times[len(times) // 2]
+        res.update(o=sim.masked_decode_attention(q, K, V, mask), pages=pages, scores=scores)
+
+    med = _median_time(run, reps)
     return dict(value=med * 1e6, unit="us/layer", cores=int(threads), kind="port",
                 sample=f"layer 0 of config 2 (32 heads, 32768 tokens, budget 2048), "
                        f"{reps} reps after 1 warmup, median; numpy oracle, BLAS threads={threads}, "
-                       f"os.cpu_count()={os.cpu_count()}, cpu={cpu_model()}",
-                o=o, pages=pages, scores=scores)
+                       f"os.cpu_count()={os.cpu_count()}, cpu={cpu_model()}", **res)
+
+
+def cpu_baselines_other_configs(k0, v0):
+    """The numpy oracle on the host cores for BASELINE configs 1, 3a, 3b, 4
+    (8k) and 5, each on a bounded sample (stated), next to the GPU figures.
+    k0, v0: layer 0's K, V [32768, 32, 128] fp16 (CPU)."""
+    import numpy as np
+    import torch
+    from oracle import sim
+    thr = _threads()
+    out = {"cores": int(thr), "kind": "port", "cpu": cpu_model()}
+    K = k0.numpy().transpose(1, 0, 2)[None]          # (1, H, L, D)
+    V = v0.numpy().transpose(1, 0, 2)[None]
+    # config 1: 4096 tokens, budget 1024, seeded N(0,1) drawn on the CPU
+    g = torch.Generator().manual_seed(0)
+    q1 = torch.randn((1, H, 1, D), generator=g).half().numpy()
+    K1 = torch.randn((1, H, 4096, D), generator=g).half().numpy()
+    V1 = torch.randn((1, H, 4096, D), generator=g).half().numpy()
+    st1 = sim.SimLayerState(K1, V1)
+
+    def c1():
+        _, pages = sim.select_pages(copy.copy(st1), q1, 1024, True, True)
+        sim.masked_decode_attention(q1, K1, V1, sim.pages_to_token_mask(pages, S, 4096))
+
+    out["config1_us_per_layer"] = round(_median_time(c1, 10) * 1e6, 1)
+    out["config1_sample"] = "one layer, 10 reps after 1 warmup, median"
+    # config 3a: metadata build (page filters, page means of V, log-norm)
+    def c3a():
+        sim.get_max_min_filters(K, S)
+        sim.log_v_norm(sim.compute_page_v_mean(L, S, V))
+
+    out["config3a_us"] = round(_median_time(c3a, 3) * 1e6, 1)
+    out["config3a_sample"] = ("32 heads x 32768 tokens of layer 0's K, V (K with its x8 "
+                              "channels), 3 reps after 1 warmup, median")
+    # config 3b: decode appends after a 4103-token prefill (the simulation
+    # appends by concatenation, so a step costs O(L))
+    st = sim.SimLayerState(K[:, :, :4103], V[:, :, :4103])
+    n3b = 64
+    t0 = time.perf_counter()
+    for i in range(n3b):
+        st.append(K[:, :, 4103 + i:4104 + i], V[:, :, 4103 + i:4104 + i])
+    out["config3b_us_per_append"] = round((time.perf_counter() - t0) / n3b * 1e6, 1)
+    out["config3b_sample"] = f"the first {n3b} of the 512 appends, mean"
+    # config 4 (8k): causal prefill in fp64, a sample of query rows
+    g4 = torch.Generator().manual_seed(0)
+    q4 = (torch.randn((8192, H, D), generator=g4) * 0.5).half().numpy()
+    k4 = (torch.randn((8192, H, D), generator=g4) * 0.5).half().numpy()
+    v4 = (torch.randn((8192, H, D), generator=g4) * 0.5).half().numpy()
+    rows = np.arange(32, 8192, 128)                  # 64 rows, mean causal length = the full set's
+    t0 = time.perf_counter()
+    sim.causal_prefill_rows(q4, k4, v4, rows)
+    per_row = (time.perf_counter() - t0) / len(rows)
+    out["config4_8k_us"] = round(per_row * 8192 * 1e6, 1)
+    out["config4_8k_TFLOPs"] = round(8192 * 8192 * 2 * H * D / (per_row * 8192) / 1e12, 5)
+    out["config4_sample"] = ("64 evenly spaced query rows of 8192 (fp64 numpy, textbook "
+                             "causal attention), time x 8192 / 64")
+    # config 5: the oracle's sparse decode of two of the batch's sequences,
+    # scaled to the batch by tokens (its cost is linear in the context)
+    gen = torch.Generator().manual_seed(5)
+    Ls = torch.randint(8192, 65537, (16,), generator=gen).tolist()
+    samp = [min(Ls), Ls[0]]
+    gq = torch.Generator().manual_seed(7)
+    t_tot = 0.0
+    for Lb in samp:
+        Kb, Vb = K[:, :, :min(Lb, L)], V[:, :, :min(Lb, L)]
+        if Lb > L:  # longer than layer 0's cache: tile it
+            reps = -(-Lb // L)
+            Kb = np.concatenate([K] * reps, axis=2)[:, :, :Lb]
+            Vb = np.concatenate([V] * reps, axis=2)[:, :, :Lb]
+        qb = torch.randn((1, H, 1, D), generator=gq).half().numpy()
+        stb = sim.SimLayerState(Kb, Vb)
+        bud = min(2048, Lb // 8)
+        t0 = time.perf_counter()
+        _, pages = sim.select_pages(stb, qb, bud, True, True)
+        sim.masked_decode_attention(qb, Kb, Vb, sim.pages_to_token_mask(pages, S, Lb))
+        t_tot += time.perf_counter() - t0
+    out["config5_us_per_batch_layer"] = round(t_tot * sum(Ls) / sum(samp) * 1e6, 1)
+    out["config5_sample"] = (f"sequences of {samp[0]} and {samp[1]} tokens of the batch "
+                             f"(K/V of layer 0, tiled past 32768), one pass each, scaled to the "
+                             f"batch's {sum(Ls)} tokens")
+    return out
+
+
+def so_identity() -> dict:
+    """md5 of the library this process loaded, its build record and whether
+    the tree's sources still match that record."""
+    from aoakv import _build, _lib
+    path = _lib.loaded_path()
+    info = {"so_path": os.path.relpath(path, ROOT), "so_md5": _build.file_md5(path)}
+    try:
+        rec = json.load(open(_build.BUILDINFO))
+    except (OSError, ValueError):
+        rec = {}
+    info["git_head"] = rec.get("git_head")
+    info["sources_differ_from_head"] = rec.get("sources_differ_from_head")
+    info["src_md5"] = _build.source_md5()
+    info["built_from_these_sources"] = (rec.get("src_md5") == info["src_md5"] and
+                                        rec.get("so_md5") == info["so_md5"])
+    return info
 
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=3200, help="layers timed (multiple of 32)")
-    ap.add_argument("--warmup", type=int, default=320)
+    ap.add_argument("--steps", type=int, default=3200,
+                    help="layers timed (one graph of exactly this many launches)")
+    ap.add_argument("--warmup", type=int, default=320, help="untimed layers before")
     ap.add_argument("--layout", choices=["hnd", "nhd"], default="hnd")
     ap.add_argument("--cpu-reps", type=int, default=20,
                     help="timed oracle passes over layer 0 (about 0.5 s each on 16 host threads: "
@@ -338,6 +465,9 @@ def main():
                           "taking H/N heads with no exchange inside the path); run with "
                           "--gpus 1"}))
         sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        print(json.dumps({"error": "--steps must be >= 1 and --warmup >= 0"}))
+        sys.exit(2)
 
     import numpy as np
     import torch
@@ -348,8 +478,8 @@ def main():
     torch.cuda.set_device(0)
     layout = ops.HND if args.layout == "hnd" else ops.NHD
     n_layers = 32
-    steps = max(n_layers, (args.steps // n_layers) * n_layers)
-    warm = max(n_layers, (args.warmup // n_layers) * n_layers)
+    steps, warm = args.steps, args.warmup
+    n_aux = max(steps, 320)   # launches behind the secondary figures
 
     if args.prefill_pass:
         res = {"workload": "BASELINE config 4: causal paged prefill, 32 heads x 128, fp16",
@@ -365,6 +495,7 @@ def main():
     log(f"[bench] {aoakv.version()} layout={args.layout} building {n_layers} layers ...")
     B = build_layers(n_layers, layout, dev)
     kv, meta, lvn, idx, midx, q = B["kv"], B["meta"], B["lvn"], B["idx"], B["midx"], B["q"]
+    k0_cpu, v0_cpu, append_us = B["k0"], B["v0"], B["append_us"]
     indptr = torch.tensor([0, P], dtype=torch.int32, device=dev)
     mindptr = torch.tensor([0, midx.numel()], dtype=torch.int32, device=dev)
     lpl = torch.tensor([S], dtype=torch.int32, device=dev)
@@ -374,9 +505,16 @@ def main():
     ws = ops.decode_workspace(1, H, H, K_SEL, dev, max_pages=P)
     flags = ops.FLAG_VALUE_AWARE | ops.FLAG_FIXED
 
-    def layer(l):
-        ops.sparse_decode_layer(q[l], o[l], kv[l], indptr, idx[l], lpl, meta[l], mindptr, midx,
-                                lvn[l], scores[l], sel[l], BUDGET, ws, P, layout, flags)
+    def make_layer(kv_, meta_, lvn_, o_, extra_flags):
+        def fn(l):
+            ops.sparse_decode_layer(q[l], o_[l], kv_[l], indptr, idx[l], lpl, meta_[l], mindptr,
+                                    midx, lvn_[l], scores[l], sel[l], BUDGET, ws, P, layout_of[0],
+                                    flags | extra_flags)
+        return fn
+
+    layout_of = [layout]
+    layer2 = make_layer(kv, meta, lvn, o, 0)                       # two launches
+    layer1 = make_layer(kv, meta, lvn, o, ops.FLAG_SINGLE_LAUNCH)  # one launch: the measured path
 
     def est(l):
         ops.estimate_topk(q[l], meta[l], mindptr, midx, indptr, idx[l], lpl, lvn[l], scores[l],
@@ -387,7 +525,7 @@ def main():
                                layout)
 
     for l in range(n_layers):
-        layer(l)
+        layer2(l)
     torch.cuda.synchronize()
     if args.pmc_pass:
         src = torch.empty(64 << 20, dtype=torch.uint8, device=dev).fill_(1)
@@ -396,15 +534,14 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         for l in range(n_layers):
-            ops.sparse_decode_layer(q[l], o[l], kv[l], indptr, idx[l], lpl, meta[l], mindptr,
-                                    midx, lvn[l], scores[l], sel[l], BUDGET, ws, P, layout,
-                                    flags | ops.FLAG_SINGLE_LAUNCH)
+            layer1(l)
         torch.cuda.synchronize()
         log("[bench] pmc pass done")
         return
 
-    def capture(fn):
-        g = torch.cuda.CUDAGraph()
+    def capture(fn, n):
+        """A HIP graph of exactly n launches, fn(i % n_layers) for i < n, as a
+        decode loop replays one layer after another."""
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
@@ -412,71 +549,76 @@ def main():
                 fn(l)
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            for l in range(n_layers):
-                fn(l)
+            for i in range(n):
+                fn(i % n_layers)
         torch.cuda.synchronize()
         return g
 
-    def time_graph(g, reps_layers):
-        reps = reps_layers // n_layers
+    def replay_timed(g, n):
+        """us per launch over one replay of an n-launch graph.  Synchronized on
+        both sides; a spin kernel keeps the stream busy while the host submits
+        the graph, so the events bracket the n launches and not the submit."""
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
+        torch.cuda._sleep(200000)
         e0.record()
-        for _ in range(reps):
-            g.replay()
+        g.replay()
         e1.record()
         torch.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1e3 / (reps * n_layers)  # us per layer
+        return e0.elapsed_time(e1) * 1e3 / n
 
-    # two launches per layer (scores + top-k, then decode)
-    g_layer = capture(layer)
-    time_graph(g_layer, warm)
-    # replays must reproduce the eager result exactly
-    o_eager = o.clone()
-    sel_eager = sel.clone()
-    g_layer.replay()
+    # two launches per layer (scores + top-k, then decode): the reference's
+    # split, timed beside the measured path and the source of the equality check
+    g2 = capture(layer2, n_aux)
+    g2.replay()
+    torch.cuda.synchronize()
+    o_eager, sel_eager = o.clone(), sel.clone()
+    g2.replay()
     torch.cuda.synchronize()
     replay_exact = bool(torch.equal(o, o_eager) and torch.equal(sel, sel_eager))
-    us_two = time_graph(g_layer, steps)
+    us_two = replay_timed(g2, n_aux)
+    del g2
 
-    # one launch per layer: the measured path
-    def layer1(l):
-        ops.sparse_decode_layer(q[l], o[l], kv[l], indptr, idx[l], lpl, meta[l], mindptr, midx,
-                                lvn[l], scores[l], sel[l], BUDGET, ws, P, layout,
-                                flags | ops.FLAG_SINGLE_LAUNCH)
-
-    g_one = capture(layer1)
-    time_graph(g_one, warm)
+    # the measured path: W warmup launches, then exactly K timed launches
+    g1 = capture(layer1, steps)
+    if warm > 0:
+        gw = capture(layer1, warm)
+        gw.replay()
+        torch.cuda.synchronize()
+        del gw
     o.zero_()
     sel.zero_()
-    g_one.replay()
-    torch.cuda.synchronize()
-    one_exact = bool(torch.equal(o, o_eager) and torch.equal(sel, sel_eager))
-    log(f"[bench] timing {steps} layers (graph replay, one launch per layer) ...")
-    us_one = time_graph(g_one, steps)
-    spin_err = int(ws[8:12].view(torch.int32).item())
-    if spin_err != 0 or not one_exact:
-        raise SystemExit(f"single-launch layer failed: error flag {spin_err}, "
+    log(f"[bench] timing {steps} layers (one graph of {steps} one-launch layers) ...")
+    us_one = replay_timed(g1, steps)
+    # every layer of the rotation ran at least once in the timed graph when
+    # steps >= 32; the layers it reached must equal the two-launch results
+    reached = min(steps, n_layers)
+    one_exact = bool(torch.equal(o[:reached], o_eager[:reached]) and
+                     torch.equal(sel[:reached], sel_eager[:reached]))
+    err_word = ops.workspace_error(ws)
+    if err_word != 0 or not one_exact:
+        raise SystemExit(f"single-launch layer failed: workspace error word {err_word}, "
                          f"equal to two launches: {one_exact}")
+    del g1
     us_layer = us_one
-    g_est, g_dec = capture(est), capture(dec)
-    time_graph(g_est, warm)
-    time_graph(g_dec, warm)
-    us_est = time_graph(g_est, steps)
-    us_dec = time_graph(g_dec, steps)
+    g_est, g_dec = capture(est, n_aux), capture(dec, n_aux)
+    us_est = replay_timed(g_est, n_aux)
+    us_dec = replay_timed(g_dec, n_aux)
+    del g_est, g_dec
     extra = {}
     if not args.no_extra:
         torch.cuda.synchronize()
         t0 = torch.cuda.Event(enable_timing=True)
         t1 = torch.cuda.Event(enable_timing=True)
         t0.record()
-        for i in range(steps):
+        for i in range(n_aux):
             layer1(i % n_layers)
         t1.record()
         torch.cuda.synchronize()
-        extra["eager_us_per_layer"] = round(t0.elapsed_time(t1) * 1e3 / steps, 3)
-        app = B["append_us"][1:]
+        extra["eager_us_per_layer"] = round(t0.elapsed_time(t1) * 1e3 / n_aux, 3)
+        app = append_us[1:]
         app_bytes = 2 * L * H * D * 2 * 2 + H * P * 2 * D * 2 + H * P * 2 + H * P * D * 2
         extra["bulk_append_32k_us"] = round(float(np.median(app)), 2)
         extra["bulk_append_32k_GBps"] = round(app_bytes / (np.median(app) * 1e-6) / 1e9, 1)
@@ -494,20 +636,50 @@ def main():
             extra[f"prefill_{Lp // 1024}k_mfma_frac"] = round(tf / 2500.0, 4)
         log("[bench] config 5 (ragged batch) ...")
         extra["config5_ragged_batch16"] = ragged_batch_bench(dev, layout)
+        # the same 32 layers in the other cache layout (the reference's
+        # drop-in layout is NHD): same seeds, so the same bits are expected
+        other = ops.NHD if layout == ops.HND else ops.HND
+        oname = "nhd" if other == ops.NHD else "hnd"
+        log(f"[bench] {oname.upper()} layout ...")
+        del B, kv, meta, lvn
+        torch.cuda.empty_cache()
+        B2 = build_layers(n_layers, other, dev)
+        o2 = torch.zeros_like(o)
+        layout_of[0] = other
+        layer1b = make_layer(B2["kv"], B2["meta"], B2["lvn"], o2, ops.FLAG_SINGLE_LAUNCH)
+        gb = capture(layer1b, n_aux)
+        gb.replay()
+        torch.cuda.synchronize()
+        us_b = replay_timed(gb, n_aux)
+        layout_of[0] = layout
+        extra[f"{oname}_us_per_layer"] = round(us_b, 3)
+        extra[f"{oname}_layer_GBps"] = round(LAYER_BYTES / (us_b * 1e-6) / 1e9, 1)
+        extra[f"{oname}_equals_{args.layout}"] = bool(torch.equal(o2, o_eager))
+        del gb, B2
+        torch.cuda.empty_cache()
 
     # the measured path is one kernel per layer: it is the dominant kernel
     dom_us, dom_bytes, dom_name = us_one, LAYER_BYTES, \
         "layer_kernel (scores + top-k + split-K sparse attention, one launch)"
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9
+    ident = so_identity()
     # HBM bytes per launch of layer_kernel from the two rocprofv3 --pmc runs
     # (FETCH_SIZE, WRITE_SIZE of `bench.py --pmc-pass`, each scaled by the
-    # counter's reading for a 64 MiB copy), kept beside their summaries
-    traffic = None
+    # counter's reading for a 64 MiB copy), kept beside their summaries; only
+    # used when they were measured on this very library
+    traffic, traffic_note = None, "no profile"
     tpath = os.path.join(ROOT, "profiles", "layer_kernel_traffic.json")
-    if args.layout == "hnd" and os.path.exists(tpath):
-        traffic = json.load(open(tpath)).get("traffic_bytes")
+    if os.path.exists(tpath):
+        tj = json.load(open(tpath))
+        if args.layout != "hnd":
+            traffic_note = "profiled for HND only"
+        elif tj.get("so_md5") != ident["so_md5"]:
+            traffic_note = f"profiled on libaoakv.so md5 {tj.get('so_md5')}, not the one loaded"
+        else:
+            traffic, traffic_note = tj.get("traffic_bytes"), "rocprofv3 --pmc of this library"
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": dom_name,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "traffic_source": traffic_note, "kernel": dom_name,
             "bytes_per_launch": dom_bytes, "us_per_launch": round(dom_us, 3)}
 
     result = {
@@ -528,21 +700,25 @@ def main():
         "graph_replay_exact": replay_exact,
         "one_launch_equals_two_launches": one_exact,
         "roofline": roof,
+        "build": ident,
     }
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (oracle) ...")
-        cb = cpu_baseline(B["k0"], B["v0"], q[0], args.cpu_reps)
+        cb = cpu_baseline(k0_cpu, v0_cpu, q[0], args.cpu_reps)
         # parity of layer 0 against the oracle on the same inputs
-        err = float(np.abs(o[0].cpu().numpy()[0].astype(np.float32) -
+        err = float(np.abs(o_eager[0].cpu().numpy()[0].astype(np.float32) -
                            cb["o"][0, :, 0].astype(np.float32)).max())
         inv = np.argsort(idx[0].cpu().numpy())      # physical -> logical
-        sl = inv[sel[0, 0].cpu().numpy()]
+        sl = inv[sel_eager[0, 0].cpu().numpy()]
         from oracle import sim
         sets_ok = all(sim.selection_matches(sl[h], cb["pages"][0, h, 0], cb["scores"][0, h, 0],
                                             True)[0] for h in range(H))
         result["cpu_baseline"] = {k: cb[k] for k in ("value", "unit", "cores", "kind", "sample")}
         result["cpu_baseline"]["value"] = round(cb["value"], 1)
         result["parity_layer0"] = {"max_abs_o_vs_oracle": err, "selections_match": sets_ok}
+        if not args.no_extra:
+            log("[bench] CPU baselines of configs 1, 3a, 3b, 4, 5 (oracle) ...")
+            extra["cpu_baselines"] = cpu_baselines_other_configs(k0_cpu, v0_cpu)
     result["extra"] = extra
     print(json.dumps(result))
 

@@ -74,10 +74,11 @@ extern "C" {
 /* aoakv_sparse_decode_layer only: run scoring, top-k and decode in ONE launch
  * (scoring workers, per-head top-k and decode items handing over through
  * the workspace) instead of two launches.  Workgroups wait on lower-indexed
- * workgroups of the launch, each wait bounded; if one gives up, 32-bit word
- * 2 of the workspace becomes non-zero, the output is invalid and handoff
- * words may be left set: call aoakv_workspace_init on the workspace before
- * using it again. */
+ * workgroups of the launch, each wait bounded; if one gives up,
+ * AOAKV_WS_ERR_WAIT is set in the workspace's error word, the output is
+ * invalid and handoff words may be left set.  Every later one-launch call
+ * on that workspace then touches no handoff word and writes NaN outputs
+ * until aoakv_workspace_init re-initialises it. */
 #define AOAKV_FLAG_SINGLE_LAUNCH 4u
 /* The reference KERNEL's selection convention instead of the simulation's
  * (controller.py:113-124, quest/utils/__init__.py:196-246,
@@ -89,6 +90,23 @@ extern "C" {
  * Not combinable with AOAKV_FLAG_FIXED.  The value statistic is still read
  * at the page's own physical index. */
 #define AOAKV_FLAG_QUEST_KERNEL 8u
+
+/* The workspace error word: 32-bit word AOAKV_WS_ERR_WORD of a decode
+ * workspace (offset 8 bytes), OR-ed by the kernels of every entry point that
+ * takes a workspace, zeroed by aoakv_workspace_init.  The library never
+ * reads it back on the host (that would synchronise); a caller checks it
+ * when it wishes, e.g. once per generated token.
+ *   AOAKV_WS_ERR_WAIT       a bounded wait of the one-launch layer gave up
+ *                           (see AOAKV_FLAG_SINGLE_LAUNCH)
+ *   AOAKV_WS_ERR_TRUNCATED  a sequence's device page table (kv_indptr) held
+ *                           more pages than the call was sized for
+ *                           (max_pages, score_stride, sel_stride, or a
+ *                           kernel limit): that sequence's scores,
+ *                           selection and output were computed on its first
+ *                           pages only.  No access leaves the sized buffers. */
+#define AOAKV_WS_ERR_WORD 2u
+#define AOAKV_WS_ERR_WAIT 1u
+#define AOAKV_WS_ERR_TRUNCATED 2u
 
 /* Thread-local description of the last failure ("" when none). */
 const char* aoakv_last_error(void);
@@ -199,7 +217,10 @@ int aoakv_estimate_attn_score(const void* q, float* scores, uint32_t score_strid
  * towards the lower page index.  Output: sel_pages[B, num_kv_heads,
  * sel_stride] int32 PHYSICAL page ids (kv_indices entries) of the selected
  * pages in ascending logical order; entries >= k_b untouched.
- * sel_stride >= max_b k_b.  Supports P_b <= 16384.  With
+ * sel_stride >= max_b k_b.  A score row is the candidate set: at most
+ * score_stride <= 16384 pages (16383 with AOAKV_FLAG_QUEST_KERNEL) per
+ * (sequence, head) take part, as the reference's top-k over an [H, n] row;
+ * a longer device page table is not flagged here (no workspace).  With
  * AOAKV_FLAG_QUEST_KERNEL: k_b - 1 pages chosen among the first P_b - 1
  * (score rows of P_b - 1 entries), the last page not written.
  */

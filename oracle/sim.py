@@ -52,8 +52,14 @@ def h(x) -> np.ndarray:
 
 
 def f(x) -> np.ndarray:
-    """Widen to fp32."""
-    return np.asarray(x).astype(np.float32)
+    """Widen to fp32 (exact).  Large fp16 arrays are widened by torch's CPU
+    conversion, which gives the same values about ten times faster than
+    numpy's."""
+    x = np.asarray(x)
+    if x.dtype == np.float16 and x.size >= (1 << 20):
+        import torch
+        return torch.from_numpy(np.ascontiguousarray(x)).float().numpy()
+    return x.astype(np.float32)
 
 
 # --------------------------------------------------------------------------
@@ -72,13 +78,23 @@ def get_max_min_filters(key_states: np.ndarray, page_size: int) -> np.ndarray:
     """
     b, nh, L, d = key_states.shape
     P = math.ceil(L / page_size)
-    pad = page_size - ((L - 1) % page_size + 1)
-    kmax = np.concatenate(
-        [key_states, np.full((b, nh, pad, d), FP16_MIN, np.float16)], axis=2)
-    kmin = np.concatenate(
-        [key_states, np.full((b, nh, pad, d), FP16_MAX, np.float16)], axis=2)
-    kmax = kmax.reshape(b, nh, P, page_size, d).max(axis=3, keepdims=True)
-    kmin = kmin.reshape(b, nh, P, page_size, d).min(axis=3, keepdims=True)
+    nfull = L // page_size
+    # full pages reduce in place; the padded last page (fp16 finfo.min /
+    # finfo.max padding never wins a max / min against a real key) separately
+    # (reduced in fp32: the fp16 values widen exactly, and the extremes
+    # narrow back exactly)
+    full = f(key_states[:, :, :nfull * page_size]).reshape(b, nh, nfull, page_size, d)
+    kmax = [h(full.max(axis=3, keepdims=True))]
+    kmin = [h(full.min(axis=3, keepdims=True))]
+    if nfull < P:
+        pad = P * page_size - L
+        last = key_states[:, :, nfull * page_size:]
+        kmax.append(np.concatenate([last, np.full((b, nh, pad, d), FP16_MIN, np.float16)],
+                                   axis=2).max(axis=2, keepdims=True)[:, :, :, None])
+        kmin.append(np.concatenate([last, np.full((b, nh, pad, d), FP16_MAX, np.float16)],
+                                   axis=2).min(axis=2, keepdims=True)[:, :, :, None])
+    kmax = np.concatenate(kmax, axis=2)
+    kmin = np.concatenate(kmin, axis=2)
     return np.concatenate([kmax, kmin], axis=3)
 
 
@@ -124,8 +140,8 @@ def _mean_tokens_fp16(x: np.ndarray, axis: int) -> np.ndarray:
     n = x.shape[axis]
     xs = np.moveaxis(f(x), axis, 0)
     acc = np.zeros(xs.shape[1:], np.float32)
-    for t in range(n):
-        acc = (acc + xs[t]).astype(np.float32)
+    for t in range(n):          # token order, one fp32 rounding per add
+        acc += xs[t]
     return h((acc / np.float32(n)).astype(np.float32))
 
 
@@ -366,6 +382,35 @@ def masked_decode_attention(q: np.ndarray, K: np.ndarray, V: np.ndarray,
     e = np.exp((w - m).astype(np.float32)).astype(np.float32)
     p = h(e / e.sum(axis=-1, keepdims=True, dtype=np.float32))
     return h(np.matmul(f(p), f(V)))
+
+
+def sparse_decode_attention(q: np.ndarray, K: np.ndarray, V: np.ndarray, pages: np.ndarray,
+                            chunk_size: int, L: int) -> np.ndarray:
+    """``masked_decode_attention`` with the page mask ``pages`` (b, h, 1, k),
+    evaluated on the selected tokens only.
+
+    The masked form fills the logits of unselected tokens with fp16
+    ``finfo.min``; with a selected logit m >= -65400 their fp32 probability
+    exp(-65504 - m) is exactly 0, so every rounded intermediate of the
+    selected tokens is unchanged and the result is the same up to the
+    summation order of the final fp32 product (tests/test_oracle.py pins it
+    against ``masked_decode_attention``).  q (b, h, 1, d), K/V (b, h, L, d),
+    pages per head (logical page ids); returns (b, h, 1, d) fp16."""
+    b, nh, _, d = q.shape
+    out = np.empty((b, nh, 1, d), np.float16)
+    for bi in range(b):
+        for hi in range(nh):
+            pg = np.unique(np.asarray(pages[bi, hi]).ravel())
+            tok = (pg[:, None] * chunk_size + np.arange(chunk_size)[None, :]).ravel()
+            tok = tok[tok < L]
+            w = h(np.matmul(f(q[bi, hi]), f(K[bi, hi, tok]).T))
+            w = f(h(f(w) / np.float32(math.sqrt(d))))
+            m = w.max(axis=-1, keepdims=True)
+            assert float(m.min()) >= -65400.0, "masked tokens would not vanish"
+            e = np.exp((w - m).astype(np.float32)).astype(np.float32)
+            p = h(e / e.sum(axis=-1, keepdims=True, dtype=np.float32))
+            out[bi, hi] = h(np.matmul(f(p), f(V[bi, hi, tok])))
+    return out
 
 
 class SimLayerState:

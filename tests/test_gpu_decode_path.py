@@ -544,6 +544,105 @@ def test_errors_are_reported_not_crashed():
                                     HND)
 
 
+@pytest.mark.parametrize("single", [False, True])
+def test_page_table_longer_than_max_pages_is_flagged(single):
+    """A device page table of 300 pages passed with max_pages = 200 (buffers
+    sized for 200): no fault, AOAKV_WS_ERR_TRUNCATED (and nothing else) in
+    the workspace error word, and the bits of the same call on the page
+    table cut to 200 pages -- scores, selection and output.  Also the dense
+    decode entry point.  Nothing reads or writes past the sized buffers."""
+    from aoakv import ops
+    _say(f"[truncation] single_launch={single}")
+    H, budget, Pdev, Pmax = 8, 1024, 300, 200
+    L = Pdev * S - 5
+    q, K, V = _sim_state(77, H, L)
+    c = make_ctrl(H, L + 16, HND, budget, shuffle=5)
+    prefill(c, K, V)
+    c.begin_forward(1)
+    qd = torch.from_numpy(q[0, :, 0].copy()).to(DEV)[None]
+    idx = c.kv_indices_with_last
+    midx = c.metadata_indices
+    lpl = c.kv_last_page_len_t
+    t = lambda a: torch.tensor(a, dtype=torch.int32, device=DEV)
+    k = min(max(3, budget // S), Pmax)
+    F = ops.FLAG_VALUE_AWARE | ops.FLAG_FIXED | (ops.FLAG_SINGLE_LAUNCH if single else 0)
+
+    def call(P_table):
+        o = torch.full_like(qd, float("nan"))
+        scores = torch.zeros((1, H, Pmax), dtype=torch.float32, device=DEV)
+        sel = torch.full((1, H, k), -1, dtype=torch.int32, device=DEV)
+        ws = ops.decode_workspace(1, H, H, k, DEV, max_pages=Pmax)
+        ops.sparse_decode_layer(qd, o, c.kv_cache.buf_layer(0), t([0, P_table]), idx, lpl,
+                                c.metadata_cache.buf_layer(0), t([0, -(-P_table // S)]), midx,
+                                c.v_log_norm_layer(0), scores, sel, budget, ws, Pmax, HND, F)
+        torch.cuda.synchronize()
+        return o, sel, scores, ops.workspace_error(ws)
+
+    o_ref, sel_ref, sc_ref, e_ref = call(Pmax)
+    o_tr, sel_tr, sc_tr, e_tr = call(Pdev)
+    assert e_ref == 0
+    assert e_tr == ops.WS_ERR_TRUNCATED
+    assert torch.equal(o_tr, o_ref) and torch.equal(sel_tr, sel_ref)
+    assert torch.equal(sc_tr, sc_ref)
+    assert not torch.isnan(o_tr).any()
+    # dense decode: the 300-page table with max_pages = 200 attends the
+    # first 200 pages, as the 200-page table does
+    outs = []
+    for P_table in (Pmax, Pdev):
+        ws = ops.decode_workspace(1, H, H, Pmax, DEV)
+        o = torch.full_like(qd, float("nan"))
+        ops.decode_sparse_attn(qd, o, c.kv_cache.buf_layer(0), t([0, P_table]), idx, lpl, None,
+                               budget, ws, Pmax, H, HND)
+        torch.cuda.synchronize()
+        outs.append((o, ops.workspace_error(ws)))
+    assert outs[0][1] == 0 and outs[1][1] == ops.WS_ERR_TRUNCATED
+    assert torch.equal(outs[0][0], outs[1][0])
+
+
+def test_one_launch_refuses_a_workspace_whose_wait_flag_is_set():
+    """The wait flag set from the host (as a wait that gave up would leave
+    it): the next one-launch call touches no handoff word and writes NaN
+    outputs; after workspace_init the call runs normally again.  No wait is
+    made to time out: the flag is planted on the host."""
+    from aoakv import ops
+    _say("[wait flag planted]")
+    H, L, budget = 8, 4096 + 9, 1024
+    q, K, V = _sim_state(78, H, L)
+    c = make_ctrl(H, L + 16, HND, budget, shuffle=6)
+    prefill(c, K, V)
+    c.begin_forward(1)
+    qd = torch.from_numpy(q[0, :, 0].copy()).to(DEV)[None]
+    P = len(c.kv_cache.indicies)
+    k = min(max(3, budget // S), P)
+    ws = ops.decode_workspace(1, H, H, k, DEV, max_pages=P)
+
+    def call():
+        o = torch.zeros_like(qd)
+        sel = torch.zeros((1, H, k), dtype=torch.int32, device=DEV)
+        ops.sparse_decode_layer(qd, o, c.kv_cache.buf_layer(0), c.kv_indptr_for_append,
+                                c.kv_indices_with_last, c.kv_last_page_len_t,
+                                c.metadata_cache.buf_layer(0), c.metadata_indptr_for_append,
+                                c.metadata_indices, c.v_log_norm_layer(0), c.scores, sel, budget,
+                                ws, P, HND, ops.FLAG_VALUE_AWARE | ops.FLAG_FIXED |
+                                ops.FLAG_SINGLE_LAUNCH)
+        torch.cuda.synchronize()
+        return o, sel
+
+    o_ok, sel_ok = call()
+    assert ops.workspace_error(ws) == 0 and not torch.isnan(o_ok).any()
+    ws[8:12].view(torch.int32).fill_(ops.WS_ERR_WAIT)     # planted by the host
+    before = ws.clone()
+    o_bad, _ = call()
+    assert torch.isnan(o_bad).all(), "outputs must be NaN while the wait flag is set"
+    assert torch.equal(ws, before), "no handoff word may be touched"
+    with pytest.raises(RuntimeError, match="gave up"):
+        c.workspace = ws
+        c.check_errors()        # reports and re-initializes
+    assert ops.workspace_error(ws) == 0
+    o2, sel2 = call()
+    assert torch.equal(o2, o_ok) and torch.equal(sel2, sel_ok)
+
+
 def test_workspace_shared_across_shrinking_selection_sizes():
     """Regression: one workspace used by calls of different selection sizes.
     Region offsets depend on the call's selection size, so a call with a

@@ -455,3 +455,28 @@ def test_logit_division_by_sqrt_head_dim_is_exact_for_every_fp16():
     assert np.array_equal(q1.view(np.uint32), ref.view(np.uint32))
     # a plain reciprocal product is not enough (the step matters)
     assert not np.array_equal(q0.astype(np.float16).view(np.uint16), ref.astype(np.float16).view(np.uint16))
+
+
+@pytest.mark.parametrize("L,k,seed", [(100, 3, 0), (4096 + 9, 64, 1), (777, 49, 2)])
+def test_sparse_decode_attention_equals_masked_form(L, k, seed):
+    """sim.sparse_decode_attention (selected tokens only) against the
+    simulation's masked form over every token (quest_attention.py:347-356):
+    the same fp16 result up to one ulp of the final product's summation
+    order, on random selections including the partial last page."""
+    H, D = 4, 128
+    g = np.random.default_rng(seed)
+    q = (g.standard_normal((1, H, 1, D)).astype(np.float32)).astype(np.float16)
+    K = (g.standard_normal((1, H, L, D)).astype(np.float32)).astype(np.float16)
+    V = (g.standard_normal((1, H, L, D)).astype(np.float32)).astype(np.float16)
+    P = sim.num_pages(L) if hasattr(sim, "num_pages") else -(-L // 16)
+    pages = np.stack([np.sort(g.choice(P, size=k, replace=False)) for _ in range(H)])
+    pages[:, -1] = P - 1  # the partial last page takes part
+    pages = pages[None, :, None, :]
+    ref = sim.masked_decode_attention(q, K, V, sim.pages_to_token_mask(pages, 16, L))
+    got = sim.sparse_decode_attention(q, K, V, pages, 16, L)
+    diff = np.abs(ref.astype(np.float32) - got.astype(np.float32))
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float32)
+    assert np.all(diff <= ulp), float(diff.max())
+    # a planted mistake: dropping the last selected page must show
+    bad = sim.sparse_decode_attention(q, K, V, pages[..., :-1], 16, L)
+    assert np.abs(bad.astype(np.float32) - ref.astype(np.float32)).max() > 1e-3
