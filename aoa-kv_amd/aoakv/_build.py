@@ -2,6 +2,12 @@
 
     python aoa-kv_amd/aoakv/_build.py     (a plain script: importing the
                                           package would load the old library)
+    python aoa-kv_amd/aoakv/_build.py --timeline
+                                          also the profiling build
+                                          libaoakv_timeline.so (phase
+                                          timestamps, AOAKV_TIMELINE); load it
+                                          with AOAKV_LIB for bench.py
+                                          --timeline-pass
 """
 from __future__ import annotations
 
@@ -17,6 +23,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 SRC_DIR = os.path.join(os.path.dirname(PKG_DIR), "csrc")
 OBJ_DIR = os.path.join(os.path.dirname(PKG_DIR), "_build")
 LIB = os.path.join(PKG_DIR, "libaoakv.so")
+TIMELINE_LIB = os.path.join(PKG_DIR, "libaoakv_timeline.so")
 # build record beside the library (travels with it; the GPU box has no .git)
 BUILDINFO = os.path.join(PKG_DIR, "libaoakv.buildinfo.json")
 SOURCES = ["append.hip", "decode.hip", "prefill.hip", "capi.cpp"]
@@ -38,9 +45,10 @@ FLAGS = [
 ]
 
 
-def _compile(src: str) -> str:
-    obj = os.path.join(OBJ_DIR, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *FLAGS, "-x", "hip", "-c", os.path.join(SRC_DIR, src), "-o", obj]
+def _compile(src: str, obj_dir: str = OBJ_DIR, defines=()) -> str:
+    obj = os.path.join(obj_dir, os.path.splitext(src)[0] + ".o")
+    cmd = [HIPCC, *FLAGS, *[f"-D{d}" for d in defines], "-x", "hip", "-c",
+           os.path.join(SRC_DIR, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
@@ -91,27 +99,37 @@ def write_buildinfo() -> dict:
     return info
 
 
-def build(verbose: bool = True) -> str:
-    """Compile every source for gfx950 and link libaoakv.so.  Always rebuilds."""
+def _link(lib: str, obj_dir: str, defines=()) -> str:
     if not os.path.exists(HIPCC):
         raise RuntimeError(f"hipcc not found at {HIPCC}")
-    os.makedirs(OBJ_DIR, exist_ok=True)
+    os.makedirs(obj_dir, exist_ok=True)
     srcs = [s for s in SOURCES if os.path.exists(os.path.join(SRC_DIR, s))]
     with cf.ThreadPoolExecutor(max_workers=min(4, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
-    tmp = LIB + ".tmp"
+        objs = list(ex.map(lambda s: _compile(s, obj_dir, defines), srcs))
+    tmp = lib + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB)
-    shutil.rmtree(OBJ_DIR, ignore_errors=True)
+    os.replace(tmp, lib)
+    shutil.rmtree(obj_dir, ignore_errors=True)
+    return lib
+
+
+def build(verbose: bool = True, timeline: bool = False) -> str:
+    """Compile every source for gfx950 and link libaoakv.so.  Always rebuilds.
+    With timeline, also the profiling build libaoakv_timeline.so."""
+    _link(LIB, OBJ_DIR)
     write_buildinfo()
     if verbose:
         print(f"built {LIB} ({os.path.getsize(LIB)} bytes)")
+    if timeline:
+        _link(TIMELINE_LIB, OBJ_DIR + "_timeline", ("AOAKV_TIMELINE",))
+        if verbose:
+            print(f"built {TIMELINE_LIB} ({os.path.getsize(TIMELINE_LIB)} bytes)")
     return LIB
 
 
 if __name__ == "__main__":
-    build()
+    build(timeline="--timeline" in sys.argv[1:])
     sys.exit(0)

@@ -31,6 +31,63 @@ constexpr int kPartialStride = kHeadDim + 4;             // o[128], m, l, pad
 constexpr int kMergeMaxChunks = 1024;                    // decode chunks per head
 constexpr uint32_t kTopkMaxPages = 16384;
 
+// ---------------------------------------------------------------- timeline
+// With AOAKV_TIMELINE defined (a separate profiling build, never the shipped
+// library), thread 0 of each workgroup notes the s_memrealtime counter (100
+// MHz, one clock for the whole GPU) at the phase points below in LDS, and
+// writes them out once, when the workgroup ends (TL_FLUSH), to its row of
+// g_tl (linear workgroup index): no global access between the points, so the
+// notes barely move the phases they time.  Every instrumented launch
+// overwrites the rows of its workgroups; aoakv_timeline_read (end of this
+// file) reads them back.  Without AOAKV_TIMELINE, TL() is empty.
+enum : int {
+  kTlStart = 0,        // workgroup entry
+  kTlStaggerDone = 1,  // staggered start over (scoring workers, decode items)
+  kTlScored0 = 2,      // scoring worker: first item's scores stored
+  kTlScored1 = 3,      // ... second item's
+  kTlScoresSeen = 4,   // top-k: the head's scores seen (sentinel / counter)
+  kTlRowLoaded = 5,    // top-k: every score word of the row loaded
+  kTlSelected = 6,     // top-k: radix select done
+  kTlSelInHand = 7,    // decode item: its selection entries known
+  kTlAttended = 8,     // decode item: K/V gathered and attended
+  kTlPartial = 9,      // decode item: partial (o, m, l) stored
+  kTlMergeLoaded = 10, // merging item: every partial loaded
+  kTlOutput = 11,      // merging item: output stored (top-k workgroup: selection stored)
+  kTlStaged = 12,      // top-k: keys staged, key range reduced
+  kTlPass1 = 13,       // top-k: first radix pass done
+  kTlEvents = 14
+};
+#ifdef AOAKV_TIMELINE
+constexpr uint32_t kTlMaxWg = 4096;
+__device__ unsigned long long g_tl[kTlMaxWg][kTlEvents];
+__shared__ unsigned long long s_tl[kTlEvents];
+#define TL(ev)                                                             \
+  do {                                                                     \
+    if (threadIdx.x == 0u) s_tl[ev] = __builtin_amdgcn_s_memrealtime();   \
+  } while (0)
+#define TL_BEGIN()                                                         \
+  do {                                                                     \
+    if (threadIdx.x == 0u)                                                 \
+      for (int e_ = 0; e_ < kTlEvents; ++e_) s_tl[e_] = 0ull;              \
+  } while (0)
+#define TL_FLUSH()                                                                         \
+  do {                                                                                     \
+    const uint32_t tl_wg = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z); \
+    if (threadIdx.x == 0u && tl_wg < kTlMaxWg)                                             \
+      for (int e_ = 0; e_ < kTlEvents; ++e_) g_tl[tl_wg][e_] = s_tl[e_];                   \
+  } while (0)
+#else
+#define TL(ev) \
+  do {         \
+  } while (0)
+#define TL_BEGIN() \
+  do {             \
+  } while (0)
+#define TL_FLUSH() \
+  do {             \
+  } while (0)
+#endif
+
 // ======================================================================
 // block-wide helpers (256 threads = 4 waves)
 // ======================================================================
@@ -161,6 +218,7 @@ __device__ __forceinline__ RadixResult radix_select(const uint32_t (&rel)[KPT], 
     kr -= above;
     hi = sft;
     buf = nxt;
+    TL(kTlPass1);
     if (count == kr) {  // every key of the bucket is selected
       take_bucket = true;
       break;
@@ -241,6 +299,10 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
         sv[m] = ld_agent(scores + i);
         iv[m] = kv_ids[i];
       }
+#ifdef AOAKV_TIMELINE
+      // (noted once the loads have returned)
+      if (__builtin_bit_cast(uint32_t, sv[KPT - 1]) != 0x7FBADBADu) TL(kTlRowLoaded);
+#endif
     } else {
       // page ids first, then this thread's score words, polled until the
       // scoring items have written them, then cleared for the next launch
@@ -268,6 +330,7 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
           if (it >= kSpinLimit && lane == 0u) flag_error(error, kErrWait);
         }
         __syncthreads();
+        TL(kTlScoresSeen);
       }
       auto load_words = [&]() {
 #pragma unroll
@@ -295,6 +358,7 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
       // written after it are left set, and the next launch must not run on
       // them
       if (it >= kSpinLimit) flag_error(error, kErrWait);
+      TL(kTlRowLoaded);
 #pragma unroll
       for (int m = 0; m < KPT; ++m) {
         const uint32_t i = tid + (uint32_t)m * kThreads;
@@ -333,6 +397,7 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
     sh.red[4 + wave] = kmax;
   }
   __syncthreads();
+  TL(kTlStaged);
   kmin = sh.red[0];
   kmax = sh.red[4];
 #pragma unroll
@@ -362,6 +427,7 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
   }
   // >= 1: k == 0 returned above, and with fixed forcing k >= 3 > nforced
   const RadixResult rr = radix_select<KPT, Mask>(rel, free_mask, kmax - kmin, k - nforced, sh);
+  TL(kTlSelected);
 
   // selection classes at the final resolution:
   //   above:  forced, or (rel & hmask) > thr  -- selected
@@ -420,6 +486,7 @@ __device__ __forceinline__ void topk_block(const float* __restrict__ scores, uin
     __syncthreads();
     if (!SELF)
       for (uint32_t i = tid; i < k; i += kThreads) put(i, (int32_t)s_out[i]);
+    TL(kTlOutput);
   } else {
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
@@ -493,15 +560,9 @@ __device__ inline uint32_t est_pages(const EstimateArgs& a, uint32_t b, uint32_t
 // stores them (agent-coherent).  Returns false, uniformly, when the chunk
 // holds no page.  A sequence whose page table exceeds what the call covers
 // sets kErrTruncated (once, from its first chunk).
-// One-launch layer: err0 is the error word as read at the workgroup's start,
-// s_err an LDS word it passes through so that the workgroup branches alike;
-// with kErrWait set nothing is stored (handoff words left set by a wait that
-// gave up must not be mixed with this launch's) and the item returns true.
-// Two launches: s_err = nullptr.
 template <int GROUP>
 __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, uint32_t h,
-                                           uint32_t chunk, EstShared& sm,
-                                           uint32_t* s_err = nullptr, uint32_t err0 = 0u) {
+                                           uint32_t chunk, EstShared& sm) {
   float* s_sc = sm.sc;
   const uint32_t lane = __lane_id();
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -610,10 +671,7 @@ __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, ui
     if (value_aware) score = score + 2.0f * __shfl(lvn_lane, s * 4 + (int)row);
     if (l16 == 0u) s_sc[wave * kEstPagesPerWave + s * 4 + row] = score;
   }
-  // the snapshot is written here, after every load of the item was issued
-  if (s_err != nullptr && threadIdx.x == 0u) *s_err = err0;
   __syncthreads();
-  if (s_err != nullptr && (*s_err & kErrWait) != 0u) return true;
   float* out = a.scores + ((size_t)b * a.Hkv + h) * a.score_stride;
   {
     const uint32_t p = chunk * kEstPagesPerBlock + threadIdx.x;
@@ -701,7 +759,21 @@ __global__ __launch_bounds__(kThreads) void estimate_kernel(EstimateArgs a) {
   }
 }
 
+#ifdef AOAKV_TIMELINE
+__device__ __forceinline__ void topk_body(const TopkArgs& a);
+
 __global__ __launch_bounds__(kThreads) void topk_kernel(TopkArgs a) {
+  TL_BEGIN();
+  TL(kTlStart);
+  topk_body(a);
+  TL_FLUSH();
+}
+
+__device__ __forceinline__ void topk_body(const TopkArgs& a)
+#else
+__global__ __launch_bounds__(kThreads) void topk_kernel(TopkArgs a)
+#endif
+{
   __shared__ TopkShared sh;
   const uint32_t h = blockIdx.x, b = blockIdx.y;
   const uint32_t pbeg = (uint32_t)a.kv_indptr[b];
@@ -900,6 +972,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
       return self_topk ? tk->key[i] : (uint32_t)ids[i];
     };
     sel_ch = entry(ich);
+    TL(kTlSelInHand);
 #pragma unroll
     for (int s = 0; s < kDecPagesPerWave; ++s) selv[s] = entry(idx0 + s);
     // this chunk's entries of the selection output (the last chunk also
@@ -918,6 +991,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
     __syncthreads();
     if (threadIdx.x < (uint32_t)kDecPagesPerBlock && e < nsel) st_agent_u32(hrow + e, 0u);
     sel_ch = sm.sel[0];
+    TL(kTlSelInHand);
 #pragma unroll
     for (int s = 0; s < kDecPagesPerWave; ++s) selv[s] = sm.sel[wave * kDecPagesPerWave + s];
   }
@@ -999,6 +1073,19 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
 #pragma unroll
   for (int j = 0; j < kVec; ++j) o[j] = 0.f;
   if (m != -INFINITY) {
+    // slots past a page's token count (the sequence's last page) hold
+    // whatever the cache held: their probability is exactly 0, but 0 * NaN
+    // is NaN, so their V is zeroed.  A wave-uniform branch (every lane holds
+    // the same two pages), taken for the last page and unused entries only,
+    // and placed where the V loads are waited for anyway: a write to vv
+    // right after its loads would make the compiler wait for them there.
+    if (ntok[0] < S || ntok[1] < S) {
+#pragma unroll
+      for (int s = 0; s < kDecPagesPerWave; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if ((uint32_t)(i * 4) + row >= ntok[s]) vv[s][i] = H8{};
+    }
     float pv[kTok];
     row_bcast8(__expf(xm - m), pv);
 #pragma unroll
@@ -1014,6 +1101,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
 #pragma unroll
   for (int j = 0; j < kVec; ++j) o[j] = cross_row_sum(o[j]);
 
+  TL(kTlAttended);
   // ---- combine the 4 waves of the block in LDS, store the chunk's (o, m, l)
   if (row == 0u) {
 #pragma unroll
@@ -1044,6 +1132,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
     else st_agent_u32(a.hpart + part_off + d, to_word(val));
   }
 
+  TL(kTlPartial);
   // ---- one block of this (sequence, head) merges the chunks
   if (HANDOFF) {
     if (chunk != nch - 1u) return;  // the head's last chunk
@@ -1118,6 +1207,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
         __builtin_amdgcn_s_sleep(1);
         load_group();
       }
+      TL(kTlMergeLoaded);
 #pragma unroll
       for (int c = 0; c < 16; ++c) {
         mw[c] -= 1u;
@@ -1161,6 +1251,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   if (half == 1u) s_o[0][d] = acc;
   __syncthreads();
   if (half == 0u) a.o[bh * kHeadDim + d] = r16((acc + s_o[0][d]) / Lsum);
+  TL(kTlOutput);
   // Every thread has read its words (barrier above): clear them -- o words by
   // their reader, m / l words by thread c.  Handoff words must be zero for
   // the next launch; the two-launch partials are cleared as well, so the
@@ -1196,7 +1287,10 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
 template <bool QUEST>
 __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
   __shared__ DecShared sm;
+  TL_BEGIN();
+  TL(kTlStart);
   decode_item<false, QUEST>(a, blockIdx.z, blockIdx.y, blockIdx.x, sm);
+  TL_FLUSH();
 }
 
 // ======================================================================
@@ -1223,34 +1317,61 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
 // (same-address device atomics serialize at ~12 ns each).
 // SELF (GROUP 1, la.self_select): the decode items select for themselves; a
 // separate instantiation, so the other path keeps its own register budget.
+#ifdef AOAKV_TIMELINE
+// the profiling build wraps the kernel body to note its start and write the
+// notes out when the workgroup ends, whichever way the body returns
+template <int GROUP, bool QUEST, bool SELF>
+__device__ __forceinline__ void layer_body(const LayerArgs& la);
+
 template <int GROUP, bool QUEST, bool SELF>
 __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
+  TL_BEGIN();
+  layer_body<GROUP, QUEST, SELF>(la);
+  TL_FLUSH();
+}
+
+template <int GROUP, bool QUEST, bool SELF>
+__device__ __forceinline__ void layer_body(const LayerArgs& la)
+#else
+template <int GROUP, bool QUEST, bool SELF>
+__global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la)
+#endif
+{
   static_assert(!SELF || GROUP == 1, "self-selection needs one query head per kv head");
   __shared__ union {
     EstTopkShared e;
     DecShared d;
   } sm;
   __shared__ uint32_t s_ok;
-  // The error word as it stands when the workgroup starts: kErrWait there
-  // means an earlier launch's wait gave up and may have left handoff words
-  // set, so no workgroup touches one (every role checks the snapshot, passed
-  // through s_err, before its first handoff access) and the output is NaN
-  // until the caller re-initialises the workspace.  Read here, checked once
-  // the role's first loads are in flight.
+  // The error word as the launch found it: kErrWait there means an earlier
+  // launch's wait gave up and may have left handoff words set, so no
+  // workgroup that reads handoff words (top-k workgroups, decode items)
+  // touches one; they check the word, passed through s_err, before their
+  // first handoff access, and the output is NaN until the caller
+  // re-initialises the workspace.  Scoring workers only write words, which a
+  // refusing reader never consumes, so they do not read it.  A plain load:
+  // the previous launch's flag is visible after the kernel boundary, and
+  // the read is served by each XCD's L2 rather than by one memory word for
+  // every workgroup (a coherent load of it in all 992 workgroups of config
+  // 2 cost 0.67 us per layer).
   __shared__ uint32_t s_err;
-  const uint32_t err0 = ld_agent_u32(la.d.error);
   const uint32_t t = blockIdx.x;
+  TL(kTlStart);
   if (t < la.n_workers) {
     {  // first item's head bh0 starts bh0 * stagger cycles in (see layer_stagger_cycles)
       const unsigned long long t0 = clock64();
       const unsigned long long wait = (unsigned long long)(t / la.est_chunks) * la.stagger;
       while (clock64() - t0 < wait) __builtin_amdgcn_s_sleep(1);
     }
+    TL(kTlStaggerDone);
+    int tl_item = 0;
     for (uint32_t i = t; i < la.n_est; i += la.n_workers) {
       const uint32_t bh = i / la.est_chunks, chunk = i % la.est_chunks;
       const uint32_t b = bh / la.e.Hkv, h = bh % la.e.Hkv;
-      if (score_item<GROUP>(la.e, b, h, chunk, sm.e.e, &s_err, err0)) {
-        if ((s_err & kErrWait) != 0u) return;  // uniform: read after score_item's barrier
+      if (score_item<GROUP>(la.e, b, h, chunk, sm.e.e)) {
+        TL(tl_item == 0 ? kTlScored0 : kTlScored1);
+        ++tl_item;
+        (void)tl_item;
         if (la.e.hscore != nullptr) {
           // the scores went out as handoff words: only end this item's use
           // of LDS before the next item's
@@ -1267,6 +1388,7 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
       }
     }
   } else if (t < la.n_workers + la.n_heads) {
+    const uint32_t err0 = *la.d.error;
     const uint32_t bh = t - la.n_workers;
     const uint32_t b = bh / la.e.Hkv, h = bh % la.e.Hkv;
     uint32_t pbeg;
@@ -1297,6 +1419,7 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
     __syncthreads();
     if (s_ok != 0u) select_item<GROUP>(la.e, b, h, plan, sm.e.tk);
   } else if (t < la.n_workers + la.n_heads + la.n_dec) {
+    const uint32_t err0 = *la.d.error;
     const uint32_t u = t - la.n_workers - la.n_heads;
     const uint32_t bh = u / la.d.max_chunks, chunk = u % la.d.max_chunks;
     const uint32_t b = bh / la.d.Hq, hq = bh % la.d.Hq;
@@ -1311,6 +1434,7 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
       const unsigned long long wait =
           (unsigned long long)(bh < first_round ? bh : first_round) * la.stagger;
       while (clock64() - t0 < wait) __builtin_amdgcn_s_sleep(8);
+      TL(kTlStaggerDone);
       decode_item<true, QUEST, true>(la.d, b, hq, chunk, sm.d, &la.e, &sm.e.tk, &s_err, err0);
     } else {
       decode_item<true, QUEST>(la.d, b, hq, chunk, sm.d, nullptr, nullptr, &s_err, err0);
@@ -1442,3 +1566,19 @@ uint32_t layer_self_blocks_per_cu() {
 }
 
 }  // namespace aoakv
+
+#ifdef AOAKV_TIMELINE
+// Profiling build only (not declared in aoakv.h): read back the phase
+// timestamps of the last instrumented launch ([4096 workgroups][kTlEvents]
+// uint64, synchronizing), or clear them.
+extern "C" int aoakv_timeline_read(void* host, size_t bytes) {
+  if (bytes > sizeof(aoakv::g_tl)) bytes = sizeof(aoakv::g_tl);
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(aoakv::g_tl), bytes, 0, hipMemcpyDeviceToHost);
+}
+extern "C" int aoakv_timeline_clear() {
+  static unsigned long long zero[aoakv::kTlMaxWg][aoakv::kTlEvents];
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(aoakv::g_tl), zero, sizeof(zero), 0,
+                                hipMemcpyHostToDevice);
+}
+extern "C" int aoakv_timeline_events() { return aoakv::kTlEvents; }
+#endif

@@ -311,6 +311,18 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
         load_tile(u == 0u ? s_buf1 : s_buf0, phys_next);
         phys_next = page_of(ti + 2u);
       }
+      if ((ti + 1u) * kPfTileKeys > L) {  // uniform: the tile holding the sequence's end
+        // rows of keys at or past L hold whatever the cache held there (the
+        // last page's unwritten slots, or the last page read again): their
+        // probability is exactly 0, but 0 * NaN is NaN in the MFMA, so their
+        // V rows are zeroed before any wave reads them
+        char* vbuf = (u == 0u ? s_buf0 : s_buf1) + kPfTileBytes;
+        const uint32_t first_dead = L - ti * kPfTileKeys;  // < kPfTileKeys
+        for (uint32_t i = first_dead * (kPfRowBytes / 16u) + threadIdx.x;
+             i < (uint32_t)kPfTileKeys * (kPfRowBytes / 16u); i += kPfThreads)
+          reinterpret_cast<uint4*>(vbuf)[i] = uint4{0u, 0u, 0u, 0u};
+        __syncthreads();
+      }
       if (ti * kPfTileKeys < wave_kend)  // wave-uniform: skip tiles above this wave's queries
         tile((const lds_char*)(u == 0u ? s_buf0 : s_buf1), ti * kPfTileKeys);
     }

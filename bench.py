@@ -439,6 +439,120 @@ def so_identity() -> dict:
     return info
 
 
+TL_NAMES = ["start", "stagger_done", "scored0", "scored1", "scores_seen", "row_loaded",
+            "selected", "sel_in_hand", "attended", "partial", "merge_loaded", "output"]
+
+
+def timeline_pass(dev, layout, fn_layer, n_layers, samples=16, tick_ns=10.0, isolated=None):
+    """Per-phase timeline of the one-launch layer (config 2), from the
+    profiling build (AOAKV_LIB=aoa-kv_amd/aoakv/libaoakv_timeline.so).  Each
+    sample launch runs right behind a replay of the 32-layer graph, as in the
+    timed loop; its workgroups' phase timestamps (s_memrealtime, 100 MHz,
+    noted in LDS and written out as each workgroup ends) are read back and
+    reduced per head.  `isolated` kernels are timed the same way, alone
+    behind the replay.  Returns a dict (JSON)."""
+    import ctypes
+    import numpy as np
+    import torch
+    from aoakv import _lib, ops
+    lib = _lib.load()
+    for name in ("aoakv_timeline_read", "aoakv_timeline_clear"):
+        if not hasattr(lib, name):
+            raise SystemExit("--timeline-pass needs the profiling build: build it with "
+                             "`python aoa-kv_amd/aoakv/_build.py --timeline` and run with "
+                             "AOAKV_LIB=aoa-kv_amd/aoakv/libaoakv_timeline.so")
+    lib.aoakv_timeline_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    n_ev = lib.aoakv_timeline_events()
+    buf = np.zeros((4096, n_ev), np.uint64)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for l in range(n_layers):
+            fn_layer(l)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        for l in range(n_layers):
+            fn_layer(l)
+    g.replay()
+    torch.cuda.synchronize()
+    H_, E_ = H, 16          # heads, 128-page scoring chunks per head (config 2)
+    n_workers = 480 if H_ * E_ > 256 else H_ * E_
+    dec0 = n_workers        # self-selecting layer: no top-k workgroups
+    def score_row(h, c):    # (workgroup, event) of head h's scoring chunk c: item
+        i = h * E_ + c      # i is worker i % n_workers's item number i // n_workers
+        return i % n_workers, 2 + i // n_workers
+
+    def dec_row(h, c):      # workgroup of head h's decode chunk c
+        return dec0 + h * 16 + c
+    per = []                # per sample: dict of per-head phase times (us)
+    spans = []
+    for smp in range(samples):
+        g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn_layer(smp % n_layers)
+        e1.record()
+        torch.cuda.synchronize()
+        lib.aoakv_timeline_read(buf.ctypes.data, buf.nbytes)
+        t = buf.astype(np.int64)
+        n_wg = dec0 + H_ * 16
+        starts = t[:n_wg, 0]
+        t0 = starts[starts > 0].min()
+        us = lambda x: (x - t0) * tick_ns / 1000.0
+        heads = []
+        for h in range(H_):
+            stored = [t[score_row(h, c)] for c in range(E_)]
+            dec = [dec_row(h, c) for c in range(16)]
+            row = {"head": h, "scored": us(max(stored))}
+            for ev, name in ((1, "dec_start"), (4, "scores_seen"), (5, "row_loaded"),
+                             (6, "selected"), (7, "sel_in_hand"), (8, "attended"),
+                             (9, "partial")):
+                vals = [us(t[d, ev]) for d in dec if t[d, ev] > 0]
+                row[name] = float(np.median(vals)) if vals else None
+                row[name + "_max"] = float(max(vals)) if vals else None
+            row["merge_loaded"] = us(t[dec[-1], 10])
+            row["output"] = us(t[dec[-1], 11])
+            heads.append(row)
+        per.append(heads)
+        spans.append((max(h["output"] for h in heads), e0.elapsed_time(e1) * 1e3))
+    # median over samples, per head and phase
+    keys = [k for k in per[0][0] if k != "head"]
+    table = []
+    for h in range(H_):
+        table.append({"head": h, **{k: round(float(np.median([p[h][k] for p in per])), 2)
+                                    for k in keys}})
+    last = max(range(H_), key=lambda h: table[h]["output"])
+    res = {"samples": samples, "tick_ns": tick_ns,
+           "end_us_median": round(float(np.median([a for a, _ in spans])), 2),
+           "event_us_median": round(float(np.median([b for _, b in spans])), 2),
+           "last_head": last, "heads": table}
+    if isolated is not None:
+        res["isolated"] = {}
+        for name, fn, evs, n_grid in isolated:
+            rows = []
+            for smp in range(samples):
+                lib.aoakv_timeline_clear()
+                g.replay()
+                fn(smp % n_layers)
+                torch.cuda.synchronize()
+                lib.aoakv_timeline_read(buf.ctypes.data, buf.nbytes)
+                t = buf.astype(np.int64)[:n_grid]
+                live = t[:, 0] > 0
+                t0 = t[live, 0].min()
+                rows.append({nm: float(np.median((t[live & (t[:, ev] > 0), ev] - t0)) *
+                                       tick_ns / 1000.0) if np.any(live & (t[:, ev] > 0)) else None
+                             for nm, ev in evs} |
+                            {nm + "_max": float((t[live & (t[:, ev] > 0), ev].max() - t0) *
+                                                tick_ns / 1000.0)
+                             if np.any(live & (t[:, ev] > 0)) else None for nm, ev in evs})
+            res["isolated"][name] = {k: round(float(np.median([r[k] for r in rows
+                                                                if r[k] is not None])), 2)
+                                     for k in rows[0] if any(r[k] is not None for r in rows)}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -453,6 +567,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip appends / eager timings")
     ap.add_argument("--prefill-pass", action="store_true",
                     help="config 4 only: causal paged prefill at 8k and 16k tokens, one JSON line")
+    ap.add_argument("--timeline-pass", action="store_true",
+                    help="per-phase timeline of the one-launch layer from the profiling build "
+                         "(AOAKV_LIB=aoa-kv_amd/aoakv/libaoakv_timeline.so); one JSON line")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="for rocprofv3 --pmc: a 64 MiB device copy x3 (calibration), then one "
                          "eager pass of the 32 one-launch layers; prints nothing else")
@@ -537,6 +654,16 @@ def main():
             layer1(l)
         torch.cuda.synchronize()
         log("[bench] pmc pass done")
+        return
+
+    if args.timeline_pass:
+        def topk_only(l):
+            ops.topk_filtering(scores[l], indptr, idx[l], lpl, BUDGET, sel[l], S, flags)
+        iso = [("topk_kernel", topk_only, [("row_loaded", 5), ("staged", 12), ("pass1", 13),
+                                           ("selected", 6), ("output", 11)], H),
+               ("decode_kernel", dec, [("attended", 8), ("partial", 9), ("output", 11)],
+                H * K_SEL // 8)]
+        print(json.dumps(timeline_pass(dev, layout, layer1, n_layers, isolated=iso)))
         return
 
     def capture(fn, n):

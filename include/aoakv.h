@@ -77,8 +77,9 @@ extern "C" {
  * workgroups of the launch, each wait bounded; if one gives up,
  * AOAKV_WS_ERR_WAIT is set in the workspace's error word, the output is
  * invalid and handoff words may be left set.  Every later one-launch call
- * on that workspace then touches no handoff word and writes NaN outputs
- * until aoakv_workspace_init re-initialises it. */
+ * on that workspace then reads no handoff word (its scoring items may still
+ * write their score words) and writes NaN outputs until
+ * aoakv_workspace_init re-initialises it. */
 #define AOAKV_FLAG_SINGLE_LAUNCH 4u
 /* The reference KERNEL's selection convention instead of the simulation's
  * (controller.py:113-124, quest/utils/__init__.py:196-246,

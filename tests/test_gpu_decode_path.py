@@ -601,9 +601,11 @@ def test_page_table_longer_than_max_pages_is_flagged(single):
 
 def test_one_launch_refuses_a_workspace_whose_wait_flag_is_set():
     """The wait flag set from the host (as a wait that gave up would leave
-    it): the next one-launch call touches no handoff word and writes NaN
-    outputs; after workspace_init the call runs normally again.  No wait is
-    made to time out: the flag is planted on the host."""
+    it): the next one-launch call consumes no handoff word -- its selection,
+    partial and counter regions stay untouched (scoring items may still
+    write their score words, which nothing reads) -- and writes NaN outputs;
+    after workspace_init the call runs normally again.  No wait is made to
+    time out: the flag is planted on the host."""
     from aoakv import ops
     _say("[wait flag planted]")
     H, L, budget = 8, 4096 + 9, 1024
@@ -634,13 +636,50 @@ def test_one_launch_refuses_a_workspace_whose_wait_flag_is_set():
     before = ws.clone()
     o_bad, _ = call()
     assert torch.isnan(o_bad).all(), "outputs must be NaN while the wait flag is set"
-    assert torch.equal(ws, before), "no handoff word may be touched"
+    from aoakv import _lib
+    dec_bytes = _lib.load().aoakv_decode_workspace_size(1, H, H, 128, k)
+    assert torch.equal(ws[:dec_bytes], before[:dec_bytes]), "decode regions must be untouched"
     with pytest.raises(RuntimeError, match="gave up"):
         c.workspace = ws
         c.check_errors()        # reports and re-initializes
     assert ops.workspace_error(ws) == 0
     o2, sel2 = call()
     assert torch.equal(o2, o_ok) and torch.equal(sel2, sel_ok)
+
+
+@pytest.mark.parametrize("layout", [NHD, HND])
+def test_decode_ignores_unwritten_slots_of_the_last_page(layout):
+    """Regression: the last page's slots past the sequence are never written
+    and may hold NaN.  Their probability is 0, but 0 * NaN is NaN: the decode
+    must not let them in.  The cache is filled with NaN before the append,
+    so every unwritten slot is NaN; sparse (two launches, one launch) and
+    dense decode must match the oracle."""
+    from aoakv import ops
+    from aoakv.utils import decode_layer, decode_sparse_attn
+    _say(f"[decode NaN slots] layout={layout}")
+    H, L, budget = 8, 4096 + 9, 1024
+    q, K, V = _sim_state(79, H, L)
+    c = make_ctrl(H, L + 2 * S, layout, budget, shuffle=9)
+    c.kv_cache.buf_layer(0).fill_(float("nan"))
+    prefill(c, K, V)
+    c.begin_forward(1)
+    st = sim.SimLayerState(K, V)
+    sc, pg = sim.select_pages(st, q, budget)
+    qd = torch.from_numpy(q[0, :, 0].copy()).to(DEV)[None]
+    for single in (False, True):
+        o = decode_layer(qd, c, 0, single_launch=single).cpu().numpy()[0]
+        assert np.isfinite(o.astype(np.float32)).all(), single
+        inv = {int(p): i for i, p in enumerate(c.kv_cache.indicies)}
+        sel = np.vectorize(inv.get)(c.topk_dindices_buffer.cpu().numpy()[0])
+        _selection_ok(sel, pg, sc, True)
+        mask = sim.pages_to_token_mask(sel[None, :, None], S, L)
+        ref = sim.masked_decode_attention(q, K, V, mask)[0, :, 0].astype(np.float32)
+        assert np.abs(o.astype(np.float32) - ref).max() <= 2e-3, single
+    od = decode_sparse_attn(qd, c, 0, None).cpu().numpy()[0]
+    assert np.isfinite(od.astype(np.float32)).all()
+    ref = sim.masked_decode_attention(q, K, V, None)[0, :, 0].astype(np.float32)
+    assert np.abs(od.astype(np.float32) - ref).max() <= 2e-3
+    assert ops.workspace_error(c.workspace) == 0
 
 
 def test_workspace_shared_across_shrinking_selection_sizes():

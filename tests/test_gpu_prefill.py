@@ -130,3 +130,32 @@ def test_prefill_gqa(layout, group):
                                         c.kv_cache.last_page_len, layout).cpu().numpy()
     ref = sim.causal_prefill_rows(q, np.repeat(k, group, axis=1), np.repeat(v, group, axis=1))
     assert np.abs(o.astype(np.float32) - ref).max() <= 2e-3
+
+
+@pytest.mark.parametrize("L", [100, 777, 4096 + 9])
+def test_prefill_ignores_unwritten_slots_past_the_sequence(L):
+    """Regression: the cache's slots past the last token are never written
+    and may hold NaN.  Their probability is 0, but 0 * NaN is NaN in the
+    MFMA: the tile holding the sequence's end must not let them in.  The
+    cache is filled with NaN before the append, so every unwritten slot is
+    NaN here."""
+    from aoakv import ops
+    from aoakv.utils import InferenceController, append_kv
+    _say(f"[prefill NaN slots] L={L}")
+    H = 8
+    q = randn16(90 + L, (L, H, D), 0.5)
+    k = randn16(91 + L, (L, H, D), 0.5)
+    v = randn16(92 + L, (L, H, D), 0.5)
+    c = InferenceController(1, H, D, S, 64, L + 2 * S, torch.float16, DEV, layout=HND,
+                            shuffle_seed=3)
+    c.kv_cache.buf_layer(0).fill_(float("nan"))
+    c.prepare_metadata(L)
+    c.begin_forward(L)
+    append_kv(torch.from_numpy(k).to(DEV), torch.from_numpy(v).to(DEV), c, 0)
+    o = ops.prefill_with_paged_kv_cache(torch.from_numpy(q).to(DEV), c.kv_cache.buf_layer(0),
+                                        c.kv_indices_with_last, len(c.kv_cache.indicies),
+                                        c.kv_cache.last_page_len, HND).cpu().numpy()
+    assert np.isfinite(o.astype(np.float32)).all()
+    rows = np.unique(np.linspace(0, L - 1, 24).astype(np.int64))
+    ref = sim.causal_prefill_rows(q, k, v, rows)
+    assert np.abs(o[rows].astype(np.float32) - ref).max() <= 2e-3
