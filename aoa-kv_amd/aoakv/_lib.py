@@ -48,6 +48,9 @@ SIGNATURES = {
     "aoakv_sparse_decode_layer": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _u32, _p,
                                   _u32, _u32, _p, _p, _sz, _u32, _u32, _u32, _u32, _u32,
                                   _u32, _u32, _u32, _p],
+    "aoakv_sparse_decode_layer_noalloc": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _u32,
+                                          _p, _u32, _u32, _p, _u32, _u32, _u32, _u32, _u32,
+                                          _u32, _u32, _u32, _p],
     "aoakv_estimate_topk": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _u32, _p, _u32, _u32, _p, _p,
                             _sz, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _p],
     "aoakv_prefill_with_paged_kv_cache": [_p, _p, _p, _p, _u32, _u32, _u32, _u32, _u32,

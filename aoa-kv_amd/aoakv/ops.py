@@ -281,6 +281,33 @@ def sparse_decode_layer(q, o, kv_data, kv_indptr, kv_indices, kv_last_page_len, 
               workspace.numel(), B, max_pages, Hq, Hkv, D, S, layout, flags, _stream())
 
 
+def sparse_decode_layer_noalloc(q, o, kv_data, kv_indptr, kv_indices, kv_last_page_len,
+                                metadata_data, metadata_indptr, metadata_indices, v_log_norm,
+                                scores, sel_pages, token_budget: int, max_pages: int, layout: int,
+                                flags: int = FLAG_VALUE_AWARE | FLAG_FIXED, token_budgets=None):
+    """sparse_decode_layer without a workspace (aoakv_sparse_decode_layer_noalloc):
+    the library's own per-GPU scratch array, two launches, nothing allocated.
+    For callers that cannot allocate; calls that overlap on one GPU race."""
+    _need(q, "q", torch.float16)
+    _need(o, "o", torch.float16)
+    _need(kv_data, "kv_data", torch.float16)
+    _need(metadata_data, "metadata_data", torch.float16)
+    _need(scores, "scores", torch.float32)
+    _need(sel_pages, "sel_pages", torch.int32)
+    if flags & FLAG_VALUE_AWARE:
+        _need(v_log_norm, "v_log_norm", torch.float16)
+    if token_budgets is not None:
+        _need(token_budgets, "token_budgets", torch.int32)
+    _, S, Hkv, D = cache_dims(kv_data, layout)
+    B, Hq, _ = q.shape
+    _lib.call("aoakv_sparse_decode_layer_noalloc", q.data_ptr(), o.data_ptr(),
+              kv_data.data_ptr(), kv_indptr.data_ptr(), kv_indices.data_ptr(),
+              kv_last_page_len.data_ptr(), metadata_data.data_ptr(), metadata_indptr.data_ptr(),
+              metadata_indices.data_ptr(), _ptr(v_log_norm), scores.data_ptr(), scores.shape[-1],
+              sel_pages.data_ptr(), sel_pages.shape[-1], token_budget, _ptr(token_budgets), B,
+              max_pages, Hq, Hkv, D, S, layout, flags, _stream())
+
+
 def estimate_topk(q, metadata_data, metadata_indptr, metadata_indices, kv_indptr, kv_indices,
                   kv_last_page_len, v_log_norm, scores, sel_pages, token_budget: int, workspace,
                   max_pages: int, layout: int, flags: int = FLAG_VALUE_AWARE | FLAG_FIXED,

@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/aoakv.h"
@@ -184,6 +185,40 @@ int launch_estimate_topk(aoakv::EstimateArgs ea, const Workspace& w, int32_t* se
   ta.flags = flags & kSelectFlags;
   ta.error = ea.error;
   return hip_status(aoakv::launch_topk(ta, batch_size, s), "topk");
+}
+
+// ---------------------------------------------------------------- no-allocation scratch
+// aoakv_sparse_decode_layer_noalloc's workspace: a file-scope device array,
+// one per GPU the library runs on, held until the process ends.  Host code
+// never uses the array's name as an address (on the host it is only a
+// stand-in symbol): the device address comes from hipGetSymbolAddress, once
+// per device with that device current, and is kept per device.  The array
+// starts zeroed (module load), and the two-launch kernels that use it leave
+// its counters and partials at zero after every call, so no call clears it.
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64];
+
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess)
+    return fail(AOAKV_ERR_HIP, "sparse_decode_layer_noalloc: hipGetDevice: %s",
+                hipGetErrorString(e));
+  if (dev < 0 || dev >= 64)
+    return fail(AOAKV_ERR_UNSUPPORTED, "sparse_decode_layer_noalloc: device %d out of range",
+                dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)); e != hipSuccess || !p)
+      return fail(AOAKV_ERR_HIP, "sparse_decode_layer_noalloc: hipGetSymbolAddress: %s",
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return AOAKV_OK;
 }
 
 }  // namespace
@@ -615,6 +650,35 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
                                    batch_size, max_pages, page_size, flags, s))
     return e;
   return hip_status(aoakv::launch_decode(da, batch_size, s), "sparse_decode_layer/decode");
+}
+
+int aoakv_sparse_decode_layer_noalloc(
+    const void* q, void* o, const void* kv_data, const int32_t* kv_indptr,
+    const int32_t* kv_indices, const int32_t* kv_last_page_len, const void* metadata_data,
+    const int32_t* metadata_indptr, const int32_t* metadata_indices, const void* v_log_norm,
+    float* scores, uint32_t score_stride, int32_t* sel_pages, uint32_t sel_stride,
+    uint32_t token_budget, const int32_t* token_budgets, uint32_t batch_size, uint32_t max_pages,
+    uint32_t num_qo_heads, uint32_t num_kv_heads, uint32_t head_dim, uint32_t page_size,
+    uint32_t layout, uint32_t flags, void* stream) {
+  REQUIRE(!(flags & AOAKV_FLAG_SINGLE_LAUNCH),
+          "sparse_decode_layer_noalloc: runs the two-launch path only (AOAKV_FLAG_SINGLE_LAUNCH "
+          "needs a workspace the caller can re-initialise after a wait gave up)");
+  // the decode workspace this call lays out must fit the scratch array
+  const uint32_t row = sel_stride + ((flags & AOAKV_FLAG_QUEST_KERNEL) ? 1u : 0u);
+  const uint32_t max_sel = row < max_pages ? row : max_pages;
+  const size_t need = ws_layout(batch_size, num_qo_heads, num_kv_heads, max_sel, nullptr, nullptr);
+  REQUIRE(need <= kNoAllocScratchBytes,
+          "sparse_decode_layer_noalloc: this call needs %zu bytes of scratch, more than the "
+          "%zu the library holds per device (batch %u x %u query heads x %u selected pages)",
+          need, kNoAllocScratchBytes, batch_size, num_qo_heads, max_sel);
+  void* ws = nullptr;
+  if (int e = scratch_for_current_device(&ws)) return e;
+  return aoakv_sparse_decode_layer(q, o, kv_data, kv_indptr, kv_indices, kv_last_page_len,
+                                   metadata_data, metadata_indptr, metadata_indices, v_log_norm,
+                                   scores, score_stride, sel_pages, sel_stride, token_budget,
+                                   token_budgets, ws, kNoAllocScratchBytes, batch_size, max_pages,
+                                   num_qo_heads, num_kv_heads, head_dim, page_size, layout, flags,
+                                   stream);
 }
 
 int aoakv_estimate_topk(const void* q, const void* metadata_data, const int32_t* metadata_indptr,

@@ -303,6 +303,30 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
                               uint32_t page_size, uint32_t layout, uint32_t flags, void* stream);
 
 /*
+ * aoakv_sparse_decode_layer without a workspace, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * Same arguments, results and bits as aoakv_sparse_decode_layer's
+ * two-launch path (AOAKV_FLAG_SINGLE_LAUNCH is rejected); its workspace is
+ * a 16 MiB device array inside the library, one per GPU, held until the
+ * process ends.  A call whose decode workspace
+ * (aoakv_decode_workspace_size of the call's shape) exceeds 16 MiB is
+ * rejected with AOAKV_ERR_INVALID.  Allocates nothing.  Calls share their
+ * GPU's array: two calls that overlap on one GPU (different streams, or
+ * different host threads without ordering) race and give wrong results.
+ * The array's error word is not reported (a device page table longer than
+ * max_pages is still cut safely, as in aoakv_sparse_decode_layer).
+ */
+int aoakv_sparse_decode_layer_noalloc(
+    const void* q, void* o, const void* kv_data, const int32_t* kv_indptr,
+    const int32_t* kv_indices, const int32_t* kv_last_page_len, const void* metadata_data,
+    const int32_t* metadata_indptr, const int32_t* metadata_indices, const void* v_log_norm,
+    float* scores, uint32_t score_stride, int32_t* sel_pages, uint32_t sel_stride,
+    uint32_t token_budget, const int32_t* token_budgets, uint32_t batch_size, uint32_t max_pages,
+    uint32_t num_qo_heads, uint32_t num_kv_heads, uint32_t head_dim, uint32_t page_size,
+    uint32_t layout, uint32_t flags, void* stream);
+
+/*
  * estimate + top-k in one launch (the first launch of
  * aoakv_sparse_decode_layer): page scores are written to `scores` and the
  * last workgroup of each (sequence, kv head) selects into sel_pages.

@@ -167,3 +167,16 @@ def test_workspace_wait_flag_reads_word_2():
     ws[8:12].view(torch.int32).fill_(0)
     ws[12:16].view(torch.int32).fill_(7)   # other words do not count
     assert not ops.workspace_wait_failed(ws)
+
+
+def test_noalloc_entry_point_rejects_without_gpu():
+    """aoakv_sparse_decode_layer_noalloc checks its flags and its scratch
+    need on the host before touching the device."""
+    from aoakv import _lib
+    lib = _lib.load()
+    p = 1  # never dereferenced: the calls are rejected first
+    args = [p] * 11 + [16384, p, 8192, 256, None, 1, 16384, 32, 8, 128, 16, 1]
+    rc = lib.aoakv_sparse_decode_layer_noalloc(*args, _lib.FLAG_SINGLE_LAUNCH, None)
+    assert rc == _lib.AOAKV_ERR_INVALID and b"two-launch" in lib.aoakv_last_error()
+    rc = lib.aoakv_sparse_decode_layer_noalloc(*args, _lib.FLAG_VALUE_AWARE, None)
+    assert rc == _lib.AOAKV_ERR_INVALID and b"scratch" in lib.aoakv_last_error()
