@@ -55,7 +55,10 @@ enum : int {
   kTlOutput = 11,      // merging item: output stored (top-k workgroup: selection stored)
   kTlStaged = 12,      // top-k: keys staged, key range reduced
   kTlPass1 = 13,       // top-k: first radix pass done
-  kTlEvents = 14
+  kTlXcc = 14,         // (not a time) the XCD the workgroup ran on (HW_REG_XCC_ID)
+  kTlClk0 = 15,        // (core clock counter, s_memtime) at the workgroup's start
+  kTlClk1 = 16,        // ... and at its end
+  kTlEvents = 17
 };
 #ifdef AOAKV_TIMELINE
 constexpr uint32_t kTlMaxWg = 4096;
@@ -67,14 +70,19 @@ __shared__ unsigned long long s_tl[kTlEvents];
   } while (0)
 #define TL_BEGIN()                                                         \
   do {                                                                     \
-    if (threadIdx.x == 0u)                                                 \
+    if (threadIdx.x == 0u) {                                               \
       for (int e_ = 0; e_ < kTlEvents; ++e_) s_tl[e_] = 0ull;              \
+      s_tl[kTlXcc] = __builtin_amdgcn_s_getreg((20) | (0 << 6) | (15 << 11)); \
+      s_tl[kTlClk0] = __builtin_amdgcn_s_memtime();                        \
+    }                                                                      \
   } while (0)
 #define TL_FLUSH()                                                                         \
   do {                                                                                     \
     const uint32_t tl_wg = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z); \
-    if (threadIdx.x == 0u && tl_wg < kTlMaxWg)                                             \
+    if (threadIdx.x == 0u && tl_wg < kTlMaxWg) {                                           \
+      s_tl[kTlClk1] = __builtin_amdgcn_s_memtime();                                        \
       for (int e_ = 0; e_ < kTlEvents; ++e_) g_tl[tl_wg][e_] = s_tl[e_];                   \
+    }                                                                                      \
   } while (0)
 #else
 #define TL(ev) \

@@ -488,6 +488,7 @@ def timeline_pass(dev, layout, fn_layer, n_layers, samples=16, tick_ns=10.0, iso
         return dec0 + h * 16 + c
     per = []                # per sample: dict of per-head phase times (us)
     spans = []
+    xcds = []
     for smp in range(samples):
         g.replay()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -517,6 +518,17 @@ def timeline_pass(dev, layout, fn_layer, n_layers, samples=16, tick_ns=10.0, iso
             heads.append(row)
         per.append(heads)
         spans.append((max(h["output"] for h in heads), e0.elapsed_time(e1) * 1e3))
+        # placement and clock: XCD of each workgroup (is it index % 8?), and
+        # core cycles per 10 ns tick over each workgroup's life
+        xcc = t[:n_wg, 14]
+        rr = float(np.mean(xcc == (np.arange(n_wg) % 8)))
+        dt = (t[:n_wg, 16] - t[:n_wg, 15]).astype(np.float64)
+        life_ticks = np.array([max(r[r[:14] > 0][:14].max() - r[0], 1) if r[0] > 0 else 1
+                               for r in t[:n_wg, :14]], np.float64)
+        ghz = dt / (life_ticks * tick_ns)
+        xcds.append((rr, float(np.median(ghz))))
+        if smp == 0:
+            xcc_sample = [int(v) for v in xcc[:64]]
     # median over samples, per head and phase
     keys = [k for k in per[0][0] if k != "head"]
     table = []
@@ -525,6 +537,9 @@ def timeline_pass(dev, layout, fn_layer, n_layers, samples=16, tick_ns=10.0, iso
                                     for k in keys}})
     last = max(range(H_), key=lambda h: table[h]["output"])
     res = {"samples": samples, "tick_ns": tick_ns,
+           "workgroups_on_xcd_index_mod_8": round(float(np.median([a for a, _ in xcds])), 3),
+           "core_ghz_median": round(float(np.median([b for _, b in xcds])), 3),
+           "xcc_id_of_workgroups_0_63": xcc_sample,
            "end_us_median": round(float(np.median([a for a, _ in spans])), 2),
            "event_us_median": round(float(np.median([b for _, b in spans])), 2),
            "last_head": last, "heads": table}
@@ -541,7 +556,11 @@ def timeline_pass(dev, layout, fn_layer, n_layers, samples=16, tick_ns=10.0, iso
                 t = buf.astype(np.int64)[:n_grid]
                 live = t[:, 0] > 0
                 t0 = t[live, 0].min()
-                rows.append({nm: float(np.median((t[live & (t[:, ev] > 0), ev] - t0)) *
+                life = (t[live, :14].max(axis=1) - t[live, 0]).astype(np.float64) * tick_ns
+                cyc = (t[live, 16] - t[live, 15]).astype(np.float64)
+                ghz_iso = float(np.median(cyc / np.maximum(life, 1.0)))
+                rows.append({"core_ghz": ghz_iso} |
+                            {nm: float(np.median((t[live & (t[:, ev] > 0), ev] - t0)) *
                                        tick_ns / 1000.0) if np.any(live & (t[:, ev] > 0)) else None
                              for nm, ev in evs} |
                             {nm + "_max": float((t[live & (t[:, ev] > 0), ev].max() - t0) *
