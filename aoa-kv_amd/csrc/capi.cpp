@@ -632,7 +632,7 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
     la.est_chunks = aoakv::est_chunks(max_pages);
     la.n_est = batch_size * num_kv_heads * la.est_chunks;
     la.n_workers = aoakv::layer_score_workers(la.n_est, la.est_chunks);
-    la.stagger = aoakv::layer_stagger_cycles(la.est_chunks);
+    la.stagger_ps = aoakv::layer_stagger_ps(la.est_chunks);
     la.n_dec = batch_size * num_qo_heads * da.max_chunks;
     // one query head per kv head, score words, and the whole launch resident
     // at once: each decode item selects its head's pages itself (no top-k

@@ -137,6 +137,22 @@ __device__ inline uint32_t wave_reduce_u32(uint32_t v) {
 // error flag and goes on with stand-in data, so every wave still exits).
 constexpr uint32_t kSpinLimit = 1u << 18;
 
+// Sleeps until `ps` picoseconds of wall time have passed since t0, a reading
+// of s_memrealtime: a 100 MHz counter of its own, so the wait does not scale
+// with the core clock (1.3-2.6 GHz with load and temperature).  The counter
+// is read a few times per wait, not polled: between reads the wave sleeps
+// for a bound on the time left (one `s_sleep 1` lasts 64 core cycles, at
+// most 5 ticks at 1.3 GHz), so each read finds at most the time left and
+// the reads converge on the end.  Polling a clock (s_memrealtime or
+// s_memtime) in every waiting wave slowed the whole layer by 0.4-1 us.
+__device__ inline void sleep_until(uint64_t t0, uint64_t ps) {
+  const uint64_t end = t0 + ps / 10000u;
+  for (uint64_t now = __builtin_amdgcn_s_memrealtime(); now < end;
+       now = __builtin_amdgcn_s_memrealtime()) {
+    for (uint32_t n = (uint32_t)((end - now) / 5u) + 1u; n != 0u; --n) __builtin_amdgcn_s_sleep(1);
+  }
+}
+
 // Polls an agent-coherent handoff word until it is written (non-zero);
 // returns the value - 1, or 0 after kSpinLimit polls with *error set.
 __device__ inline uint32_t wait_word(const uint32_t* p, uint32_t* error) {
@@ -1366,11 +1382,8 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la)
   const uint32_t t = blockIdx.x;
   TL(kTlStart);
   if (t < la.n_workers) {
-    {  // first item's head bh0 starts bh0 * stagger cycles in (see layer_stagger_cycles)
-      const unsigned long long t0 = clock64();
-      const unsigned long long wait = (unsigned long long)(t / la.est_chunks) * la.stagger;
-      while (clock64() - t0 < wait) __builtin_amdgcn_s_sleep(1);
-    }
+    // the first item's head bh0 starts bh0 * stagger in (see layer_stagger_ps)
+    sleep_until(__builtin_amdgcn_s_memrealtime(), (uint64_t)(t / la.est_chunks) * la.stagger_ps);
     TL(kTlStaggerDone);
     int tl_item = 0;
     for (uint32_t i = t; i < la.n_est; i += la.n_workers) {
@@ -1380,7 +1393,7 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la)
         TL(tl_item == 0 ? kTlScored0 : kTlScored1);
         ++tl_item;
         (void)tl_item;
-        if (la.e.hscore != nullptr) {
+        if (SELF || la.e.hscore != nullptr) {  // (SELF runs on score words only)
           // the scores went out as handoff words: only end this item's use
           // of LDS before the next item's
           __syncthreads();
@@ -1395,7 +1408,7 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la)
         }
       }
     }
-  } else if (t < la.n_workers + la.n_heads) {
+  } else if (!SELF && t < la.n_workers + la.n_heads) {  // (SELF: no top-k workgroups)
     const uint32_t err0 = *la.d.error;
     const uint32_t bh = t - la.n_workers;
     const uint32_t b = bh / la.e.Hkv, h = bh % la.e.Hkv;
@@ -1438,10 +1451,8 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la)
       // polls to the memory traffic of the first heads' scoring (23.0 vs
       // 24.15 us per layer at config 2)
       const uint32_t first_round = (la.n_workers - 1u) / la.est_chunks;
-      const unsigned long long t0 = clock64();
-      const unsigned long long wait =
-          (unsigned long long)(bh < first_round ? bh : first_round) * la.stagger;
-      while (clock64() - t0 < wait) __builtin_amdgcn_s_sleep(8);
+      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+      sleep_until(t0, (uint64_t)(bh < first_round ? bh : first_round) * la.stagger_ps);
       TL(kTlStaggerDone);
       decode_item<true, QUEST, true>(la.d, b, hq, chunk, sm.d, &la.e, &sm.e.tk, &s_err, err0);
     } else {
@@ -1549,17 +1560,19 @@ uint32_t layer_score_workers(uint32_t n_est, uint32_t est_chunks) {
 // The scoring workers of the first round would otherwise issue all their
 // loads at once, and HBM would finish every head's chunks at about the same
 // time, late (a head is done when its last chunk is).  Starting head h's
-// workers h * stagger cycles in, a little faster than HBM streams one head's
-// metadata (est_chunks * 128 pages * 514 B at 2,800 B per core cycle, ~6.7
-// TB/s at 2.4 GHz, so the memory queue never runs dry), finishes the heads
-// one after another, so the top-k, gathers and merge of the first heads
-// overlap the scoring of the later ones.  Config 2 (16 chunks per head), us
-// per layer by cycles per head: none 24.95, 300: 24.7, 350: 24.42, 376:
-// 24.37, 400: 24.42-24.5, 421: 24.7, 450: 25.2, 700: 26.4.
-uint32_t layer_stagger_cycles(uint32_t est_chunks) {
-  constexpr uint32_t kChunkBytes = kEstPagesPerBlock * (2u * kHeadDim * 2u + 2u);
-  constexpr uint32_t kStreamBytesPerCycle = 2800u;
-  return (uint32_t)((uint64_t)est_chunks * kChunkBytes / kStreamBytesPerCycle);
+// workers h * stagger in, a little faster than HBM streams one head's
+// metadata (est_chunks * 128 pages * 514 B at kStreamBytesPerNs, so the
+// memory queue never runs dry), finishes the heads one after another, so the
+// top-k, gathers and merge of the first heads overlap the scoring of the
+// later ones.  Timed in wall time (s_memrealtime), not core cycles, so the
+// offset holds whatever the clock.  Config 2 (16 chunks per head: 1.05 MB),
+// us per layer by bytes per ns: 5600: 24.06, 6100: 23.69, 6600: 23.35-23.39,
+// 7100: 23.20-23.26, 7600: 23.31, 8200: 23.49, 9000: 23.85 (the former
+// core-cycle stagger at its best, 376 cycles per head: 23.26).
+uint32_t layer_stagger_ps(uint32_t est_chunks) {
+  constexpr uint64_t kChunkBytes = kEstPagesPerBlock * (2u * kHeadDim * 2u + 2u);
+  constexpr uint64_t kStreamBytesPerNs = 7100u;
+  return (uint32_t)((uint64_t)est_chunks * kChunkBytes * 1000u / kStreamBytesPerNs);
 }
 uint32_t counter_stride() { return kCounterStride; }
 // Workgroups of the self-selecting layer kernel one CU holds at once (its LDS

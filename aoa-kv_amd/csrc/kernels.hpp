@@ -168,7 +168,7 @@ struct LayerArgs {
   uint32_t n_workers;  // scoring workgroups (<= n_est), items taken round-robin
   uint32_t n_heads;    // top-k workgroups: B * Hkv
   uint32_t n_dec;      // decode items: B * Hq * d.max_chunks
-  uint32_t stagger;    // core cycles between the scoring starts of consecutive heads
+  uint32_t stagger_ps; // wall time (ps) between the scoring starts of consecutive heads
   uint32_t self_select;  // decode items run their head's top-k themselves (n_heads = 0)
 };
 
@@ -189,7 +189,7 @@ uint32_t decode_max_chunks();  // split-K chunks per head the merge holds
 uint32_t topk_max_pages();     // pages per (sequence, head) top-k supports
 uint32_t fused_topk_max_pages();  // ... and the fused estimate + top-k kernel
 uint32_t layer_score_workers(uint32_t n_est, uint32_t est_chunks);  // one-launch layer scorers
-uint32_t layer_stagger_cycles(uint32_t est_chunks);  // one-launch scoring start offset per head
+uint32_t layer_stagger_ps(uint32_t est_chunks);  // one-launch scoring start offset per head (ps)
 uint32_t counter_stride();        // u32 words between per-head counters (one cache line each)
 uint32_t layer_self_blocks_per_cu();  // self-selecting layer workgroups resident per CU
 
