@@ -672,7 +672,7 @@ def main():
         for l in range(n_layers):
             layer1(l)
         torch.cuda.synchronize()
-        log("[bench] pmc pass done")
+        log(f"[bench] pmc pass done (libaoakv.so md5 {so_identity()['so_md5']})")
         return
 
     if args.timeline_pass:
