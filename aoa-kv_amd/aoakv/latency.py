@@ -58,6 +58,9 @@ def parse_args(argv=None):
     p.add_argument("--page_size", type=int, default=16)
     p.add_argument("--iteration", type=int, default=10)
     p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--roctx", action="store_true",
+                   help="open the reference's nvtx ranges as roctx ranges (aoakv.tracing; "
+                        "recorded by rocprofv3 --marker-trace)")
     p.add_argument("--three_call", action="store_true",
                    help="decode with the reference's three calls instead of one launch")
     p.add_argument("--out", default=None, help="CSV to append to (optional)")
@@ -76,6 +79,9 @@ def main(argv=None):
     from . import _lib
     from .shim import MODEL_SHAPES, QuestLlamaModel
 
+    if args.roctx:
+        from . import tracing
+        tracing.enable()
     lib_path = Path(_lib.loaded_path()).resolve()
     md5 = hashlib.md5(lib_path.read_bytes()).hexdigest()
     device = torch.device("cuda:0")

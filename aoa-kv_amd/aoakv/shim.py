@@ -18,6 +18,7 @@ from typing import Optional
 import torch
 from torch import nn
 
+from . import tracing as tr
 from . import utils as qutils
 from .utils import InferenceController, TensorLayout
 
@@ -83,22 +84,33 @@ class QuestAttention(nn.Module):
         bsz, q_len, _ = hidden_states.shape
         assert bsz == 1, "QuestAttention only supports batch size 1."
         c = iController
-        q = self.q_proj(hidden_states).view(q_len, self.num_heads, self.head_dim)
-        k = self.k_proj(hidden_states).view(q_len, self.num_key_value_heads, self.head_dim)
-        v = self.v_proj(hidden_states).view(q_len, self.num_key_value_heads, self.head_dim)
-        qutils.rope_append_kv(q, k, v, c, self.layer_idx, rope_scale=self.rope_scale,
-                              rope_theta=self.rope_theta)
+        # roctx ranges named as the reference's nvtx ranges (QuestAttention.py:87-176);
+        # RoPE and the append are one launch here
+        with tr.range("qkv_proj"):
+            q = self.q_proj(hidden_states).view(q_len, self.num_heads, self.head_dim)
+            k = self.k_proj(hidden_states).view(q_len, self.num_key_value_heads, self.head_dim)
+            v = self.v_proj(hidden_states).view(q_len, self.num_key_value_heads, self.head_dim)
+        with tr.range("RoPE+append_kv"):
+            qutils.rope_append_kv(q, k, v, c, self.layer_idx, rope_scale=self.rope_scale,
+                                  rope_theta=self.rope_theta)
         if q_len > 1:
-            o = qutils.prefill_forward(q, c, self.layer_idx)
+            with tr.range("prefill_attn"):
+                o = qutils.prefill_forward(q, c, self.layer_idx)
         elif not c.need_estimate():
-            o = qutils.decode_sparse_attn(q, c, self.layer_idx, c.kv_indices_without_last)
+            with tr.range("full_attn"):
+                o = qutils.decode_sparse_attn(q, c, self.layer_idx, c.kv_indices_without_last)
         elif self.single_launch:
-            o = qutils.decode_layer(q, c, self.layer_idx, single_launch=True)
+            with tr.range("estimate+topk+approx_attn"):
+                o = qutils.decode_layer(q, c, self.layer_idx, single_launch=True)
         else:
-            s = qutils.decode_estimate(q, c, self.layer_idx)
-            qutils.decode_topk(s, c)
-            o = qutils.decode_sparse_attn(q, c, self.layer_idx, c.topk_dindices_buffer)
-        return self.o_proj(o.reshape(1, q_len, self.hidden_size))
+            with tr.range("estimate"):
+                s = qutils.decode_estimate(q, c, self.layer_idx)
+            with tr.range("topk"):
+                qutils.decode_topk(s, c)
+            with tr.range("approx_attn"):
+                o = qutils.decode_sparse_attn(q, c, self.layer_idx, c.topk_dindices_buffer)
+        with tr.range("o_proj"):
+            return self.o_proj(o.reshape(1, q_len, self.hidden_size))
 
 
 class LlamaMLP(nn.Module):
@@ -121,8 +133,15 @@ class DecoderLayer(nn.Module):
         self.mlp = LlamaMLP(cfg)
 
     def forward(self, h, iController):
-        h = h + self.self_attn(self.input_layernorm(h), iController)
-        return h + self.mlp(self.post_attention_layernorm(h))
+        # ranges as the reference's decoder layer (llama.py:138-164)
+        with tr.range("input_norm"):
+            x = self.input_layernorm(h)
+        with tr.range("LlamaAttention"):
+            h = h + self.self_attn(x, iController)
+        with tr.range("norm"):
+            x = self.post_attention_layernorm(h)
+        with tr.range("mlp"):
+            return h + self.mlp(x)
 
 
 class QuestLlamaModel(nn.Module):
@@ -183,6 +202,7 @@ class QuestLlamaModel(nn.Module):
                 c.end_forward()
                 c.set_page_budget(self._page_budget)
                 c.begin_forward(seq_len, updateTensor=(idx == 0))
-            h = layer(h, c)
+            with tr.range(f"layer={idx}"):  # llama.py:465-475
+                h = layer(h, c)
         c.end_forward()
         return self.norm(h)
