@@ -9,6 +9,12 @@ switch trees.  Differences, by design:
   first and last page, k = min(max(3, min(L, budget)/page), P));
 * the decode workspace is allocated once, not per begin_forward, and no op
   synchronises with the host;
+* the device page tables live in buffers allocated once: begin_forward
+  writes only what changed since the last call (the new page ids, the page
+  counts, the last page's length) with fills that carry the value as a
+  kernel argument, so a decode step makes no host-to-device copy and no
+  allocation; ``kv_indices_without_last`` is a broadcast view, not the
+  reference's per-head copy (controller.py:130-131);
 * scores are fp32 and the per-page value statistic is written for every
   page, with the page mean of V kept in ``v_mean`` for the running mean.
 
@@ -69,13 +75,25 @@ class InferenceController:
         self.inference_page_budget = None
 
         self.kv_indices_with_last = None
-        self.kv_indices_without_last = None
         self.metadata_indices = None
         self.kv_last_page_idx = None
         self.metadata_last_page_idx = None
         self.kv_indptr_for_append = None
         self.metadata_indptr_for_append = None
         self.kv_last_page_len_t = None
+        self._kv_without_last = None
+
+        # device page tables, written incrementally by begin_forward: page
+        # ids [0, n) of kv / metadata are on the device (n_up), as are the
+        # page counts and last page length last written
+        max_md_pages = (max_kv_pages + page_size - 1) // page_size
+        i32 = dict(dtype=torch.int32, device=device)
+        self._kv_ids = torch.zeros(max_kv_pages, **i32)
+        self._md_ids = torch.zeros(max_md_pages, **i32)
+        self._kv_indptr = torch.zeros(2, **i32)
+        self._md_indptr = torch.zeros(2, **i32)
+        self._lpl = torch.zeros(1, **i32)
+        self._up = {"kv": 0, "md": 0, "P": 0, "Pm": 0, "lpl": 0}
 
         # fixed-size decode buffers (one layer at a time)
         self.scores = torch.empty((1, self.num_kv_heads, max_kv_pages), dtype=torch.float32,
@@ -116,22 +134,43 @@ class InferenceController:
         new_pages = self.kv_cache.append_seq(seq_len)
         self.metadata_cache.append_seq(new_pages)
 
+    @staticmethod
+    def _sync_ids(buf: torch.Tensor, ids, done: int) -> int:
+        """Writes ids[done:] into buf (ids [0, done) are there already);
+        returns len(ids).  One new page (a decode step every page_size
+        tokens) is a fill; more (a prefill) one copy."""
+        n = len(ids)
+        if n - done == 1:
+            buf[n - 1].fill_(ids[n - 1])
+        elif n > done:
+            buf[done:n].copy_(torch.tensor(ids[done:], dtype=torch.int32))
+        return n
+
     def begin_forward(self, seq_len: int, updateTensor: bool = True):
-        """Upload the page tables for the coming ops (controller.py:92-141)."""
+        """Update the device page tables for the coming ops (controller.py:92-141):
+        only what changed since the last call is written."""
         kv = self.kv_cache.indicies
         md = self.metadata_cache.indicies
         if updateTensor:
-            dev = self.device
-            self.kv_indices_with_last = torch.tensor(kv, dtype=torch.int32, device=dev)
-            self.metadata_indices = torch.tensor(md, dtype=torch.int32, device=dev)
-            self.kv_indptr_for_append = torch.tensor([0, len(kv)], dtype=torch.int32, device=dev)
-            self.metadata_indptr_for_append = torch.tensor([0, len(md)], dtype=torch.int32,
-                                                           device=dev)
-            self.kv_last_page_len_t = torch.tensor([self.kv_cache.last_page_len],
-                                                   dtype=torch.int32, device=dev)
+            up = self._up
+            P, Pm, lpl = len(kv), len(md), self.kv_cache.last_page_len
+            if P < up["kv"] or Pm < up["md"]:  # pages were released
+                up.update(kv=0, md=0)
+            up["kv"] = self._sync_ids(self._kv_ids, kv, up["kv"])
+            up["md"] = self._sync_ids(self._md_ids, md, up["md"])
+            for key, val, t in (("P", P, self._kv_indptr[1]), ("Pm", Pm, self._md_indptr[1]),
+                                ("lpl", lpl, self._lpl[0])):
+                if up[key] != val:
+                    t.fill_(val)
+                    up[key] = val
+            self.kv_indices_with_last = self._kv_ids[:P]
+            self.metadata_indices = self._md_ids[:Pm]
+            self.kv_indptr_for_append = self._kv_indptr
+            self.metadata_indptr_for_append = self._md_indptr
+            self.kv_last_page_len_t = self._lpl
             self.kv_last_page_idx = kv[-1]
             self.metadata_last_page_idx = md[-1]
-            self.kv_indices_without_last = self.kv_indices_with_last[:-1].repeat(self.num_heads, 1)
+            self._kv_without_last = None
         if seq_len == 1:
             P = len(kv)
             self.inference_page_budget = min(self._page_budget, P)
@@ -141,6 +180,19 @@ class InferenceController:
 
     def end_forward(self):
         pass
+
+    @property
+    def kv_indices_without_last(self) -> Optional[torch.Tensor]:
+        """[num_heads, P - 1]: every page but the last, per head (the dense
+        decode's page list, controller.py:130-131); a broadcast view of the
+        page table, the same object until the next begin_forward."""
+        if self.kv_indices_with_last is None:
+            return None
+        if self._kv_without_last is None:
+            P = self.kv_indices_with_last.numel()
+            self._kv_without_last = self._kv_ids[:max(P - 1, 0)].unsqueeze(0).expand(
+                self.num_heads, max(P - 1, 0))
+        return self._kv_without_last
 
     def need_estimate(self) -> bool:
         """True when the sequence has more pages than the page budget."""
@@ -178,6 +230,7 @@ class InferenceController:
     def clean_states(self):
         self.kv_cache.release()
         self.metadata_cache.release()
+        self._up.update(kv=0, md=0)
 
     def v_log_norm_layer(self, layer_idx: int):
         return self.v_log_norm[layer_idx]

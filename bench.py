@@ -127,8 +127,11 @@ def decode_appends(dev, layout, n_app=512, mode="append", graph=True):
     for i in range(n_app):
         c.prepare_metadata(1)
         c.begin_forward(1)
-        steps.append((c.kv_indptr_for_append, c.kv_indices_with_last, c.kv_last_page_len_t,
-                      c.metadata_indptr_for_append, c.metadata_indices))
+        # (the controller updates one set of device tables in place: keep a
+        # copy of each step's)
+        steps.append(tuple(t.clone() for t in (
+            c.kv_indptr_for_append, c.kv_indices_with_last, c.kv_last_page_len_t,
+            c.metadata_indptr_for_append, c.metadata_indices)))
     torch.cuda.synchronize()
 
     def run_steps():
