@@ -15,12 +15,12 @@
 #include "kernels.hpp"
 
 namespace aoakv {
-RopeFreqs rope_freqs(float rope_scale, float rope_theta) {
-  RopeFreqs r;
+RopeFreqs rope_freqs(float rope_scale, float rope_theta, uint32_t head_dim) {
+  RopeFreqs r{};
   const float rcp_scale = 1.0f / rope_scale, rcp_theta = 1.0f / rope_theta;
-  for (int i = 0; i < kHeadDim / 2; ++i)
+  for (uint32_t i = 0; i < head_dim / 2u; ++i)
     r.f[i] = (float)((double)rcp_scale *
-                     std::pow((double)rcp_theta, (double)(2 * i) / (double)kHeadDim));
+                     std::pow((double)rcp_theta, (double)(2u * i) / (double)head_dim));
   return r;
 }
 }  // namespace aoakv
@@ -72,11 +72,14 @@ uint32_t resident_layer_workgroups() {
     if (!(cond)) return fail(AOAKV_ERR_INVALID, __VA_ARGS__); \
   } while (0)
 
+// head_dim 64 / 128 / 256 (the reference's SWITCH_HEAD_DIM) and page sizes
+// 1..32; (128, 16) runs the tuned kernels, the rest generic.hip's
 int check_shape(uint32_t head_dim, uint32_t page_size, uint32_t layout, uint32_t num_heads) {
-  if (head_dim != (uint32_t)aoakv::kHeadDim)
-    return fail(AOAKV_ERR_UNSUPPORTED, "head_dim %u unsupported (only 128)", head_dim);
-  if (page_size != (uint32_t)aoakv::kPageSize)
-    return fail(AOAKV_ERR_UNSUPPORTED, "page_size %u unsupported (only 16)", page_size);
+  if (head_dim != 64u && head_dim != 128u && head_dim != 256u)
+    return fail(AOAKV_ERR_UNSUPPORTED, "head_dim %u unsupported (64, 128, 256)", head_dim);
+  if (page_size == 0u || page_size > aoakv::kMaxPageSize)
+    return fail(AOAKV_ERR_UNSUPPORTED, "page_size %u unsupported (1..%u)", page_size,
+                aoakv::kMaxPageSize);
   if (layout > 1u) return fail(AOAKV_ERR_UNSUPPORTED, "layout %u unknown (0=NHD, 1=HND)", layout);
   if (num_heads == 0u || num_heads > 256u)
     return fail(AOAKV_ERR_UNSUPPORTED, "num_heads %u out of range [1, 256]", num_heads);
@@ -155,12 +158,14 @@ size_t ws_layout(uint32_t B, uint32_t hq, uint32_t hkv, uint32_t max_sel_pages, 
 }
 
 // Scores + top-k: one fused launch when every sequence fits the fused
-// kernel's top-k, else scores then the standalone top-k kernel.
+// kernel's top-k, else scores then the standalone top-k kernel (always so
+// for the shapes of generic.hip).
 int launch_estimate_topk(aoakv::EstimateArgs ea, const Workspace& w, int32_t* sel_pages,
                          uint32_t sel_stride, uint32_t token_budget, const int32_t* token_budgets,
-                         uint32_t batch_size, uint32_t max_pages, uint32_t page_size,
-                         uint32_t flags, hipStream_t s) {
-  if (max_pages <= aoakv::fused_topk_max_pages()) {
+                         uint32_t batch_size, uint32_t max_pages, uint32_t head_dim,
+                         uint32_t page_size, uint32_t flags, hipStream_t s) {
+  const bool tuned = aoakv::tuned_shape(head_dim, page_size);
+  if (tuned && max_pages <= aoakv::fused_topk_max_pages()) {
     ea.sel = sel_pages;
     ea.sel_stride = sel_stride;
     ea.token_budget = token_budget;
@@ -168,7 +173,9 @@ int launch_estimate_topk(aoakv::EstimateArgs ea, const Workspace& w, int32_t* se
     ea.counters = w.est_counters;
     return hip_status(aoakv::launch_estimate(ea, batch_size, max_pages, s), "estimate_topk");
   }
-  if (int e = hip_status(aoakv::launch_estimate(ea, batch_size, max_pages, s), "estimate"))
+  if (int e = hip_status(tuned ? aoakv::launch_estimate(ea, batch_size, max_pages, s)
+                               : aoakv::launch_gen_estimate(ea, batch_size, max_pages, head_dim, s),
+                         "estimate"))
     return e;
   aoakv::TopkArgs ta{};
   ta.scores = ea.scores;
@@ -263,7 +270,10 @@ int aoakv_append_kv_cache_prefill(const void* k, const void* v, uint32_t num_new
   a.num_pages = num_kv_pages;
   a.last_page_len = kv_last_page_len;
   a.g = aoakv::make_geom(layout, num_heads, page_size, head_dim);
-  return hip_status(aoakv::launch_append_prefill(a, static_cast<hipStream_t>(stream)),
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return hip_status(aoakv::tuned_shape(head_dim, page_size)
+                        ? aoakv::launch_append_prefill(a, s)
+                        : aoakv::launch_gen_append_prefill(a, head_dim, s),
                     "append_kv_cache_prefill");
 }
 
@@ -296,7 +306,10 @@ int aoakv_append_kv_cache_decode(const void* k, const void* v, uint32_t batch_si
   a.H = num_heads;
   a.S = page_size;
   a.g = aoakv::make_geom(layout, num_heads, page_size, head_dim);
-  return hip_status(aoakv::launch_append_decode(a, batch_size, static_cast<hipStream_t>(stream)),
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return hip_status(aoakv::tuned_shape(head_dim, page_size)
+                        ? aoakv::launch_append_decode(a, batch_size, s)
+                        : aoakv::launch_gen_append_decode(a, batch_size, head_dim, s),
                     "append_kv_cache_decode");
 }
 
@@ -328,8 +341,11 @@ int aoakv_apply_rope_in_place(void* q, void* k, uint32_t seq_len, uint32_t past_
   a.past = past_kv_len;
   a.Hq = num_qo_heads;
   a.Hkv = num_kv_heads;
-  a.rope_f = aoakv::rope_freqs(rope_scale, rope_theta);
-  return hip_status(aoakv::launch_rope(a, static_cast<hipStream_t>(stream)), "apply_rope_in_place");
+  a.rope_f = aoakv::rope_freqs(rope_scale, rope_theta, head_dim);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return hip_status(head_dim == (uint32_t)aoakv::kHeadDim ? aoakv::launch_rope(a, s)
+                                                          : aoakv::launch_gen_rope(a, head_dim, s),
+                    "apply_rope_in_place");
 }
 
 int aoakv_rope_append_kv_cache_decode(void* q, void* k, const void* v, uint32_t batch_size,
@@ -369,8 +385,11 @@ int aoakv_rope_append_kv_cache_decode(void* q, void* k, const void* v, uint32_t 
   a.rope = 1u;
   a.q = static_cast<aoakv::f16*>(q);
   a.Hq = num_qo_heads;
-  a.rope_f = aoakv::rope_freqs(rope_scale, rope_theta);
-  return hip_status(aoakv::launch_append_decode(a, batch_size, static_cast<hipStream_t>(stream)),
+  a.rope_f = aoakv::rope_freqs(rope_scale, rope_theta, head_dim);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return hip_status(aoakv::tuned_shape(head_dim, page_size)
+                        ? aoakv::launch_append_decode(a, batch_size, s)
+                        : aoakv::launch_gen_append_decode(a, batch_size, head_dim, s),
                     "rope_append_kv_cache_decode");
 }
 
@@ -430,9 +449,11 @@ int aoakv_estimate_attn_score(const void* q, float* scores, uint32_t score_strid
                             v_log_norm, batch_size, max_pages, num_qo_heads, num_kv_heads,
                             head_dim, page_size, layout, flags))
     return e;
-  return hip_status(
-      aoakv::launch_estimate(a, batch_size, max_pages, static_cast<hipStream_t>(stream)),
-      "estimate_attn_score");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return hip_status(aoakv::tuned_shape(head_dim, page_size)
+                        ? aoakv::launch_estimate(a, batch_size, max_pages, s)
+                        : aoakv::launch_gen_estimate(a, batch_size, max_pages, head_dim, s),
+                    "estimate_attn_score");
 }
 
 int aoakv_topk_filtering(const float* scores, uint32_t score_stride,
@@ -443,8 +464,8 @@ int aoakv_topk_filtering(const float* scores, uint32_t score_stride,
                          uint32_t flags, void* stream) {
   REQUIRE(scores && kv_indptr && kv_indices && kv_last_page_len && sel_pages,
           "topk_filtering: null pointer argument");
-  REQUIRE(page_size == (uint32_t)aoakv::kPageSize, "topk_filtering: page_size %u unsupported",
-          page_size);
+  REQUIRE(page_size >= 1u && page_size <= aoakv::kMaxPageSize,
+          "topk_filtering: page_size %u unsupported (1..%u)", page_size, aoakv::kMaxPageSize);
   REQUIRE(batch_size >= 1u && batch_size <= 65535u && num_kv_heads >= 1u &&
               num_kv_heads <= 65535u,
           "topk_filtering: bad batch_size %u / num_kv_heads %u", batch_size, num_kv_heads);
@@ -570,7 +591,10 @@ int aoakv_decode_sparse_attn(const void* q, void* o, const void* kv_data,
                           workspace_bytes, batch_size, max_pages, num_qo_heads, num_kv_heads,
                           head_dim, page_size, layout, flags))
     return e;
-  return hip_status(aoakv::launch_decode(a, batch_size, static_cast<hipStream_t>(stream)),
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return hip_status(aoakv::tuned_shape(head_dim, page_size)
+                        ? aoakv::launch_decode(a, batch_size, s)
+                        : aoakv::launch_gen_decode(a, batch_size, head_dim, s),
                     "decode_sparse_attn");
 }
 
@@ -606,7 +630,8 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
   hipStream_t s = static_cast<hipStream_t>(stream);
   ea.flags &= kSelectFlags;
   ea.error = da.error;
-  if ((flags & AOAKV_FLAG_SINGLE_LAUNCH) && max_pages <= aoakv::fused_topk_max_pages()) {
+  const bool tuned = aoakv::tuned_shape(head_dim, page_size);
+  if (tuned && (flags & AOAKV_FLAG_SINGLE_LAUNCH) && max_pages <= aoakv::fused_topk_max_pages()) {
     // one launch: scoring, top-k and decode items of every head
     aoakv::LayerArgs la{};
     la.e = ea;
@@ -647,9 +672,11 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
     return hip_status(aoakv::launch_layer(la, s), "sparse_decode_layer");
   }
   if (int e = launch_estimate_topk(ea, w, sel_pages, sel_stride, token_budget, token_budgets,
-                                   batch_size, max_pages, page_size, flags, s))
+                                   batch_size, max_pages, head_dim, page_size, flags, s))
     return e;
-  return hip_status(aoakv::launch_decode(da, batch_size, s), "sparse_decode_layer/decode");
+  return hip_status(tuned ? aoakv::launch_decode(da, batch_size, s)
+                          : aoakv::launch_gen_decode(da, batch_size, head_dim, s),
+                    "sparse_decode_layer/decode");
 }
 
 int aoakv_sparse_decode_layer_noalloc(
@@ -708,7 +735,7 @@ int aoakv_estimate_topk(const void* q, const void* metadata_data, const int32_t*
           workspace_bytes, need);
   ea.error = w.ctl + aoakv::kErrWord;
   return launch_estimate_topk(ea, w, sel_pages, sel_stride, token_budget, token_budgets,
-                              batch_size, max_pages, page_size, flags,
+                              batch_size, max_pages, head_dim, page_size, flags,
                               static_cast<hipStream_t>(stream));
 }
 
@@ -743,9 +770,11 @@ int aoakv_prefill_with_paged_kv_cache(const void* q, void* o, const void* kv_dat
   a.L = (uint32_t)L;
   a.Lq = qo_len;
   a.causal = causal ? 1u : 0u;
-  a.sm_scale = 1.0f / aoakv::kSqrtHeadDim;
+  a.sm_scale = 1.0f / std::sqrt((float)head_dim);
   a.g = aoakv::make_geom(layout, num_kv_heads, page_size, head_dim);
-  return hip_status(aoakv::launch_prefill(a, static_cast<hipStream_t>(stream)),
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return hip_status(aoakv::tuned_shape(head_dim, page_size) ? aoakv::launch_prefill(a, s)
+                                                              : aoakv::launch_gen_prefill(a, head_dim, s),
                     "prefill_with_paged_kv_cache");
 }
 

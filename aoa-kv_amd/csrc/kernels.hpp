@@ -27,13 +27,22 @@ __device__ inline void flag_error(uint32_t* error, uint32_t bits) {
   if (error != nullptr) atomicOr(error, bits);
 }
 
-// RoPE frequencies f_i = rcp_scale * rcp_theta^(2i / 128), i < 64: fixed by
-// (rope_scale, rope_theta), so computed once on the host (rope_freqs) and
+// Head dims the library takes: the tuned kernels are for kHeadDim (with
+// kPageSize); 64 and 256, and other page sizes up to kMaxPageSize, run the
+// kernels of generic.hip.
+constexpr int kMaxHeadDim = 256;
+constexpr uint32_t kMaxPageSize = 32;
+inline bool tuned_shape(uint32_t head_dim, uint32_t page_size) {
+  return head_dim == (uint32_t)kHeadDim && page_size == (uint32_t)kPageSize;
+}
+
+// RoPE frequencies f_i = rcp_scale * rcp_theta^(2i / D), i < D / 2: fixed by
+// (rope_scale, rope_theta, D), so computed once on the host (rope_freqs) and
 // passed with the launch instead of per lane on the device.
 struct RopeFreqs {
-  float f[kHeadDim / 2];
+  float f[kMaxHeadDim / 2];
 };
-RopeFreqs rope_freqs(float rope_scale, float rope_theta);
+RopeFreqs rope_freqs(float rope_scale, float rope_theta, uint32_t head_dim = kHeadDim);
 
 struct AppendPrefillArgs {
   const f16* k;            // [N, H, D]
@@ -192,5 +201,16 @@ uint32_t layer_score_workers(uint32_t n_est, uint32_t est_chunks);  // one-launc
 uint32_t layer_stagger_ps(uint32_t est_chunks);  // one-launch scoring start offset per head (ps)
 uint32_t counter_stride();        // u32 words between per-head counters (one cache line each)
 uint32_t layer_self_blocks_per_cu();  // self-selecting layer workgroups resident per CU
+
+// generic.hip: the other head dims (64, 128, 256) and page sizes (1..32)
+hipError_t launch_gen_append_prefill(const AppendPrefillArgs& a, uint32_t head_dim, hipStream_t s);
+hipError_t launch_gen_append_decode(const AppendDecodeArgs& a, uint32_t batch, uint32_t head_dim,
+                                    hipStream_t s);
+hipError_t launch_gen_rope(const RopeArgs& a, uint32_t head_dim, hipStream_t s);
+hipError_t launch_gen_estimate(const EstimateArgs& a, uint32_t batch, uint32_t max_pages,
+                               uint32_t head_dim, hipStream_t s);
+hipError_t launch_gen_decode(const DecodeArgs& a, uint32_t batch, uint32_t head_dim,
+                             hipStream_t s);
+hipError_t launch_gen_prefill(const PrefillArgs& a, uint32_t head_dim, hipStream_t s);
 
 }  // namespace aoakv

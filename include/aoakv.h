@@ -47,8 +47,12 @@
  *     device memory and performs no host synchronisation.
  *   - Return value: 0 on success, otherwise an AOAKV_ERR_* code;
  *     aoakv_last_error() then describes the failure (thread-local).
- *   - Supported shapes: head_dim 128, page_size 16, num_heads <= 256,
- *     num_qo_heads a multiple of num_kv_heads with group size <= 8.
+ *   - Supported shapes: head_dim 64, 128 or 256 (the reference's
+ *     SWITCH_HEAD_DIM, decode_page.cuh:718-760), page_size 1..32,
+ *     num_heads <= 256, num_qo_heads a multiple of num_kv_heads with group
+ *     size 1, 2, 4 or 8.  head_dim 128 with page_size 16 runs the tuned
+ *     kernels; the other shapes run simpler kernels with the same results
+ *     (AOAKV_FLAG_SINGLE_LAUNCH is then ignored: two launches).
  */
 #ifndef AOAKV_H_
 #define AOAKV_H_

@@ -50,12 +50,15 @@ def test_validation_errors_without_gpu():
     from aoakv import _lib
     lib = _lib.load()
     nul = None
-    # unsupported head_dim is rejected before anything touches the device
-    rc = lib.aoakv_append_kv_cache_prefill(1, 1, 4, 1, 1, 1, 4, 1, 1, 1, 1, 32, 64, 16, 1, nul)
+    # unsupported head_dim (not 64 / 128 / 256) and page sizes (not 1..32) are
+    # rejected before anything touches the device
+    rc = lib.aoakv_append_kv_cache_prefill(1, 1, 4, 1, 1, 1, 4, 1, 1, 1, 1, 32, 96, 16, 1, nul)
     assert rc == _lib.AOAKV_ERR_UNSUPPORTED
     assert b"head_dim" in lib.aoakv_last_error()
-    rc = lib.aoakv_append_kv_cache_prefill(1, 1, 4, 1, 1, 1, 4, 1, 1, 1, 1, 32, 128, 8, 1, nul)
-    assert rc == _lib.AOAKV_ERR_UNSUPPORTED and b"page_size" in lib.aoakv_last_error()
+    for page_size in (0, 33, 64):
+        rc = lib.aoakv_append_kv_cache_prefill(1, 1, 4, 1, 1, 1, 4, 1, 1, 1, 1, 32, 128,
+                                               page_size, 1, nul)
+        assert rc == _lib.AOAKV_ERR_UNSUPPORTED and b"page_size" in lib.aoakv_last_error()
     rc = lib.aoakv_append_kv_cache_prefill(1, 1, 4, 1, 1, 1, 4, 1, 1, 1, 1, 32, 128, 16, 7, nul)
     assert rc == _lib.AOAKV_ERR_UNSUPPORTED and b"layout" in lib.aoakv_last_error()
     # null pointers
@@ -141,7 +144,7 @@ def test_rope_validation_without_gpu():
     from aoakv import _lib
     lib = _lib.load()
     nul = None
-    rc = lib.aoakv_apply_rope_in_place(1, 1, 4, 0, 32, 32, 64, 1.0, 1e4, nul)
+    rc = lib.aoakv_apply_rope_in_place(1, 1, 4, 0, 32, 32, 96, 1.0, 1e4, nul)
     assert rc == _lib.AOAKV_ERR_UNSUPPORTED and b"head_dim" in lib.aoakv_last_error()
     rc = lib.aoakv_apply_rope_in_place(1, 1, 4, 0, 32, 32, 128, 0.0, 1e4, nul)
     assert rc == _lib.AOAKV_ERR_INVALID and b"rope_scale" in lib.aoakv_last_error()

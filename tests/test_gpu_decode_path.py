@@ -533,14 +533,14 @@ def test_gqa_selection_and_decode(Hq, Hkv, L, budget):
 def test_errors_are_reported_not_crashed():
     """Bad arguments come back as AoakvError before any launch."""
     from aoakv import AoakvError, ops
-    kv = torch.zeros((4, 2, 8, 16, 64), dtype=torch.float16, device=DEV)   # head_dim 64
+    kv = torch.zeros((4, 2, 8, 16, 96), dtype=torch.float16, device=DEV)   # head_dim 96
     with pytest.raises(AoakvError, match="head_dim"):
-        ops.append_kv_cache_prefill(torch.zeros((3, 8, 64), dtype=torch.float16, device=DEV),
-                                    torch.zeros((3, 8, 64), dtype=torch.float16, device=DEV),
+        ops.append_kv_cache_prefill(torch.zeros((3, 8, 96), dtype=torch.float16, device=DEV),
+                                    torch.zeros((3, 8, 96), dtype=torch.float16, device=DEV),
                                     kv, torch.zeros(4, dtype=torch.int32, device=DEV), 1, 3,
                                     kv, torch.zeros(1, dtype=torch.int32, device=DEV),
                                     torch.zeros((4, 8), dtype=torch.float16, device=DEV),
-                                    torch.zeros((4, 8, 64), dtype=torch.float16, device=DEV),
+                                    torch.zeros((4, 8, 96), dtype=torch.float16, device=DEV),
                                     HND)
 
 
