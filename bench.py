@@ -89,6 +89,9 @@ def build_layers(n_layers, layout, dev):
             device=dev, dtype=torch.int32)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
+        # a spin kernel keeps the stream busy while the host submits the
+        # launch, so the events bracket the kernel and not the submit
+        torch.cuda._sleep(100000)
         e0.record()
         ops.append_kv_cache_prefill(k, v, kv[l], idx[l], P, S, meta[l], midx, lvn[l], vmean[l],
                                     layout)
@@ -198,6 +201,7 @@ def prefill_bench(dev, layout, L, reps=5):
     ops.prefill_with_paged_kv_cache(*args, o=o)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(100000)  # busy stream: the events bracket the launches, not the submit
     e0.record()
     for _ in range(reps):
         ops.prefill_with_paged_kv_cache(*args, o=o)
@@ -288,6 +292,7 @@ def ragged_batch_bench(dev, layout, reps=20):
         call()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(100000)  # busy stream: the events bracket the launches, not the submit
         e0.record()
         for _ in range(reps):
             call()
