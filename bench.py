@@ -304,6 +304,88 @@ def ragged_batch_bench(dev, layout, reps=20):
     return out
 
 
+def gqa_bench(dev, layout, n_layers=8, hq=32, hkv=8, launches=256):
+    """The GQA path (group-consistent selection, filter_util.py:351-368) at a
+    Llama-3-8B attention shape: 32 query heads over 8 kv heads x 128, the
+    config-2 context (32768 tokens, page 16) and budget (2048 tokens).
+    n_layers independent layers (1.1 GB, past the memory-side cache) are
+    replayed round-robin from a HIP graph, both decode paths; the one-launch
+    layer keeps its top-k workgroups here (self-selection needs one query
+    head per kv head).  Bytes are the unique ones a layer must read: every
+    page's metadata and value statistic for the 8 kv heads, the selected
+    pages' K/V once per kv head (its 4 query heads share them), q, o and the
+    selection."""
+    import torch
+    from aoakv import ops
+    Pm = math.ceil(P / S)
+    shape = (n_layers, P, 2, hkv, S, D) if layout == ops.HND else (n_layers, P, 2, S, hkv, D)
+    kv = torch.empty(shape, dtype=torch.float16, device=dev)
+    meta = torch.empty((n_layers, Pm) + shape[2:], dtype=torch.float16, device=dev)
+    lvn = torch.empty((n_layers, P, hkv), dtype=torch.float16, device=dev)
+    vmean = torch.empty((n_layers, P, hkv, D), dtype=torch.float16, device=dev)
+    idx = torch.empty((n_layers, P), dtype=torch.int32, device=dev)
+    midx = torch.arange(Pm, dtype=torch.int32, device=dev)
+    q = torch.empty((n_layers, 1, hq, D), dtype=torch.float16, device=dev)
+    for l in range(n_layers):
+        g = torch.Generator(device=dev).manual_seed(500 + l)
+        k = torch.randn((L, hkv, D), generator=g, device=dev, dtype=torch.float32)
+        ch = torch.randperm(D, generator=torch.Generator().manual_seed(600 + l))[:4].to(dev)
+        k[:, :, ch] *= 8.0
+        v = torch.randn((L, hkv, D), generator=g, device=dev, dtype=torch.float32).half()
+        q[l] = torch.randn((1, hq, D), generator=g, device=dev, dtype=torch.float32).half()
+        idx[l] = torch.randperm(P, generator=torch.Generator().manual_seed(700 + l)).to(
+            device=dev, dtype=torch.int32)
+        ops.append_kv_cache_prefill(k.half(), v, kv[l], idx[l], P, S, meta[l], midx, lvn[l],
+                                    vmean[l], layout)
+        del k, v
+    indptr = torch.tensor([0, P], dtype=torch.int32, device=dev)
+    mindptr = torch.tensor([0, Pm], dtype=torch.int32, device=dev)
+    lpl = torch.tensor([S], dtype=torch.int32, device=dev)
+    scores = torch.zeros((n_layers, 1, hkv, P), dtype=torch.float32, device=dev)
+    sel = torch.zeros((n_layers, 1, hkv, K_SEL), dtype=torch.int32, device=dev)
+    o = torch.zeros((n_layers, 1, hq, D), dtype=torch.float16, device=dev)
+    ws = ops.decode_workspace(1, hq, hkv, K_SEL, dev, max_pages=P)
+    nbytes = (hkv * P * (2 * D * 2 + 2) + hkv * K_SEL * S * D * 2 * 2 + hkv * K_SEL * 4 +
+              2 * hq * D * 2)
+    out = {"shape": f"{hq} query heads / {hkv} kv heads x {D}, {L} ctx, page {S}, budget {BUDGET}",
+           "bytes": int(nbytes), "layers_rotated": n_layers, "launches_timed": launches}
+    base = ops.FLAG_VALUE_AWARE | ops.FLAG_FIXED
+    results = {}
+    for name, flags in (("two_launch", base), ("one_launch", base | ops.FLAG_SINGLE_LAUNCH)):
+        def layer(l, flags=flags):
+            ops.sparse_decode_layer(q[l], o[l], kv[l], indptr, idx[l], lpl, meta[l], mindptr,
+                                    midx, lvn[l], scores[l], sel[l], BUDGET, ws, P, layout, flags)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for l in range(n_layers):
+                layer(l)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        results[name] = (o.clone(), sel.clone())
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for i in range(launches):
+                layer(i % n_layers)
+        gr.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(100000)  # busy stream: the events bracket the launches, not the submit
+        e0.record()
+        gr.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / launches
+        out[f"us_per_layer_{name}"] = round(us, 3)
+        out[f"GBps_{name}"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+        del gr
+    (o2, s2), (o1, s1) = results["two_launch"], results["one_launch"]
+    out["one_launch_equals_two_launch"] = bool(torch.equal(o1, o2) and torch.equal(s1, s2))
+    if ops.workspace_error(ws) != 0:
+        raise SystemExit(f"GQA layer: workspace error word {ops.workspace_error(ws)}")
+    return out
+
+
 def _threads() -> int:
     try:
         from threadpoolctl import threadpool_info
@@ -790,6 +872,8 @@ def main():
             extra[f"prefill_{Lp // 1024}k_mfma_frac"] = round(tf / 2500.0, 4)
         log("[bench] config 5 (ragged batch) ...")
         extra["config5_ragged_batch16"] = ragged_batch_bench(dev, layout)
+        log("[bench] GQA layer (32 / 8 heads) ...")
+        extra["gqa_32q_8kv_32k"] = gqa_bench(dev, layout)
         # the same 32 layers in the other cache layout (the reference's
         # drop-in layout is NHD): same seeds, so the same bits are expected
         other = ops.NHD if layout == ops.HND else ops.HND
