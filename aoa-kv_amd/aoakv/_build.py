@@ -26,7 +26,7 @@ LIB = os.path.join(PKG_DIR, "libaoakv.so")
 TIMELINE_LIB = os.path.join(PKG_DIR, "libaoakv_timeline.so")
 # build record beside the library (travels with it; the GPU box has no .git)
 BUILDINFO = os.path.join(PKG_DIR, "libaoakv.buildinfo.json")
-SOURCES = ["append.hip", "decode.hip", "prefill.hip", "generic.hip", "capi.cpp"]
+SOURCES = ["append.hip", "decode.hip", "prefill.hip", "generic.hip", "norm.hip", "capi.cpp"]
 REPO_DIR = os.path.dirname(os.path.dirname(PKG_DIR))
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -56,6 +56,7 @@ SIGNATURES = {
     "aoakv_prefill_with_paged_kv_cache": [_p, _p, _p, _p, _u32, _u32, _u32, _u32, _u32,
                                           _u32, _u32, _u32, _u32, _p],
     "aoakv_apply_rope_in_place": [_p, _p, _u32, _u32, _u32, _u32, _u32, _f32, _f32, _p],
+    "aoakv_rms_norm_forward": [_p, _p, _p, _u32, _u32, _f32, _p],
     "aoakv_rope_append_kv_cache_decode": [_p, _p, _p, _u32, _u32, _p, _p, _p, _p, _p, _p, _p,
                                           _p, _p, _u32, _u32, _u32, _u32, _f32, _f32, _p],
 }

@@ -14,8 +14,11 @@ run on libaoakv.so -- the package's own build, or the one the environment
 variable AOAKV_LIB names -- and the md5 of the library loaded goes into every
 row.  ``--method`` is the older spelling of the same choice.  Both use the
 simulation's selection unless ``--semantics quest_kernel`` asks for the
-reference kernels' convention.  Weights are random and seeded (no checkpoint
-is loaded; latency does not depend on weight values), inputs are random
+reference kernels' convention.  ``--graph`` replays each decode step's
+layers from a HIP graph (``QuestLlamaModel.decode_graphed``): at batch 1 the
+eager step is bound by its per-layer host dispatch.  Weights are random and
+seeded (no checkpoint is loaded; latency does not depend on weight values),
+inputs are random
 embeddings as in the reference driver, and timing uses events with a
 synchronize on both sides after ``--warmup`` discarded iterations.  The
 decode workspace's error word is read once per iteration (every step with
@@ -63,11 +66,16 @@ def parse_args(argv=None):
                         "recorded by rocprofv3 --marker-trace)")
     p.add_argument("--three_call", action="store_true",
                    help="decode with the reference's three calls instead of one launch")
+    p.add_argument("--graph", action="store_true",
+                   help="replay each decode step's layers from a HIP graph (the host planner "
+                        "runs eagerly before each replay; CSV method gets a _graph suffix)")
     p.add_argument("--out", default=None, help="CSV to append to (optional)")
     args = p.parse_args(argv)
     if args.kernel and args.method and KERNELS[args.kernel] != args.method:
         p.error(f"--kernel {args.kernel} and --method {args.method} disagree")
     args.method = KERNELS[args.kernel] if args.kernel else (args.method or "AOA_KV")
+    if args.graph and args.debug_checks:
+        p.error("--debug_checks synchronizes after every step; it cannot run inside --graph")
     return args
 
 
@@ -122,7 +130,7 @@ def main(argv=None):
                 x = torch.randn(1, 1, cfg.hidden_size, generator=g, dtype=dtype, device=device)
                 torch.cuda.synchronize()
                 start.record()
-                model(x)
+                model.decode_graphed(x) if args.graph else model(x)
                 end.record()
                 torch.cuda.synchronize()
                 if measured:
@@ -134,7 +142,8 @@ def main(argv=None):
             print(f"iteration {it} done ({'measured' if measured else 'warmup'})", flush=True)
 
     row = {
-        "method": args.method + ("" if args.semantics == "sim" else "_quest_kernel"),
+        "method": (args.method + ("" if args.semantics == "sim" else "_quest_kernel") +
+                   ("_graph" if args.graph else "")),
         "kernel_md5": md5, "gpu": gpu, "model": args.model, "context_len": args.context_len,
         "token_budget": args.token_budget, "page_size": args.page_size,
         "decode_len": args.decode_len, "iteration": args.iteration,

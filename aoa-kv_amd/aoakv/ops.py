@@ -108,6 +108,21 @@ def apply_rope_in_place(q, k, past_kv_len: int, rope_scale: float = 1.0,
               _stream())
 
 
+def rms_norm_forward(input, weight, output, epsilon: float):
+    """Reference: quest/ops/csrc/rms_norm.cu:185-213 (bsk_ops.h:29): RMSNorm of
+    input [..., n] fp16 (rows over the leading dims) with weight [n] into
+    output (input's shape; may be input itself)."""
+    _need(input, "input", torch.float16)
+    _need(weight, "weight", torch.float16)
+    _need(output, "output", torch.float16)
+    n = input.shape[-1]
+    if weight.shape != (n,) or output.shape != input.shape:
+        raise ValueError(f"weight must be [{n}] and output {tuple(input.shape)}, got "
+                         f"{tuple(weight.shape)} / {tuple(output.shape)}")
+    _lib.call("aoakv_rms_norm_forward", input.data_ptr(), weight.data_ptr(), output.data_ptr(),
+              input.numel() // n, n, float(epsilon), _stream())
+
+
 def rope_append_kv_cache_decode(q, k, v, kv_data, kv_indptr, kv_indices, kv_last_page_len,
                                 metadata_data, metadata_indptr, metadata_indices, v_log_norm,
                                 v_mean, layout: int, rope_scale: float = 1.0,

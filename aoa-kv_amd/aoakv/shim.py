@@ -6,8 +6,8 @@ Mirrors the reference's model integration: ``QuestAttention.forward``
 llama.py:424-486, 520-560), including the two leading layers that attend
 densely (``_quest_skip_layer = 2``).  There is no checkpoint here: weights
 are random (seeded), which is what a latency measurement needs; the shapes
-are the model's.  Projections, RMSNorm and the MLP are plain torch (hipBLASLt
-GEMMs); RoPE, the paged append, prefill and the decode layer are the
+are the model's.  Projections and the MLP are plain torch (hipBLASLt GEMMs);
+RMSNorm, RoPE, the paged append, prefill and the decode layer are the
 library's kernels.  Batch size 1, as the reference's QuestAttention.
 """
 from __future__ import annotations
@@ -45,15 +45,16 @@ MODEL_SHAPES = {
 
 
 class RMSNorm(nn.Module):
+    """The reference model's LlamaRMSNorm (quest/models/llama.py:62-72): one
+    launch of the library's rms_norm kernel (utils.rms_norm_forward)."""
+
     def __init__(self, n: int, eps: float):
         super().__init__()
         self.weight = nn.Parameter(torch.ones(n))
         self.eps = eps
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        xf = x.float()
-        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
-        return self.weight * xf.to(x.dtype)
+        return qutils.rms_norm_forward(x, self.weight, self.eps)
 
 
 class QuestAttention(nn.Module):
@@ -186,6 +187,7 @@ class QuestLlamaModel(nn.Module):
         """Frees the sequence's pages for a new conversation (llama.py:554-560)."""
         assert self.iController is not None, "Must be called after init."
         self.iController.clean_states()
+        self.drop_graph()
 
     @torch.no_grad()
     def forward(self, inputs_embeds: torch.Tensor) -> torch.Tensor:
@@ -196,13 +198,77 @@ class QuestLlamaModel(nn.Module):
         if self._skip > 0:
             c.set_page_budget(self._max_page_limit)
             c.begin_forward(seq_len)
-        h = inputs_embeds
+        return self._layers(inputs_embeds, seq_len, tables_written=self._skip > 0)
+
+    def _layers(self, h: torch.Tensor, seq_len: int, tables_written: bool) -> torch.Tensor:
+        """The decoder layers and the final norm, switching to the page budget
+        after the dense layers (llama.py:465-475).  Past the first
+        begin_forward (which writes the device page tables) the controller
+        calls here change host state only."""
+        c = self.iController
         for idx, layer in enumerate(self.layers):
             if idx == self._skip:
                 c.end_forward()
                 c.set_page_budget(self._page_budget)
-                c.begin_forward(seq_len, updateTensor=(idx == 0))
+                c.begin_forward(seq_len, updateTensor=(idx == 0 and not tables_written))
             with tr.range(f"layer={idx}"):  # llama.py:465-475
                 h = layer(h, c)
         c.end_forward()
         return self.norm(h)
+
+    @torch.no_grad()
+    def decode_graphed(self, inputs_embeds: torch.Tensor) -> torch.Tensor:
+        """One decode step (inputs_embeds [1, 1, hidden]) with the layers
+        replayed from a HIP graph: the host planner runs first (it writes the
+        device page tables: new page ids, page counts, the last page's length),
+        then one replay launches every kernel of the step, instead of the
+        dozens of host dispatches per layer of ``forward``.  The kernels take
+        the token's position, page table and page count from those device
+        tables; inside the graph the host passes them the cache's capacity as
+        the page bound (``static_page_bound``), so the only argument that
+        changes over a generation is whether the sparse layers select at all
+        (the sequence outgrew the page budget), and the graph is captured
+        again when it does.  The returned tensor is the graph's output
+        buffer, overwritten by the next step.  Same results as ``forward``
+        (the page bound sizes grids only)."""
+        c = self.iController
+        assert c is not None, "Please init Quest Controller first."
+        assert tuple(inputs_embeds.shape[:2]) == (1, 1), "one token per decode step"
+        assert not c.debug_checks, "debug_checks synchronize; not inside a graph"
+        if not getattr(self, "_graph_warm", False):
+            # the first single-token step runs eagerly: the GEMM libraries set
+            # up their single-row paths on first use, which a capture cannot do
+            self._graph_warm = True
+            return self.forward(inputs_embeds)
+        c.prepare_metadata(1)
+        c.set_page_budget(self._max_page_limit if self._skip > 0 else self._page_budget)
+        c.begin_forward(1)
+        key = len(c.kv_cache.indicies) > self._page_budget  # the sparse layers select
+        if getattr(self, "_graph_key", None) != key:
+            # the previous graph and its memory pool go first (each capture
+            # has a pool of its own)
+            self._graph, self._graph_out = None, None
+            if getattr(self, "_graph_in", None) is None:
+                self._graph_in = torch.empty_like(inputs_embeds)
+            self._graph_in.copy_(inputs_embeds)
+            g = torch.cuda.CUDAGraph()
+            c.static_page_bound = True
+            try:
+                with torch.cuda.graph(g):
+                    self._graph_out = self._layers(self._graph_in, 1, tables_written=True)
+            finally:
+                c.static_page_bound = False
+            self._graph, self._graph_key = g, key
+        else:
+            self._graph_in.copy_(inputs_embeds)
+            # the host state forward leaves behind (page budget, selection view)
+            c.end_forward()
+            c.set_page_budget(self._page_budget)
+            c.begin_forward(1, updateTensor=False)
+        self._graph.replay()
+        return self._graph_out
+
+    def drop_graph(self):
+        """Forget the captured decode step (quest_clear does, for a new
+        conversation)."""
+        self._graph, self._graph_out, self._graph_key = None, None, None

@@ -53,14 +53,13 @@ def apply_rope_in_place(q: torch.Tensor, k: torch.Tensor, past_kv_len: int,
 
 
 def rms_norm_forward(input: torch.Tensor, weight: torch.Tensor, epsilon: float) -> torch.Tensor:
-    """RMSNorm of the last dim (reference __init__.py:54-67, which calls the
-    rms_norm kernel of ops/csrc/rms_norm.cu): s = 1/sqrt(mean(x^2) + eps) in
-    fp32 over the fp32 values of x, then x * s * weight in fp32, rounded once
-    to x's dtype.  RMSNorm is outside the decode path, so this is torch on
-    the GPU (hipBLASLt / elementwise), not a libaoakv kernel."""
-    xf = input.float()
-    s = torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + epsilon)
-    return (xf * s * weight.float()).to(input.dtype)
+    """RMSNorm of the last dim (reference __init__.py:54-67): libaoakv's
+    rms_norm kernel (aoakv_rms_norm_forward), r = 1/sqrt(sum(x^2)/n + eps) in
+    fp32 over the fp32 values of x, then (x * r) * weight in fp32, rounded
+    once to fp16.  A new output tensor, as the reference returns."""
+    o = torch.empty_like(input)
+    ops.rms_norm_forward(input.contiguous(), weight.contiguous(), o, epsilon)
+    return o
 
 
 def rope_append_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
@@ -124,8 +123,8 @@ def decode_estimate(q: torch.Tensor, iController: InferenceController, layer_idx
     ops.estimate_attn_score(
         q.view(1, c.num_heads, c.head_dim), c.scores, c.metadata_cache.buf_layer(layer_idx),
         c.metadata_indptr_for_append, c.metadata_indices, c.kv_indptr_for_append,
-        c.kv_indices_with_last, c.kv_last_page_len_t, c.v_log_norm_layer(layer_idx), P,
-        c.layout, c.flags)
+        c.kv_indices_with_last, c.kv_last_page_len_t, c.v_log_norm_layer(layer_idx),
+        c.decode_max_pages, c.layout, c.flags)
     return c.scores[0, :, :P - 1 if c.quest_kernel else P]
 
 
@@ -166,7 +165,7 @@ def decode_sparse_attn(q: torch.Tensor, iController: InferenceController, layer_
     o = torch.empty_like(q3)
     ops.decode_sparse_attn(
         q3, o, c.kv_cache.buf_layer(layer_idx), c.kv_indptr_for_append, c.kv_indices_with_last,
-        c.kv_last_page_len_t, sel, c.token_budget, c.workspace, len(c.kv_cache.indicies),
+        c.kv_last_page_len_t, sel, c.token_budget, c.workspace, c.decode_max_pages,
         c.num_kv_heads, c.layout, flags=c.flags & ops.FLAG_QUEST_KERNEL)
     return o.view_as(q)
 
@@ -185,7 +184,7 @@ def decode_layer(q: torch.Tensor, iController: InferenceController, layer_idx: i
         q3, o, c.kv_cache.buf_layer(layer_idx), c.kv_indptr_for_append, c.kv_indices_with_last,
         c.kv_last_page_len_t, c.metadata_cache.buf_layer(layer_idx),
         c.metadata_indptr_for_append, c.metadata_indices, c.v_log_norm_layer(layer_idx),
-        c.scores, c._sel, c.token_budget, c.workspace, len(c.kv_cache.indicies), c.layout,
+        c.scores, c._sel, c.token_budget, c.workspace, c.decode_max_pages, c.layout,
         c.flags | (ops.FLAG_SINGLE_LAUNCH if single_launch else 0))
     if c.debug_checks:
         c.check_errors()

@@ -106,6 +106,10 @@ class InferenceController:
         # check the workspace error word after every fused decode layer call
         # (synchronizes: for debugging; check_errors() once per token is cheap)
         self.debug_checks = False
+        # decode calls size their grids for the cache's capacity instead of
+        # the current page count (a graph replayed over many steps; the
+        # kernels read the page count from the device tables either way)
+        self.static_page_bound = False
 
     # ------------------------------------------------------------ budget
     @property
@@ -193,6 +197,12 @@ class InferenceController:
             self._kv_without_last = self._kv_ids[:max(P - 1, 0)].unsqueeze(0).expand(
                 self.num_heads, max(P - 1, 0))
         return self._kv_without_last
+
+    @property
+    def decode_max_pages(self) -> int:
+        """The page-count bound the decode calls pass by value: the current
+        page count, or the capacity with ``static_page_bound``."""
+        return self.max_kv_pages if self.static_page_bound else len(self.kv_cache.indicies)
 
     def need_estimate(self) -> bool:
         """True when the sequence has more pages than the page budget."""

@@ -104,6 +104,28 @@ int check_flags(uint32_t flags, uint32_t allowed, const char* fn) {
 // quest_kernel convention selects k - 1 >= 0 pages besides the last.
 uint32_t min_sel_stride(uint32_t flags) { return (flags & AOAKV_FLAG_QUEST_KERNEL) ? 1u : 3u; }
 
+// Pages one head attends at most: every page (dense), else the selection row
+// (plus the last page with the quest_kernel convention), and with one token
+// budget for every sequence no more than that budget selects at any length
+// (num_selected_pages is monotone in the length and the page count).  The
+// decode grid, its workspace regions and the one-launch selection handoff
+// rows are sized by it, so a caller's selection buffer wider than the budget
+// (one row per page of the cache) costs no idle workgroups.
+uint32_t max_selected(const int32_t* sel_pages, uint32_t sel_stride, uint32_t token_budget,
+                      const int32_t* token_budgets, uint32_t max_pages, uint32_t page_size,
+                      uint32_t flags) {
+  if (!sel_pages) return max_pages;
+  const bool quest = (flags & AOAKV_FLAG_QUEST_KERNEL) != 0u;
+  const uint32_t row = sel_stride + (quest ? 1u : 0u);
+  uint32_t m = row < max_pages ? row : max_pages;
+  if (!token_budgets) {
+    const uint32_t k = aoakv::num_selected_pages(0xFFFFFFFFu, token_budget, page_size, max_pages,
+                                                 quest ? aoakv::kFlagQuestKernel : 0u);
+    m = k < m ? k : m;
+  }
+  return m;
+}
+
 int check_group(uint32_t hq, uint32_t hkv) {
   if (hkv == 0u || hq % hkv != 0u)
     return fail(AOAKV_ERR_INVALID, "num_qo_heads %u not a multiple of num_kv_heads %u", hq, hkv);
@@ -323,6 +345,23 @@ static int check_rope(float rope_scale, float rope_theta, const char* fn) {
   return AOAKV_OK;
 }
 
+int aoakv_rms_norm_forward(const void* x, const void* w, void* out, uint32_t rows, uint32_t n,
+                           float epsilon, void* stream) {
+  REQUIRE(x && w && out, "rms_norm_forward: null pointer argument");
+  REQUIRE(rows >= 1u, "rms_norm_forward: rows must be >= 1");
+  REQUIRE(n >= 8u && n <= 65536u && n % 8u == 0u,
+          "rms_norm_forward: n = %u must be a multiple of 8 in [8, 65536]", n);
+  REQUIRE(epsilon >= 0.f, "rms_norm_forward: epsilon must be >= 0");
+  aoakv::RmsNormArgs a{};
+  a.x = static_cast<const aoakv::f16*>(x);
+  a.w = static_cast<const aoakv::f16*>(w);
+  a.out = static_cast<aoakv::f16*>(out);
+  a.n = n;
+  a.eps = epsilon;
+  return hip_status(aoakv::launch_rms_norm(a, rows, static_cast<hipStream_t>(stream)),
+                    "rms_norm_forward");
+}
+
 int aoakv_apply_rope_in_place(void* q, void* k, uint32_t seq_len, uint32_t past_kv_len,
                               uint32_t num_qo_heads, uint32_t num_kv_heads, uint32_t head_dim,
                               float rope_scale, float rope_theta, void* stream) {
@@ -539,11 +578,8 @@ static int fill_decode(aoakv::DecodeArgs& a, Workspace& w, const void* q, void* 
   REQUIRE(batch_size >= 1u && batch_size <= 65535u, "decode_sparse_attn: bad batch_size %u",
           batch_size);
   REQUIRE(max_pages >= 1u, "decode_sparse_attn: max_pages must be >= 1");
-  const bool quest = (flags & AOAKV_FLAG_QUEST_KERNEL) != 0u;
-  // pages attended per head: the selection row (plus the last page with the
-  // quest_kernel convention), at most every page
-  const uint32_t row = sel_stride + (quest ? 1u : 0u);
-  const uint32_t max_sel = sel_pages ? (row < max_pages ? row : max_pages) : max_pages;
+  const uint32_t max_sel = max_selected(sel_pages, sel_stride, token_budget, token_budgets,
+                                        max_pages, page_size, flags);
   REQUIRE(!sel_pages || sel_stride >= min_sel_stride(flags), "decode_sparse_attn: sel_stride %u < %u",
           sel_stride, min_sel_stride(flags));
   REQUIRE(aoakv::decode_chunks(max_sel) <= aoakv::decode_max_chunks(),
@@ -640,7 +676,11 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
     la.e.token_budget = token_budget;
     la.e.token_budgets = token_budgets;
     la.e.counters = w.est_counters;
-    const uint32_t max_sel = sel_stride < max_pages ? sel_stride : max_pages;
+    // handoff rows of the selection entries (the quest_kernel convention's
+    // last page is not among them)
+    const uint32_t sel_cap = max_selected(sel_pages, sel_stride, token_budget, token_budgets,
+                                          max_pages, page_size, flags);
+    const uint32_t max_sel = sel_cap < sel_stride ? sel_cap : sel_stride;
     la.e.hsel = w.hsel;
     la.e.hsel_stride = max_sel;
     la.d = da;
@@ -691,8 +731,8 @@ int aoakv_sparse_decode_layer_noalloc(
           "sparse_decode_layer_noalloc: runs the two-launch path only (AOAKV_FLAG_SINGLE_LAUNCH "
           "needs a workspace the caller can re-initialise after a wait gave up)");
   // the decode workspace this call lays out must fit the scratch array
-  const uint32_t row = sel_stride + ((flags & AOAKV_FLAG_QUEST_KERNEL) ? 1u : 0u);
-  const uint32_t max_sel = row < max_pages ? row : max_pages;
+  const uint32_t max_sel = max_selected(sel_pages, sel_stride, token_budget, token_budgets,
+                                        max_pages, page_size, flags);
   const size_t need = ws_layout(batch_size, num_qo_heads, num_kv_heads, max_sel, nullptr, nullptr);
   REQUIRE(need <= kNoAllocScratchBytes,
           "sparse_decode_layer_noalloc: this call needs %zu bytes of scratch, more than the "

@@ -192,6 +192,16 @@ uint32_t est_chunks(uint32_t max_pages);
 hipError_t launch_decode(const DecodeArgs& a, uint32_t batch, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s);
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t s);
+
+// RMSNorm of `rows` fp16 rows of n elements (n a multiple of 8), one weight row.
+struct RmsNormArgs {
+  const f16* x;
+  const f16* w;
+  f16* out;
+  uint32_t n;
+  float eps;
+};
+hipError_t launch_rms_norm(const RmsNormArgs& a, uint32_t rows, hipStream_t s);
 uint32_t decode_chunks(uint32_t max_sel_pages);
 uint32_t partial_stride();
 uint32_t decode_max_chunks();  // split-K chunks per head the merge holds

@@ -15,6 +15,7 @@
  *     .begin/forward/end_forward    aoakv_decode_sparse_attn
  *   prefill_with_paged_kv_cache  -> aoakv_prefill_with_paged_kv_cache
  *   apply_rope_in_place          -> aoakv_apply_rope_in_place
+ *   rms_norm_forward             -> aoakv_rms_norm_forward
  *
  * plus fused entry points: aoakv_sparse_decode_layer (estimate + top-k +
  * sparse decode for one layer), aoakv_estimate_topk, and
@@ -171,6 +172,17 @@ int aoakv_append_kv_cache_decode(const void* k, const void* v, uint32_t batch_si
 int aoakv_apply_rope_in_place(void* q, void* k, uint32_t seq_len, uint32_t past_kv_len,
                               uint32_t num_qo_heads, uint32_t num_kv_heads, uint32_t head_dim,
                               float rope_scale, float rope_theta, void* stream);
+
+/*
+ * RMSNorm of x [rows, n] (fp16, row-major) with weight w [n] into out [rows,
+ * n]: out = fp16((x * r) * w), r = 1 / sqrt(sum(x^2) / n + epsilon), x and w
+ * widened to fp32 and the sum in fp32.  Replaces rms_norm_forward (reference
+ * bsk_ops.h:29, rms_norm.cu:76-213, quest/utils/__init__.py:54-67; the
+ * reference model's LlamaRMSNorm, quest/models/llama.py:62-72).
+ * n a multiple of 8, 8 <= n <= 65536; rows >= 1.  out may alias x.
+ */
+int aoakv_rms_norm_forward(const void* x, const void* w, void* out, uint32_t rows, uint32_t n,
+                           float epsilon, void* stream);
 
 /*
  * The decode step's RoPE and append in one launch: aoakv_apply_rope_in_place

@@ -515,6 +515,27 @@ def apply_rope(x: np.ndarray, positions: np.ndarray, rope_scale: float = 1.0,
 
 
 # --------------------------------------------------------------------------
+# RMSNorm (the model's norm, outside the decode layer)
+# --------------------------------------------------------------------------
+
+def rms_norm_forward(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """The reference's rms_norm_forward kernel (quest/ops/csrc/rms_norm.cu:
+    76-159, ``rmsnorm_twoPassAlgo_e8``): per row, s = sum of the fp32 squares
+    (fp32), r = 1/sqrt(s / n + eps), out = fp16((x * r) * w) with each
+    product in fp32.  The kernel sums in a thread/warp tree; here the row is
+    summed in float64 and rounded to fp32 once (the two differ by a few fp32
+    ulps of s, far below one fp16 ulp of the output), and r is the correctly
+    rounded fp32 reciprocal square root.
+
+    x (..., n) fp16, w (n,) fp16; returns fp16 of x's shape."""
+    xf = x.astype(np.float32)
+    s = (xf.astype(np.float64) ** 2).sum(axis=-1, keepdims=True).astype(np.float32)
+    u = (s / np.float32(x.shape[-1])).astype(np.float32) + np.float32(eps)   # fp32 ops
+    r = (1.0 / np.sqrt(u.astype(np.float64))).astype(np.float32)
+    return ((xf * r).astype(np.float32) * w.astype(np.float32)).astype(np.float16)
+
+
+# --------------------------------------------------------------------------
 # Dense causal prefill (textbook; quest/tests/test_prefill_attention.py:17-44,
 # kernels/src/include/cpu_reference.h:56-159)
 # --------------------------------------------------------------------------

@@ -178,7 +178,9 @@ def test_noalloc_entry_point_rejects_without_gpu():
     from aoakv import _lib
     lib = _lib.load()
     p = 1  # never dereferenced: the calls are rejected first
-    args = [p] * 11 + [16384, p, 8192, 256, None, 1, 16384, 32, 8, 128, 16, 1]
+    # a budget of 131072 tokens selects 8192 pages per head (the selection
+    # row's width): 32 heads x 8192 pages need more than the scratch array
+    args = [p] * 11 + [16384, p, 8192, 131072, None, 1, 16384, 32, 8, 128, 16, 1]
     rc = lib.aoakv_sparse_decode_layer_noalloc(*args, _lib.FLAG_SINGLE_LAUNCH, None)
     assert rc == _lib.AOAKV_ERR_INVALID and b"two-launch" in lib.aoakv_last_error()
     rc = lib.aoakv_sparse_decode_layer_noalloc(*args, _lib.FLAG_VALUE_AWARE, None)

@@ -15,6 +15,7 @@ latency/bench_latency.py:125-168.  CPU only: nothing here launches a kernel.
 import inspect
 
 import pytest
+import torch
 
 torch = pytest.importorskip("torch")
 import aoakv  # noqa: E402
@@ -94,18 +95,34 @@ def test_controller_exposes_the_reference_attributes():
         assert f"self.{attr}" in src or isinstance(getattr(cls, attr, None), property), attr
 
 
-def test_rms_norm_forward_matches_fp32_formula_on_cpu():
-    # reference rms_norm.cu: fp32 sum of squares, rsqrt(mean + eps), x * s * w
-    # in fp32, one rounding to the input dtype
-    g = torch.Generator().manual_seed(0)
-    x = torch.randn(3, 4096, generator=g).half()
-    w = (torch.rand(4096, generator=g) + 0.5).half()
-    out = qutils.rms_norm_forward(x, w, 1e-5)
-    assert out.dtype == torch.float16 and out.shape == x.shape
-    xd = x.double()
-    ref = xd / torch.sqrt(xd.pow(2).mean(-1, keepdim=True) + 1e-5) * w.double()
+def test_rms_norm_oracle_is_pinned_by_the_formula():
+    """The oracle's rms_norm_forward (the reference kernel rms_norm.cu:76-159:
+    fp32 sum of squares, 1/sqrt(mean + eps), (x * r) * w in fp32, one fp16
+    rounding) against the float64 formula, and by its invariances: a dropped
+    eps, a sum for the mean or a missing weight fails these."""
+    import numpy as np
+    from oracle import sim
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((3, 4096)).astype(np.float16)
+    w = (rng.random(4096) + 0.5).astype(np.float16)
+    out = sim.rms_norm_forward(x, w, 1e-5)
+    assert out.dtype == np.float16 and out.shape == x.shape
+    xd = x.astype(np.float64)
+    ref = xd / np.sqrt((xd ** 2).mean(-1, keepdims=True) + 1e-5) * w.astype(np.float64)
     # one fp16 rounding of a value computed in fp32
-    assert torch.allclose(out.double(), ref, rtol=2e-3, atol=1e-3)
-    # a row scaled by c normalises to the same output (scale invariance)
-    out2 = qutils.rms_norm_forward((x.float() * 2.0).half(), w, 0.0)
-    assert torch.equal(out2, qutils.rms_norm_forward(x, w, 0.0))
+    np.testing.assert_allclose(out.astype(np.float64), ref, rtol=2e-3, atol=1e-3)
+    # a row scaled by 2 normalises to the same output (eps 0), eps matters
+    # where the mean square is small
+    assert np.array_equal(sim.rms_norm_forward((x.astype(np.float32) * 2).astype(np.float16),
+                                               w, 0.0), sim.rms_norm_forward(x, w, 0.0))
+    tiny = (x.astype(np.float32) * 1e-3).astype(np.float16)
+    assert not np.allclose(sim.rms_norm_forward(tiny, w, 1e-2).astype(np.float32),
+                           sim.rms_norm_forward(tiny, w, 0.0).astype(np.float32), rtol=0.1)
+
+
+def test_rms_norm_forward_refuses_host_tensors():
+    """The drop-in rms_norm_forward runs the library kernel: host tensors are
+    refused, not computed on the CPU."""
+    x = torch.zeros(2, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="device tensor"):
+        qutils.rms_norm_forward(x, torch.ones(64, dtype=torch.float16), 1e-6)

@@ -158,3 +158,28 @@ def test_quest_kernel_semantics_and_plain_quest_run():
         outs.append(torch.cat([t[:, -1] for t in o[1:]]))
     # different selection rules attend different pages
     assert not torch.equal(outs[0], outs[1]) and not torch.equal(outs[0], outs[2])
+
+
+@pytest.mark.parametrize("heads,kv_heads,single_launch", [(2, 2, True), (4, 2, True), (2, 2, False)])
+def test_graphed_decode_equals_forward(heads, kv_heads, single_launch):
+    """decode_graphed (the layers replayed from a HIP graph, the grids sized
+    for the cache's capacity, captured again when the sparse layers start
+    selecting) gives the bits of the eager forward at every step: a prefill
+    below the budget, then decode steps that cross five page boundaries and
+    the budget, then a second conversation after quest_clear.  Every replay
+    is checked, with the planner's eager work and the other model's launches
+    between replays."""
+    _say(f"[shim-graph] heads={heads} kv={kv_heads} single_launch={single_launch}")
+    cfg = _cfg(128 * heads, heads, kv_heads, layers=4)
+    eager, graphed = (_make(cfg, single_launch=single_launch, budget=64) for _ in range(2))
+    g = torch.Generator(device=DEV).manual_seed(8)
+    for conv, (n0, steps) in enumerate([(40, 70), (150, 20)]):
+        for step, n in enumerate([n0] + [1] * steps):
+            x = torch.randn(1, n, cfg.hidden_size, generator=g, device=DEV).half()
+            with torch.inference_mode():
+                want = eager(x)
+                got = graphed(x) if n > 1 else graphed.decode_graphed(x)
+            assert torch.equal(got, want), (conv, step)
+        for mm in (eager, graphed):
+            assert int(mm.iController.workspace[8:12].view(torch.int32).item()) == 0
+            mm.quest_clear()

@@ -81,10 +81,11 @@ def test_noalloc_layer_rejects_single_launch_and_oversized_calls():
     with pytest.raises(AoakvError, match="two-launch"):
         ops.sparse_decode_layer_noalloc(*args, P, HND,
                                         ops.FLAG_VALUE_AWARE | ops.FLAG_SINGLE_LAUNCH)
-    # 32 query heads x 8192 selected pages: a decode workspace of ~35 MB
+    # 32 query heads x 8192 selected pages (a budget of 131072 tokens fills
+    # the 8192-wide selection rows): a decode workspace of ~35 MB
     q32 = torch.zeros((1, 32, D), dtype=torch.float16, device=DEV)
     big_sel = torch.zeros((1, 8, 8192), dtype=torch.int32, device=DEV)
     big_scores = torch.zeros((1, 8, 16384), dtype=torch.float32, device=DEV)
-    big = (q32, torch.empty_like(q32)) + args[2:10] + (big_scores, big_sel, 256)
+    big = (q32, torch.empty_like(q32)) + args[2:10] + (big_scores, big_sel, 131072)
     with pytest.raises(AoakvError, match="scratch"):
         ops.sparse_decode_layer_noalloc(*big, 16384, HND, ops.FLAG_VALUE_AWARE)
