@@ -7,8 +7,10 @@ pages per head; keys N(0,1) with 4 of 128 channels x8, values N(0,1).  A
 step is one layer's sparse decode: value-aware page scores of all 2048 pages,
 per-head top-k, split-K attention over the selected pages.  The 32 layers
 (2.15 GB of cache+metadata touched per pass, far above the 256 MB MALL) are
-visited round-robin; the 32 launches of a pass (one per layer) are captured
-in a HIP graph and replayed, as a decode loop would run them.  The
+visited round-robin.  The timed steps are submitted while a spin kernel holds
+the stream, so the events around them bracket exactly the --steps kernels,
+back to back; the same steps replayed from one HIP graph are reported beside
+(a replay adds a start-up of about 7.5 us before its first kernel).  The
 two-launch path (scores + top-k, then decode) is timed beside it and must
 give the same bits.
 
@@ -805,6 +807,29 @@ def main():
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e3 / n
 
+    def queued_timed(fn, n):
+        """us per launch over n launches fn(i % n_layers) queued behind a spin
+        kernel: the host submits all n while the GPU spins, so the events
+        (recorded between the spin and the first launch, and after the last)
+        bracket n back-to-back kernels with no host gap and no graph-launch
+        start-up (a replayed graph spends about 7.5 us before its first
+        kernel).  Synchronized on both sides.  Returns (us, host submit ms,
+        spin ms): the figure holds when the submit took less than the spin."""
+        es, e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        # >= 100 us of spin per launch at 2.5 GHz (a launch takes 20-60 us to submit)
+        spin_cycles = max(2_000_000, 250_000 * n)
+        torch.cuda.synchronize()
+        es.record()
+        torch.cuda._sleep(spin_cycles)
+        t0 = time.perf_counter()
+        e0.record()
+        for i in range(n):
+            fn(i % n_layers)
+        e1.record()
+        submit_ms = (time.perf_counter() - t0) * 1e3
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / n, submit_ms, es.elapsed_time(e0)
+
     # two launches per layer (scores + top-k, then decode): the reference's
     # split, timed beside the measured path and the source of the equality check
     g2 = capture(layer2, n_aux)
@@ -826,13 +851,28 @@ def main():
         del gw
     o.zero_()
     sel.zero_()
-    log(f"[bench] timing {steps} layers (one graph of {steps} one-launch layers) ...")
-    us_one = replay_timed(g1, steps)
-    # every layer of the rotation ran at least once in the timed graph when
-    # steps >= 32; the layers it reached must equal the two-launch results
+    log(f"[bench] timing {steps} layers (one-launch layers queued behind a spin kernel) ...")
+    us_queued, submit_ms, spin_ms = queued_timed(layer1, steps)
+    # every layer of the rotation ran at least once in the timed launches when
+    # steps >= 32; the layers they reached must equal the two-launch results
     reached = min(steps, n_layers)
     one_exact = bool(torch.equal(o[:reached], o_eager[:reached]) and
                      torch.equal(sel[:reached], sel_eager[:reached]))
+    # the same launches replayed from one graph (with its start-up)
+    o.zero_()
+    sel.zero_()
+    log(f"[bench] timing {steps} layers (one graph of {steps} one-launch layers) ...")
+    us_graph = replay_timed(g1, steps)
+    one_exact = one_exact and bool(torch.equal(o[:reached], o_eager[:reached]) and
+                                   torch.equal(sel[:reached], sel_eager[:reached]))
+    # the queued figure holds only if the host submitted every launch before
+    # the spin ended (long runs fill the hardware queue, and the submit then
+    # waits on the GPU); otherwise the graph replay is the figure, its
+    # start-up spread over the steps
+    queued_ok = submit_ms < spin_ms
+    us_one = us_queued if queued_ok else us_graph
+    timing = ("launches queued behind a spin kernel, events around them" if queued_ok else
+              "one HIP graph of the launches, events around its replay")
     err_word = ops.workspace_error(ws)
     if err_word != 0 or not one_exact:
         raise SystemExit(f"single-launch layer failed: workspace error word {err_word}, "
@@ -929,10 +969,12 @@ def main():
                                "2048 pages + per-head top-128 + split-K attention), 32 heads x "
                                "128, 32768 ctx, page 16, budget 2048, 32 rotated layers",
                    "layout": args.layout.upper(), "launches_per_layer": 1,
-                   "hip_graph": True},
+                   "timing": timing},
         "layer_GBps": round(LAYER_BYTES / (us_layer * 1e-6) / 1e9, 1),
         "layer_bytes": LAYER_BYTES,
         "layer_hbm_frac": round(LAYER_BYTES / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "queued_us_per_layer": round(us_queued, 3), "queued_submit_ms": round(submit_ms, 2),
+        "queued_spin_ms": round(spin_ms, 2), "graph_us_per_layer": round(us_graph, 3),
         "two_launch_us_per_layer": round(us_two, 3),
         "two_launch_kernel_us": {"estimate_topk": round(us_est, 3), "decode": round(us_dec, 3)},
         "graph_replay_exact": replay_exact,
