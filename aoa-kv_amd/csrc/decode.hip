@@ -1189,19 +1189,17 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
     const uint32_t ng = nm - g0 < 16u ? nm - g0 : 16u;
     const size_t gb = base + (size_t)g0 * kPartialStride;
     // unconditional loads of clamped chunk indices, masked after
-    uint32_t mw[16], lw[16], ow[8];
+    // the group's m and l words, one per lane (lane c % 32: m of chunk c for
+    // c < 16, l of chunk c - 16 above; lanes 32-63 repeat lanes 0-31) and read
+    // out with readlane: one load per wave instead of one per word
+    const uint32_t mlc = lane % 16u, mll = (lane / 16u) % 2u;
+    uint32_t mlw, ow[8];
     auto load_group = [&]() {
-#pragma unroll
-      for (int c = 0; c < 16; ++c) {
-        const uint32_t cc = (uint32_t)c < ng ? (uint32_t)c : ng - 1u;
-        const size_t at = gb + cc * kPartialStride + kHeadDim;
-        if (HANDOFF) {
-          mw[c] = ld_agent_u32(a.hpart + at);
-          lw[c] = ld_agent_u32(a.hpart + at + 1);
-        } else {
-          mw[c] = __builtin_bit_cast(uint32_t, ld_agent(a.partial + at));
-          lw[c] = __builtin_bit_cast(uint32_t, ld_agent(a.partial + at + 1));
-        }
+      {
+        const uint32_t cc = mlc < ng ? mlc : ng - 1u;
+        const size_t at = gb + cc * kPartialStride + kHeadDim + mll;
+        mlw = HANDOFF ? ld_agent_u32(a.hpart + at)
+                      : __builtin_bit_cast(uint32_t, ld_agent(a.partial + at));
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -1213,14 +1211,13 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
     };
     load_group();
     if (HANDOFF) {
-      // re-poll until every word of the group is written, then decode
+      // re-poll (the whole wave) until every word of the group it uses is
+      // written, then decode
       auto missing = [&]() {
-        bool z = false;
-#pragma unroll
-        for (int c = 0; c < 16; ++c) z |= (uint32_t)c < ng && (mw[c] == 0u || lw[c] == 0u);
+        bool z = mlc < ng && mlw == 0u;
 #pragma unroll
         for (int i = 0; i < 8; ++i) z |= half + 2u * i < ng && ow[i] == 0u;
-        return z;
+        return __builtin_amdgcn_ballot_w64(z) != 0u;
       };
       uint32_t it = 0u;
       while (missing()) {
@@ -1232,19 +1229,17 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
         load_group();
       }
       TL(kTlMergeLoaded);
-#pragma unroll
-      for (int c = 0; c < 16; ++c) {
-        mw[c] -= 1u;
-        lw[c] -= 1u;
-      }
+      mlw -= 1u;
 #pragma unroll
       for (int i = 0; i < 8; ++i) ow[i] -= 1u;
     }
     float mv[16], lv[16], ov[8];
 #pragma unroll
     for (int c = 0; c < 16; ++c) {
-      mv[c] = (uint32_t)c < ng ? __builtin_bit_cast(float, mw[c]) : -INFINITY;
-      lv[c] = (uint32_t)c < ng ? __builtin_bit_cast(float, lw[c]) : 0.f;
+      const float m_c = __builtin_bit_cast(float, __builtin_amdgcn_readlane((int)mlw, c));
+      const float l_c = __builtin_bit_cast(float, __builtin_amdgcn_readlane((int)mlw, 16 + c));
+      mv[c] = (uint32_t)c < ng ? m_c : -INFINITY;
+      lv[c] = (uint32_t)c < ng ? l_c : 0.f;
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) ov[i] = half + 2u * i < ng ? __builtin_bit_cast(float, ow[i]) : 0.f;
