@@ -1255,7 +1255,12 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
       Lsum = Lsum + mv[c] * lv[c];
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc = acc + mv[half + 2 * i] * ov[i];
+    for (int i = 0; i < 8; ++i) {
+      // chunk half + 2i's weight: a two-way select on the wave-uniform half
+      // (indexing the array with it compiled to a 16-way select per term)
+      const float wgt = half != 0u ? mv[2 * i + 1] : mv[2 * i];
+      acc = acc + wgt * ov[i];
+    }
     M = Mn;
   }
   {  // the last chunk
