@@ -1188,18 +1188,21 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   for (uint32_t g0 = 0; g0 < nm; g0 += 16u) {
     const uint32_t ng = nm - g0 < 16u ? nm - g0 : 16u;
     const size_t gb = base + (size_t)g0 * kPartialStride;
-    // unconditional loads of clamped chunk indices, masked after
-    // the group's m and l words, one per lane (lane c % 32: m of chunk c for
-    // c < 16, l of chunk c - 16 above; lanes 32-63 repeat lanes 0-31) and read
-    // out with readlane: one load per wave instead of one per word
-    const uint32_t mlc = lane % 16u, mll = (lane / 16u) % 2u;
-    uint32_t mlw, ow[8];
+    // unconditional loads of clamped chunk indices, masked after.  Lane j
+    // loads chunk j % 16's m and l words (the wave's four rows hold the same
+    // 16 chunks), so the group max, the chunk weights and the weighted sum
+    // of l are formed across the 16 lanes of a row, not by every thread for
+    // every chunk (32 readlanes, 16 exponentials and 16 products each)
+    const uint32_t mlc = lane % 16u;
+    uint32_t mw, lw, ow[8];
     auto load_group = [&]() {
       {
         const uint32_t cc = mlc < ng ? mlc : ng - 1u;
-        const size_t at = gb + cc * kPartialStride + kHeadDim + mll;
-        mlw = HANDOFF ? ld_agent_u32(a.hpart + at)
-                      : __builtin_bit_cast(uint32_t, ld_agent(a.partial + at));
+        const size_t at = gb + cc * kPartialStride + kHeadDim;
+        mw = HANDOFF ? ld_agent_u32(a.hpart + at)
+                     : __builtin_bit_cast(uint32_t, ld_agent(a.partial + at));
+        lw = HANDOFF ? ld_agent_u32(a.hpart + at + 1u)
+                     : __builtin_bit_cast(uint32_t, ld_agent(a.partial + at + 1u));
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -1214,7 +1217,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
       // re-poll (the whole wave) until every word of the group it uses is
       // written, then decode
       auto missing = [&]() {
-        bool z = mlc < ng && mlw == 0u;
+        bool z = mlc < ng && (mw == 0u || lw == 0u);
 #pragma unroll
         for (int i = 0; i < 8; ++i) z |= half + 2u * i < ng && ow[i] == 0u;
         return __builtin_amdgcn_ballot_w64(z) != 0u;
@@ -1229,38 +1232,27 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
         load_group();
       }
       TL(kTlMergeLoaded);
-      mlw -= 1u;
+      mw -= 1u;
+      lw -= 1u;
 #pragma unroll
       for (int i = 0; i < 8; ++i) ow[i] -= 1u;
     }
-    float mv[16], lv[16], ov[8];
-#pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      const float m_c = __builtin_bit_cast(float, __builtin_amdgcn_readlane((int)mlw, c));
-      const float l_c = __builtin_bit_cast(float, __builtin_amdgcn_readlane((int)mlw, 16 + c));
-      mv[c] = (uint32_t)c < ng ? m_c : -INFINITY;
-      lv[c] = (uint32_t)c < ng ? l_c : 0.f;
-    }
+    const float m_c = mlc < ng ? __builtin_bit_cast(float, mw) : -INFINITY;
+    const float l_c = mlc < ng ? __builtin_bit_cast(float, lw) : 0.f;
+    float ov[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) ov[i] = half + 2u * i < ng ? __builtin_bit_cast(float, ow[i]) : 0.f;
-    float Mn = M;
-#pragma unroll
-    for (int c = 0; c < 16; ++c) Mn = fmaxf(Mn, mv[c]);
+    const float Mn = fmaxf(M, row_max16(m_c));
     const float keep = M == -INFINITY ? 0.f : __expf(M - Mn);
-    Lsum = Lsum * keep;
+    const float w_c = m_c == -INFINITY ? 0.f : __expf(m_c - Mn);  // chunk mlc's weight
+    Lsum = Lsum * keep + row_sum16(w_c * l_c);
     acc = acc * keep;
+    // this thread's chunks half + 2i: lane 2i of w_h holds chunk half + 2i's
+    // weight (half is wave-uniform), read out with readlane
+    const float w_h = half != 0u ? dpp<kRowShl1>(w_c) : w_c;
 #pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      mv[c] = mv[c] == -INFINITY ? 0.f : __expf(mv[c] - Mn);  // chunk weight
-      Lsum = Lsum + mv[c] * lv[c];
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      // chunk half + 2i's weight: a two-way select on the wave-uniform half
-      // (indexing the array with it compiled to a 16-way select per term)
-      const float wgt = half != 0u ? mv[2 * i + 1] : mv[2 * i];
-      acc = acc + wgt * ov[i];
-    }
+    for (int i = 0; i < 8; ++i)
+      acc = acc + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w_h), 2 * i)) * ov[i];
     M = Mn;
   }
   {  // the last chunk

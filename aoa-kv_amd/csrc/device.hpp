@@ -94,6 +94,7 @@ constexpr int kQuadSwap1 = 0xB1;
 constexpr int kQuadSwap2 = 0x4E;
 constexpr int kRowHalfMirror = 0x141;
 constexpr int kRowMirror = 0x140;
+constexpr int kRowShl1 = 0x101;  // row_shl:1 (lane l of a row reads lane l + 1)
 
 // Sum over the 16 lanes of a DPP row; every lane of the row gets the sum.
 __device__ inline float row_sum16(float x) {
