@@ -847,6 +847,19 @@ __device__ __forceinline__ void row_bcast8(float v, float (&out)[8]) {
   out[7] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x157, 0xF, 0xF, false));
 }
 
+// out[i] = lane 2i of v's DPP row, in every lane of the row (row_newbcast)
+__device__ __forceinline__ void row_bcast_even8(float v, float (&out)[8]) {
+  const int x = __builtin_bit_cast(int, v);
+  out[0] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x150, 0xF, 0xF, false));
+  out[1] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x152, 0xF, 0xF, false));
+  out[2] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x154, 0xF, 0xF, false));
+  out[3] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x156, 0xF, 0xF, false));
+  out[4] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x158, 0xF, 0xF, false));
+  out[5] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x15A, 0xF, 0xF, false));
+  out[6] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x15C, 0xF, 0xF, false));
+  out[7] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x15E, 0xF, 0xF, false));
+}
+
 struct DecShared {
   float o[4][kHeadDim];
   float ml[4][2];
@@ -1247,12 +1260,13 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
     const float w_c = m_c == -INFINITY ? 0.f : __expf(m_c - Mn);  // chunk mlc's weight
     Lsum = Lsum * keep + row_sum16(w_c * l_c);
     acc = acc * keep;
-    // this thread's chunks half + 2i: lane 2i of w_h holds chunk half + 2i's
-    // weight (half is wave-uniform), read out with readlane
+    // this thread's chunks half + 2i: lane 2i of w_h's row holds chunk
+    // half + 2i's weight (half is wave-uniform), broadcast with DPP
     const float w_h = half != 0u ? dpp<kRowShl1>(w_c) : w_c;
+    float wt[8];
+    row_bcast_even8(w_h, wt);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      acc = acc + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w_h), 2 * i)) * ov[i];
+    for (int i = 0; i < 8; ++i) acc = acc + wt[i] * ov[i];
     M = Mn;
   }
   {  // the last chunk
