@@ -331,12 +331,15 @@ def test_fused_estimate_topk_long_rows(L):
 
 @pytest.mark.parametrize("layout", [NHD, HND])
 @pytest.mark.parametrize("L,budget,outlier", [(4096, 1024, False), (4096 + 9, 1024, False),
-                                              (1000, 1024, False), (32768, 2048, True)])
+                                              (1000, 1024, False), (32768, 2048, True),
+                                              (32768, 4096, True)])
 def test_full_decode_step_matches_simulation(layout, L, budget, outlier):
     """Config-1 shape, and config 2 at its full size (32768 tokens, budget
     2048, 4 key channels x8): prefill L-1 tokens, append one, then estimate /
     top-k / sparse decode; o within 2e-3 of the simulation's masked
-    attention; the two fused layer paths give the same bits."""
+    attention; the two fused layer paths give the same bits.  Budget 4096
+    (256 pages, 32 decode chunks per head) takes the split-K merge through
+    two groups of 16 chunks, in both layer paths."""
     from aoakv.utils import decode_estimate, decode_sparse_attn, decode_topk, decode_layer
     _say(f"[decode-step] layout={layout} L={L} budget={budget} outlier={outlier}")
     H = 32
