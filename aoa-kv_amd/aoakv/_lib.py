@@ -21,6 +21,7 @@ FLAG_VALUE_AWARE = 1
 FLAG_FIXED = 2
 FLAG_SINGLE_LAUNCH = 4
 FLAG_QUEST_KERNEL = 8
+FLAG_GROUPED_DECODE = 16
 
 _u32 = ctypes.c_uint32
 _p = ctypes.c_void_p

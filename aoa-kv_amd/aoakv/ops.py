@@ -11,8 +11,8 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._lib import (FLAG_FIXED, FLAG_QUEST_KERNEL, FLAG_SINGLE_LAUNCH,  # noqa: F401  (re-exported)
-                   FLAG_VALUE_AWARE)
+from ._lib import (FLAG_FIXED, FLAG_GROUPED_DECODE, FLAG_QUEST_KERNEL,  # noqa: F401
+                   FLAG_SINGLE_LAUNCH, FLAG_VALUE_AWARE)  # (re-exported)
 
 NHD = 0
 HND = 1

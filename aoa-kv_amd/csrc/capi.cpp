@@ -53,18 +53,20 @@ int hip_status(hipError_t e, const char* what) {
 // at once: CUs times the kernel's occupancy per CU (four at 36 KB of LDS and
 // 112 VGPRs).  0 if the device cannot be queried.  Cached per device (benign
 // races: every writer stores the same value).
-uint32_t resident_layer_workgroups() {
-  static uint32_t cache[64];
+uint32_t resident_layer_workgroups(uint32_t group, uint32_t heads_per_item) {
+  static uint32_t cache[64][8];
+  const uint32_t gi = (group == 1u ? 0u : group == 2u ? 1u : group == 4u ? 2u : 3u) +
+                      (heads_per_item > 1u ? 4u : 0u);
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0u;
-  if (cache[dev] == 0u) {
+  if (cache[dev][gi] == 0u) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         cus <= 0)
       return 0u;
-    cache[dev] = aoakv::layer_self_blocks_per_cu() * (uint32_t)cus;
+    cache[dev][gi] = aoakv::layer_self_blocks_per_cu(group, heads_per_item) * (uint32_t)cus;
   }
-  return cache[dev];
+  return cache[dev][gi];
 }
 
 #define REQUIRE(cond, ...)                                  \
@@ -606,6 +608,11 @@ static int fill_decode(aoakv::DecodeArgs& a, Workspace& w, const void* q, void* 
   a.max_chunks = aoakv::decode_chunks(max_sel);
   a.max_pages = max_pages;
   a.flags = flags & AOAKV_FLAG_QUEST_KERNEL;
+  // grouped decode only where it changes anything (a group of 2 or more) and
+  // the tuned kernels run (the generic ones serve one query head each)
+  a.heads_per_item = (flags & AOAKV_FLAG_GROUPED_DECODE) && aoakv::tuned_shape(head_dim, page_size)
+                         ? num_qo_heads / num_kv_heads
+                         : 1u;
   a.g = aoakv::make_geom(layout, num_kv_heads, page_size, head_dim);
   a.error = w.ctl + aoakv::kErrWord;
   return AOAKV_OK;
@@ -619,7 +626,9 @@ int aoakv_decode_sparse_attn(const void* q, void* o, const void* kv_data,
                              size_t workspace_bytes, uint32_t batch_size, uint32_t max_pages,
                              uint32_t num_qo_heads, uint32_t num_kv_heads, uint32_t head_dim,
                              uint32_t page_size, uint32_t layout, uint32_t flags, void* stream) {
-  if (int e = check_flags(flags, AOAKV_FLAG_QUEST_KERNEL, "decode_sparse_attn")) return e;
+  if (int e = check_flags(flags, AOAKV_FLAG_QUEST_KERNEL | AOAKV_FLAG_GROUPED_DECODE,
+                          "decode_sparse_attn"))
+    return e;
   aoakv::DecodeArgs a{};
   Workspace w{};
   if (int e = fill_decode(a, w, q, o, kv_data, kv_indptr, kv_indices, kv_last_page_len,
@@ -652,7 +661,7 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
   if (int e = fill_estimate(ea, q, scores, score_stride, metadata_data, metadata_indptr,
                             metadata_indices, kv_indptr, kv_indices, kv_last_page_len,
                             v_log_norm, batch_size, max_pages, num_qo_heads, num_kv_heads,
-                            head_dim, page_size, layout, flags))
+                            head_dim, page_size, layout, flags & ~AOAKV_FLAG_GROUPED_DECODE))
     return e;
   REQUIRE(sel_stride >= min_sel_stride(flags), "sparse_decode_layer: sel_stride %u < %u",
           sel_stride, min_sel_stride(flags));
@@ -683,6 +692,7 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
     const uint32_t max_sel = sel_cap < sel_stride ? sel_cap : sel_stride;
     la.e.hsel = w.hsel;
     la.e.hsel_stride = max_sel;
+    la.e.hsel_gi = da.heads_per_item;
     la.d = da;
     la.d.hsel = w.hsel;
     la.d.hsel_stride = max_sel;
@@ -698,14 +708,17 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
     la.n_est = batch_size * num_kv_heads * la.est_chunks;
     la.n_workers = aoakv::layer_score_workers(la.n_est, la.est_chunks);
     la.stagger_ps = aoakv::layer_stagger_ps(la.est_chunks);
-    la.n_dec = batch_size * num_qo_heads * da.max_chunks;
-    // one query head per kv head, score words, and the whole launch resident
-    // at once: each decode item selects its head's pages itself (no top-k
-    // workgroups, no selection handoff).  With more workgroups than the GPU
+    la.n_dec = batch_size * (num_qo_heads / da.heads_per_item) * da.max_chunks;
+    // score words and the whole launch resident at once: each decode item
+    // selects its kv head's pages itself (no top-k workgroups, no selection
+    // handoff; with GQA every query head's items do, and the group's last
+    // merging item clears the words).  With more workgroups than the GPU
     // holds, the 16 copies of every top-k cost more than the handoff they
     // save (config 5, 512 heads: 316 vs 250 us per layer).
-    la.self_select = la.e.hscore != nullptr && num_qo_heads == num_kv_heads &&
-                             la.n_workers + la.n_dec <= resident_layer_workgroups()
+    la.self_select = la.e.hscore != nullptr &&
+                             la.n_workers + la.n_dec <=
+                                 resident_layer_workgroups(num_qo_heads / num_kv_heads,
+                                                           da.heads_per_item)
                          ? 1u
                          : 0u;
     la.n_heads = la.self_select ? 0u : batch_size * num_kv_heads;

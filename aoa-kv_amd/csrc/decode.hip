@@ -263,9 +263,9 @@ __device__ __forceinline__ RadixResult radix_select(const uint32_t (&rel)[KPT], 
 // coalesced; with KPT = 64 (rows up to 16384 pages) keys are read and the
 // output written per thread.
 //
-// SELF (one-launch layer, one query head per kv head): every decode
-// workgroup of the head runs this same selection on the same score words.
-// The words are only read (the head's merging workgroup clears them), their
+// SELF (one-launch layer): every decode workgroup of the kv head (of each
+// query head of its group) runs this same selection on the same score words.
+// The words are only read (a merging workgroup clears them), their
 // wait starts with one sentinel word per scoring chunk, and the output stays
 // in sh.key[0, k) for the caller (nothing is stored).
 template <int KPT, bool SELF = false>
@@ -746,13 +746,16 @@ __device__ __forceinline__ void select_item(const EstimateArgs& a, uint32_t b, u
                                             const SelPlan& pl, TopkShared& tk) {
   const uint32_t P = pl.P, k = pl.k, pbeg = pl.pbeg;
   const bool handoff = pl.handoff;
+  // one handoff row per decode item of the kv head's group: GROUP / gi copies,
+  // rows b * Hq + h * GROUP + c * gi (each item clears the row it reads)
+  const uint32_t gi = a.hsel_gi > 1u ? a.hsel_gi : 1u;
   uint32_t* hout = handoff ? a.hsel + ((size_t)b * a.Hq + h * GROUP) * a.hsel_stride : nullptr;
   uint32_t* hwords =
       a.hscore ? a.hscore + ((size_t)b * a.Hkv + h) * a.hscore_stride : nullptr;
   topk_staged(a.scores + ((size_t)b * a.Hkv + h) * a.score_stride, P, k,
               (a.flags & kFlagFixed) != 0u, a.kv_indices + pbeg,
-              a.sel + ((size_t)b * a.Hkv + h) * a.sel_stride, tk, hout, a.hsel_stride, GROUP,
-              hwords, a.error);
+              a.sel + ((size_t)b * a.Hkv + h) * a.sel_stride, tk, hout, a.hsel_stride * gi,
+              GROUP / gi, hwords, a.error);
 }
 
 // Scores one chunk; with a.sel set, the last block of the head to finish
@@ -860,51 +863,66 @@ __device__ __forceinline__ void row_bcast_even8(float v, float (&out)[8]) {
   out[7] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x15E, 0xF, 0xF, false));
 }
 
+// G query heads per workgroup (the kv head's group): per wave and head the
+// softmax statistics and output, then the workgroup's combined partials.
+template <int G>
 struct DecShared {
-  float o[4][kHeadDim];
-  float ml[4][2];
-  float own[kHeadDim + 2];  // the merging block's own partial (one-launch layer)
+  float o[4][G][kHeadDim];
+  float ml[4][G][2];
+  float own[G][kHeadDim + 2];  // the merging block's own partials (one-launch layer)
   uint32_t sel[kDecPagesPerBlock];
   uint32_t last;
 };
 
-// Attends pages [8*chunk, 8*chunk + 8) of the selection of (sequence b,
-// query head hq) and merges the head's chunks.
+// Attends pages [8*chunk, 8*chunk + 8) of the selection of (sequence b, kv
+// head hq0 / group) for the G query heads hq0 .. hq0 + G - 1 of that kv
+// head's group: the K/V tiles are loaded once and stay in registers while each
+// head's logits, softmax and weighted sum run over them.  G = 1 gives each
+// query head its own workgroups (the default: the query heads of a group land
+// on one XCD, 16 or a multiple of 8 workgroup indices apart, so they share the
+// tiles through its L2 while running in parallel); G = group is the
+// reference's decode block, one threadIdx.y per query head of the group
+// (decode_attn.cuh:497-500).  Then the chunks are merged per query head.
 //   HANDOFF = false (two launches): the selection comes from the previous
-//     launch; chunks hand their partial (o, m, l) to the last block to
-//     arrive at a per-head counter.
+//     launch; chunks hand their partials (o, m, l) to the last block to
+//     arrive at a per-(sequence, kv head) counter.
 //   HANDOFF = true (one launch): the selection is read from the handoff rows
-//     the head's top-k writes in this launch, each entry polled until
-//     written; partials go to handoff words and the head's last chunk
-//     polls them and merges.  Every block only waits on blocks with smaller
-//     indices, which were dispatched before it.
-//   SELF (one launch, one query head per kv head): instead of polling a
-//     selection, the workgroup runs the head's top-k itself from the score
-//     words (every chunk of the head computes the same selection) and keeps
-//     its entries; the merging chunk clears the score words at the end.
+//     the kv head's top-k writes in this launch, each entry polled until
+//     written; partials go to handoff words and the last chunk polls them
+//     and merges.  Every block only waits on blocks with smaller indices,
+//     which were dispatched before it.
+//   SELF (one launch): instead of polling a selection, the workgroup runs the
+//     kv head's top-k itself from the score words (every chunk of the head
+//     computes the same selection) and keeps its entries; the merging chunk
+//     clears the score words at the end (with G < group, the last of the
+//     group's merging chunks to finish, counted per (sequence, kv head)).
+//     clear_ctr: that counter (G < group only).
 // QUEST (quest_kernel convention): the selection rows hold the pages chosen
 // besides the last page, which is always attended as the final entry
 // (quest/utils/__init__.py:237, approx_attn.cu:68-151).
 // One launch: err0 is the error word as read at the workgroup's start and
 // s_err an LDS word for it; with kErrWait set no handoff word is touched and
-// the head's output is NaN (written by its chunk 0).
-template <bool HANDOFF, bool QUEST, bool SELF = false>
-__device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uint32_t hq,
-                                            uint32_t chunk, DecShared& sm,
+// the group's outputs are NaN (written by its chunk 0).
+template <bool HANDOFF, bool QUEST, bool SELF = false, int G = 1>
+__device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uint32_t hq0,
+                                            uint32_t chunk, DecShared<G>& sm,
                                             const EstimateArgs* ea = nullptr,
                                             TopkShared* tk = nullptr, uint32_t* s_err = nullptr,
-                                            uint32_t err0 = 0u) {
+                                            uint32_t err0 = 0u, uint32_t* clear_ctr = nullptr) {
   static_assert(!SELF || HANDOFF, "self-selection is a one-launch mode");
-  float (*s_o)[kHeadDim] = sm.o;
-  float (*s_ml)[2] = sm.ml;
   const uint32_t lane = __lane_id();
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t row = lane / kLanesPerRow;
   const uint32_t l16 = lane % kLanesPerRow;
-  const uint32_t hkv = hq / (a.Hq / a.Hkv);
   const uint32_t S = kPageSize;
   const uint32_t d0 = l16 * kVec;
-  const size_t bh = (size_t)b * a.Hq + hq;
+  const uint32_t group = a.Hq / a.Hkv;
+  const uint32_t hkv = hq0 / group;
+  const size_t bh0 = (size_t)b * a.Hq + hq0;  // the item's first query head
+  // the item whose merge ends the use of the kv head's score words clears
+  // them: G = group, the merging chunk; G < group, the last of the group's
+  // merging chunks (clear_ctr); a malformed sequence's first query head
+  const bool words_owner = (uint32_t)G == group || clear_ctr == nullptr;
   const uint32_t idx0 = chunk * kDecPagesPerBlock + wave * kDecPagesPerWave;
   const uint32_t* sel_row =
       a.sel ? reinterpret_cast<const uint32_t*>(a.sel) + ((size_t)b * a.Hkv + hkv) * a.sel_stride
@@ -917,7 +935,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   const uint32_t P_table = (uint32_t)a.kv_indptr[b + 1] - pbeg;
   // a page table longer than the call was sized for is cut where the
   // scoring cuts it (est_pages), so the selection's size and the decode's
-  // agree; flagged once per (sequence, head)
+  // agree; flagged once per (sequence, kv head)
   const uint32_t P = P_table < a.max_pages ? P_table : a.max_pages;
   const uint32_t lpl = (uint32_t)a.kv_last_page_len[b];
   const int32_t tbv = *(a.token_budgets ? a.token_budgets + b : a.kv_indptr + b);
@@ -934,7 +952,9 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
     for (int s = 0; s < kDecPagesPerWave; ++s)
       selv[s] = ld_agent_u32(sel_src + (idx0 + s < sel_last ? idx0 + s : sel_last));
   }
-  const H8 qq = ld16(a.q + bh * kHeadDim + d0);
+  H8 qq[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) qq[g] = ld16(a.q + (bh0 + g) * kHeadDim + d0);
   __builtin_amdgcn_sched_barrier(0);  // keep the issue order written here
   // SELF: the head's top-k shape and its score words
   SelPlan pl{};
@@ -956,14 +976,16 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
     if (threadIdx.x == 0u) *s_err = err0;
     __syncthreads();
     if ((*s_err & kErrWait) != 0u) {
-      if (chunk == 0u && threadIdx.x < (uint32_t)kHeadDim)
-        a.o[bh * kHeadDim + threadIdx.x] = (f16)__builtin_nanf("");
+      if (chunk == 0u)
+        for (uint32_t i = threadIdx.x; i < (uint32_t)(G * kHeadDim); i += kThreads)
+          a.o[bh0 * kHeadDim + i] = (f16)__builtin_nanf("");
       return;
     }
   }
   if (P != P_table && chunk == 0u && threadIdx.x == 0u) flag_error(a.error, kErrTruncated);
   if (P == 0u || lpl == 0u || lpl > S) {  // malformed page table
-    if (SELF && chunk == 0u) consume_words();  // the words were written all the same
+    // the words were written all the same: consumed once per kv head
+    if (SELF && chunk == 0u && hq0 % group == 0u) consume_words();
     return;
   }
   // physical id of the sequence's last page (the one holding lpl tokens)
@@ -1019,9 +1041,9 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
     for (uint32_t i = ich + threadIdx.x; i < o_end; i += kThreads)
       sel_out[i] = (int32_t)(self_topk ? tk->key[i] : (uint32_t)ids[i]);
   } else if (HANDOFF) {
-    // this chunk's entries of the head's selection, each polled until the
+    // this chunk's entries of the kv head's selection, each polled until the
     // top-k of this launch has written it, then cleared for the next launch
-    uint32_t* hrow = a.hsel + bh * a.hsel_stride;
+    uint32_t* hrow = a.hsel + bh0 * a.hsel_stride;  // this item's copy
     const uint32_t e = ich + threadIdx.x;
     if (threadIdx.x < (uint32_t)kDecPagesPerBlock)
       sm.sel[threadIdx.x] = e < nsel ? wait_word(hrow + e, a.error) : 0u;
@@ -1062,167 +1084,173 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
     for (int i = 0; i < 4; ++i) vv[s][i] = ld16(a.kv + vbase + (size_t)(i * 4 + row) * a.g.tok);
   }
   __builtin_amdgcn_sched_barrier(0);
-  // q as four fp16 pairs: each logit term pair is one v_dot2_f32_f16
-  // (exact fp16 products, fp32 sum)
-  half2v q2[kVec / 2];
-#pragma unroll
-  for (int m = 0; m < kVec / 2; ++m) q2[m] = half_pair(qq, m);
   // tokens per page: the sequence's last page holds lpl of them
   if constexpr (!QUEST) last_phys = (uint32_t)a.kv_indices[pbeg + P - 1u];
   uint32_t ntok[kDecPagesPerWave];
 #pragma unroll
   for (int s = 0; s < kDecPagesPerWave; ++s)
     ntok[s] = live[s] ? (phys[s] == last_phys ? lpl : S) : 0u;
+  bool v_zeroed = false;  // the V of slots past a page's tokens, zeroed once
 
-  // ---- logits: fp16(q.k), then fp16(. / sqrt(d))  (quest_attention.py:265-268).
-  // The 16 lanes of a row hold the same 8 dot sums (tokens i*4 + row of the
-  // wave's two pages, u = 4s + i); lane l16 % 8 rounds and exponentiates
-  // token u = l16 % 8 only, and the row takes each token's value from its
-  // lane with DPP row_newbcast (the same arithmetic per token, once).
   constexpr int kTok = kDecPagesPerWave * 4;
   static_assert(kTok == 8, "one rounding lane per token of a row");
-  float raw[kTok];
-#pragma unroll
-  for (int s = 0; s < kDecPagesPerWave; ++s) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float acc = 0.f;
-#pragma unroll
-      for (int m = 0; m < kVec / 2; ++m)
-        acc = __builtin_amdgcn_fdot2(q2[m], half_pair(kk[s][i], m), acc, false);
-      raw[s * 4 + i] = row_sum16(acc);
-    }
-  }
   const uint32_t um = l16 % (uint32_t)kTok;  // this lane's token
-  float pick = raw[0];
 #pragma unroll
-  for (int u = 1; u < kTok; ++u) pick = um == (uint32_t)u ? raw[u] : pick;
-  float xm = (float)r16(div_sqrt_head_dim_f16((float)r16(pick)));
-  xm = (um % 4u) * 4u + row < (um < 4u ? ntok[0] : ntok[1]) ? xm : -INFINITY;
-  float x[kTok];
-  row_bcast8(xm, x);
-  float mloc = -INFINITY;
+  for (int g = 0; g < G; ++g) {
+    // q as four fp16 pairs: each logit term pair is one v_dot2_f32_f16
+    // (exact fp16 products, fp32 sum)
+    half2v q2[kVec / 2];
 #pragma unroll
-  for (int u = 0; u < kTok; ++u) mloc = fmaxf(mloc, x[u]);
-  const float m = cross_row_max(mloc);
-  float lsum = 0.f;
-  float o[kVec];
+    for (int m = 0; m < kVec / 2; ++m) q2[m] = half_pair(qq[g], m);
+    // ---- logits: fp16(q.k), then fp16(. / sqrt(d))  (quest_attention.py:265-268).
+    // The 16 lanes of a row hold the same 8 dot sums (tokens i*4 + row of the
+    // wave's two pages, u = 4s + i); lane l16 % 8 rounds and exponentiates
+    // token u = l16 % 8 only, and the row takes each token's value from its
+    // lane with DPP row_newbcast (the same arithmetic per token, once).
+    float raw[kTok];
 #pragma unroll
-  for (int j = 0; j < kVec; ++j) o[j] = 0.f;
-  if (m != -INFINITY) {
-    // slots past a page's token count (the sequence's last page) hold
-    // whatever the cache held: their probability is exactly 0, but 0 * NaN
-    // is NaN, so their V is zeroed.  A wave-uniform branch (every lane holds
-    // the same two pages), taken for the last page and unused entries only,
-    // and placed where the V loads are waited for anyway: a write to vv
-    // right after its loads would make the compiler wait for them there.
-    if (ntok[0] < S || ntok[1] < S) {
+    for (int s = 0; s < kDecPagesPerWave; ++s) {
 #pragma unroll
-      for (int s = 0; s < kDecPagesPerWave; ++s)
+      for (int i = 0; i < 4; ++i) {
+        float acc = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if ((uint32_t)(i * 4) + row >= ntok[s]) vv[s][i] = H8{};
+        for (int m = 0; m < kVec / 2; ++m)
+          acc = __builtin_amdgcn_fdot2(q2[m], half_pair(kk[s][i], m), acc, false);
+        raw[s * 4 + i] = row_sum16(acc);
+      }
     }
-    float pv[kTok];
-    row_bcast8(__expf(xm - m), pv);
+    float pick = raw[0];
 #pragma unroll
-    for (int u = 0; u < kTok; ++u) {
-      const float p = pv[u];
-      lsum = lsum + p;
-      // one mixed-precision FMA per dim (fp16 V converted in the FMA)
+    for (int u = 1; u < kTok; ++u) pick = um == (uint32_t)u ? raw[u] : pick;
+    float xm = (float)r16(div_sqrt_head_dim_f16((float)r16(pick)));
+    xm = (um % 4u) * 4u + row < (um < 4u ? ntok[0] : ntok[1]) ? xm : -INFINITY;
+    float x[kTok];
+    row_bcast8(xm, x);
+    float mloc = -INFINITY;
 #pragma unroll
-      for (int j = 0; j < kVec; ++j) o[j] = __builtin_fmaf(p, (float)vv[u / 4][u % 4].v[j], o[j]);
+    for (int u = 0; u < kTok; ++u) mloc = fmaxf(mloc, x[u]);
+    const float m = cross_row_max(mloc);
+    float lsum = 0.f;
+    float o[kVec];
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) o[j] = 0.f;
+    if (m != -INFINITY) {
+      // slots past a page's token count (the sequence's last page) hold
+      // whatever the cache held: their probability is exactly 0, but 0 * NaN
+      // is NaN, so their V is zeroed.  A wave-uniform branch (every lane holds
+      // the same two pages), taken for the last page and unused entries only,
+      // and placed where the V loads are waited for anyway: a write to vv
+      // right after its loads would make the compiler wait for them there.
+      if (!v_zeroed && (ntok[0] < S || ntok[1] < S)) {
+#pragma unroll
+        for (int s = 0; s < kDecPagesPerWave; ++s)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if ((uint32_t)(i * 4) + row >= ntok[s]) vv[s][i] = H8{};
+        v_zeroed = true;
+      }
+      float pv[kTok];
+      row_bcast8(__expf(xm - m), pv);
+#pragma unroll
+      for (int u = 0; u < kTok; ++u) {
+        const float p = pv[u];
+        lsum = lsum + p;
+        // one mixed-precision FMA per dim (fp16 V converted in the FMA)
+#pragma unroll
+        for (int j = 0; j < kVec; ++j) o[j] = __builtin_fmaf(p, (float)vv[u / 4][u % 4].v[j], o[j]);
+      }
+    }
+    lsum = cross_row_sum(lsum);
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) o[j] = cross_row_sum(o[j]);
+    // this wave's (o, m, l) of head g
+    if (row == 0u) {
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) sm.o[wave][g][d0 + j] = o[j];
+      if (l16 == 0u) {
+        sm.ml[wave][g][0] = m;
+        sm.ml[wave][g][1] = lsum;
+      }
     }
   }
-  lsum = cross_row_sum(lsum);
-#pragma unroll
-  for (int j = 0; j < kVec; ++j) o[j] = cross_row_sum(o[j]);
 
   TL(kTlAttended);
   // ---- combine the 4 waves of the block in LDS, store the chunk's (o, m, l)
-  if (row == 0u) {
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) s_o[wave][d0 + j] = o[j];
-    if (l16 == 0u) {
-      s_ml[wave][0] = m;
-      s_ml[wave][1] = lsum;
-    }
-  }
+  // per query head
   __syncthreads();
-  const size_t part_off = (bh * a.max_chunks + chunk) * kPartialStride;
-  if (threadIdx.x < (uint32_t)kHeadDim + 2u) {
-    const uint32_t d = threadIdx.x;
-    const float M = fmaxf(fmaxf(s_ml[0][0], s_ml[1][0]), fmaxf(s_ml[2][0], s_ml[3][0]));
+  for (uint32_t idx = threadIdx.x; idx < (uint32_t)G * (kHeadDim + 2u); idx += kThreads) {
+    const uint32_t g = G == 1 ? 0u : idx / (kHeadDim + 2u);
+    const uint32_t d = G == 1 ? idx : idx % (kHeadDim + 2u);
+    const float M = fmaxf(fmaxf(sm.ml[0][g][0], sm.ml[1][g][0]), fmaxf(sm.ml[2][g][0], sm.ml[3][g][0]));
     float acc = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const float sc = s_ml[w][0] == -INFINITY ? 0.f : __expf(s_ml[w][0] - M);
-      const float val = d < (uint32_t)kHeadDim ? s_o[w][d] : s_ml[w][1];
+      const float sc = sm.ml[w][g][0] == -INFINITY ? 0.f : __expf(sm.ml[w][g][0] - M);
+      const float val = d < (uint32_t)kHeadDim ? sm.o[w][g][d] : sm.ml[w][g][1];
       acc = acc + sc * val;
     }
     // slots 0..127: o; slot 128: m; slot 129: l
     const float val = d == (uint32_t)kHeadDim ? M : acc;
+    const size_t part_off = ((bh0 + g) * a.max_chunks + chunk) * kPartialStride;
     // the one-launch merging block (the head's last chunk) keeps its own
-    // partial in LDS: no store, no poll of it
+    // partials in LDS: no store, no poll of them
     if (!HANDOFF) st_agent(a.partial + part_off + d, val);
-    else if (chunk == nch - 1u) sm.own[d] = val;
+    else if (chunk == nch - 1u) sm.own[g][d] = val;
     else st_agent_u32(a.hpart + part_off + d, to_word(val));
   }
 
   TL(kTlPartial);
-  // ---- one block of this (sequence, head) merges the chunks
+  // ---- one block of this (sequence, kv head) merges the chunks of each of
+  // its query heads
   if (HANDOFF) {
     if (chunk != nch - 1u) return;  // the head's last chunk
-    __syncthreads();                // its own partial is in LDS
+    __syncthreads();                // its own partials are in LDS
   } else {
-    if (!arrive_last(&a.counters[bh * kCounterStride], nch, &sm.last)) return;
+    if (!arrive_last(&a.counters[bh0 * kCounterStride], nch, &sm.last)) return;
   }
-  const size_t base = bh * a.max_chunks * kPartialStride;
-  // chunks in groups of 16: every load of a group is issued before any is
-  // used (one memory round trip per group; handoff words are re-polled until
-  // written); thread t sums dim t%128 over the chunks of parity t/128, with
-  // the group max folded in online
-  // the head's last chunk (nch - 1) is folded in after the others: in the
-  // one-launch layer it is the merging block's own partial, from LDS
   const uint32_t d = threadIdx.x % kHeadDim, half = threadIdx.x / kHeadDim;
   const uint32_t nm = nch - 1u;  // chunks merged from memory
-  float lm, ll, lo;              // the last chunk's m, l, o[d]
-  if (HANDOFF) {
-    lm = sm.own[kHeadDim];
-    ll = sm.own[kHeadDim + 1];
-    lo = sm.own[d];
-  } else {
-    const size_t at = base + (size_t)nm * kPartialStride;
-    lm = ld_agent(a.partial + at + kHeadDim);
-    ll = ld_agent(a.partial + at + kHeadDim + 1);
-    lo = ld_agent(a.partial + at + d);
+  // chunks in groups of 16, the G heads' words of a group loaded together:
+  // every load of a group is issued before any is used (one memory round
+  // trip per group, handoff words re-polled until written); thread t sums dim
+  // t%128 over the chunks of parity t/128, with the group max folded in online.
+  // The last chunk (nch - 1) is folded in after the others: in the one-launch
+  // layer it is the merging block's own partial, from LDS.
+  float M[G], Lsum[G], acc[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    M[g] = -INFINITY;
+    Lsum[g] = 0.f;
+    acc[g] = 0.f;
   }
-  float M = -INFINITY, Lsum = 0.f, acc = 0.f;
   for (uint32_t g0 = 0; g0 < nm; g0 += 16u) {
     const uint32_t ng = nm - g0 < 16u ? nm - g0 : 16u;
-    const size_t gb = base + (size_t)g0 * kPartialStride;
     // unconditional loads of clamped chunk indices, masked after.  Lane j
     // loads chunk j % 16's m and l words (the wave's four rows hold the same
     // 16 chunks), so the group max, the chunk weights and the weighted sum
     // of l are formed across the 16 lanes of a row, not by every thread for
     // every chunk (32 readlanes, 16 exponentials and 16 products each)
     const uint32_t mlc = lane % 16u;
-    uint32_t mw, lw, ow[8];
+    uint32_t mw[G], lw[G], ow[G][8];
     auto load_group = [&]() {
-      {
-        const uint32_t cc = mlc < ng ? mlc : ng - 1u;
-        const size_t at = gb + cc * kPartialStride + kHeadDim;
-        mw = HANDOFF ? ld_agent_u32(a.hpart + at)
-                     : __builtin_bit_cast(uint32_t, ld_agent(a.partial + at));
-        lw = HANDOFF ? ld_agent_u32(a.hpart + at + 1u)
-                     : __builtin_bit_cast(uint32_t, ld_agent(a.partial + at + 1u));
-      }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t c = half + 2u * i;
-        const size_t at = gb + (c < ng ? c : ng - 1u) * kPartialStride + d;
-        ow[i] = HANDOFF ? ld_agent_u32(a.hpart + at)
-                        : __builtin_bit_cast(uint32_t, ld_agent(a.partial + at));
+      for (int g = 0; g < G; ++g) {
+        const size_t gb = ((bh0 + g) * a.max_chunks + g0) * kPartialStride;
+        {
+          const uint32_t cc = mlc < ng ? mlc : ng - 1u;
+          const size_t at = gb + cc * kPartialStride + kHeadDim;
+          mw[g] = HANDOFF ? ld_agent_u32(a.hpart + at)
+                          : __builtin_bit_cast(uint32_t, ld_agent(a.partial + at));
+          lw[g] = HANDOFF ? ld_agent_u32(a.hpart + at + 1u)
+                          : __builtin_bit_cast(uint32_t, ld_agent(a.partial + at + 1u));
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t c = half + 2u * i;
+          const size_t at = gb + (c < ng ? c : ng - 1u) * kPartialStride + d;
+          ow[g][i] = HANDOFF ? ld_agent_u32(a.hpart + at)
+                             : __builtin_bit_cast(uint32_t, ld_agent(a.partial + at));
+        }
       }
     };
     load_group();
@@ -1230,9 +1258,13 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
       // re-poll (the whole wave) until every word of the group it uses is
       // written, then decode
       auto missing = [&]() {
-        bool z = mlc < ng && (mw == 0u || lw == 0u);
+        bool z = false;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) z |= half + 2u * i < ng && ow[i] == 0u;
+        for (int g = 0; g < G; ++g) {
+          z |= mlc < ng && (mw[g] == 0u || lw[g] == 0u);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) z |= half + 2u * i < ng && ow[g][i] == 0u;
+        }
         return __builtin_amdgcn_ballot_w64(z) != 0u;
       };
       uint32_t it = 0u;
@@ -1245,81 +1277,125 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
         load_group();
       }
       TL(kTlMergeLoaded);
-      mw -= 1u;
-      lw -= 1u;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ow[i] -= 1u;
+      for (int g = 0; g < G; ++g) {
+        mw[g] -= 1u;
+        lw[g] -= 1u;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ow[g][i] -= 1u;
+      }
     }
-    const float m_c = mlc < ng ? __builtin_bit_cast(float, mw) : -INFINITY;
-    const float l_c = mlc < ng ? __builtin_bit_cast(float, lw) : 0.f;
-    float ov[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ov[i] = half + 2u * i < ng ? __builtin_bit_cast(float, ow[i]) : 0.f;
-    const float Mn = fmaxf(M, row_max16(m_c));
-    const float keep = M == -INFINITY ? 0.f : __expf(M - Mn);
-    const float w_c = m_c == -INFINITY ? 0.f : __expf(m_c - Mn);  // chunk mlc's weight
-    Lsum = Lsum * keep + row_sum16(w_c * l_c);
-    acc = acc * keep;
-    // this thread's chunks half + 2i: lane 2i of w_h's row holds chunk
-    // half + 2i's weight (half is wave-uniform), broadcast with DPP
-    const float w_h = half != 0u ? dpp<kRowShl1>(w_c) : w_c;
-    float wt[8];
-    row_bcast_even8(w_h, wt);
+    for (int g = 0; g < G; ++g) {
+      const float m_c = mlc < ng ? __builtin_bit_cast(float, mw[g]) : -INFINITY;
+      const float l_c = mlc < ng ? __builtin_bit_cast(float, lw[g]) : 0.f;
+      float ov[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc = acc + wt[i] * ov[i];
-    M = Mn;
+      for (int i = 0; i < 8; ++i) ov[i] = half + 2u * i < ng ? __builtin_bit_cast(float, ow[g][i]) : 0.f;
+      const float Mn = fmaxf(M[g], row_max16(m_c));
+      const float keep = M[g] == -INFINITY ? 0.f : __expf(M[g] - Mn);
+      const float w_c = m_c == -INFINITY ? 0.f : __expf(m_c - Mn);  // chunk mlc's weight
+      Lsum[g] = Lsum[g] * keep + row_sum16(w_c * l_c);
+      acc[g] = acc[g] * keep;
+      // this thread's chunks half + 2i: lane 2i of w_h's row holds chunk
+      // half + 2i's weight (half is wave-uniform), broadcast with DPP
+      const float w_h = half != 0u ? dpp<kRowShl1>(w_c) : w_c;
+      float wt[8];
+      row_bcast_even8(w_h, wt);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[g] = acc[g] + wt[i] * ov[i];
+      M[g] = Mn;
+    }
   }
-  {  // the last chunk
-    const float Mn = fmaxf(M, lm);
-    const float keep = M == -INFINITY ? 0.f : __expf(M - Mn);
-    Lsum = Lsum * keep;
-    acc = acc * keep;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {  // the last chunk
+    float lm, ll, lo;
+    if (HANDOFF) {
+      lm = sm.own[g][kHeadDim];
+      ll = sm.own[g][kHeadDim + 1];
+      lo = sm.own[g][d];
+    } else {
+      const size_t at = ((bh0 + g) * a.max_chunks + nm) * kPartialStride;
+      lm = ld_agent(a.partial + at + kHeadDim);
+      ll = ld_agent(a.partial + at + kHeadDim + 1);
+      lo = ld_agent(a.partial + at + d);
+    }
+    const float Mn = fmaxf(M[g], lm);
+    const float keep = M[g] == -INFINITY ? 0.f : __expf(M[g] - Mn);
+    Lsum[g] = Lsum[g] * keep;
+    acc[g] = acc[g] * keep;
     const float w = lm == -INFINITY ? 0.f : __expf(lm - Mn);
-    Lsum = Lsum + w * ll;
-    if (half == (nm & 1u)) acc = acc + w * lo;  // the half that sums its parity
+    Lsum[g] = Lsum[g] + w * ll;
+    if (half == (nm & 1u)) acc[g] = acc[g] + w * lo;  // the half that sums its parity
+    if (half == 1u) sm.o[0][g][d] = acc[g];
   }
-  if (half == 1u) s_o[0][d] = acc;
   __syncthreads();
-  if (half == 0u) a.o[bh * kHeadDim + d] = r16((acc + s_o[0][d]) / Lsum);
+  if (half == 0u) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      a.o[(bh0 + g) * kHeadDim + d] = r16((acc[g] + sm.o[0][g][d]) / Lsum[g]);
+  }
   TL(kTlOutput);
-  // Every thread has read its words (barrier above): clear them -- o words by
-  // their reader, m / l words by thread c.  Handoff words must be zero for
+  // Every thread has read its words (barriers above): clear them -- o words
+  // by their reader, m / l words by thread c.  Handoff words must be zero for
   // the next launch; the two-launch partials are cleared as well, so the
   // whole workspace is zero between calls whatever its layout: region
   // offsets depend on the call's selection size, and a later call with a
   // smaller one places its handoff words where these partials were.
   uint32_t* pwords = HANDOFF ? a.hpart : reinterpret_cast<uint32_t*>(a.partial);
-  for (uint32_t g0 = 0; g0 < nch; g0 += 16u) {
-    const size_t gb = base + (size_t)g0 * kPartialStride;
+#pragma unroll 1
+  for (uint32_t g = 0; g < (uint32_t)G; ++g) {
+    const size_t base = (bh0 + g) * a.max_chunks * kPartialStride;
+    for (uint32_t g0 = 0; g0 < nch; g0 += 16u) {
+      const size_t gb = base + (size_t)g0 * kPartialStride;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t c = g0 + half + 2u * i;
-      if (c < nch) st_agent_u32(pwords + gb + (half + 2u * i) * kPartialStride + d, 0u);
-    }
-    const uint32_t c = g0 + threadIdx.x;
-    if (threadIdx.x < 16u && c < nch) {
-      st_agent_u32(pwords + gb + threadIdx.x * kPartialStride + kHeadDim, 0u);
-      st_agent_u32(pwords + gb + threadIdx.x * kPartialStride + kHeadDim + 1, 0u);
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t c = g0 + half + 2u * i;
+        if (c < nch) st_agent_u32(pwords + gb + (half + 2u * i) * kPartialStride + d, 0u);
+      }
+      const uint32_t c = g0 + threadIdx.x;
+      if (threadIdx.x < 16u && c < nch) {
+        st_agent_u32(pwords + gb + threadIdx.x * kPartialStride + kHeadDim, 0u);
+        st_agent_u32(pwords + gb + threadIdx.x * kPartialStride + kHeadDim + 1, 0u);
+      }
     }
   }
   if constexpr (SELF) {
     // every chunk's partial arrived, and each chunk stored its partial after
     // its top-k had read the score words: clear them (without a top-k no one
-    // waited for them, so wait first)
-    if (self_topk) {
-      for (uint32_t i = threadIdx.x; i < pl.P; i += kThreads) st_agent_u32(words + i, 0u);
-    } else {
-      consume_words();
+    // waited for them, so wait first).  With G < group the group's other
+    // query heads may still be reading them: the last merging item of the
+    // group to get here clears them and resets the count.
+    bool mine = words_owner;
+    if (!mine) {
+      __syncthreads();  // every thread of this item is done with the words
+      if (threadIdx.x == 0u) {
+        const uint32_t prev =
+            __hip_atomic_fetch_add(clear_ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = prev == group / (uint32_t)G - 1u;
+        if (last) __hip_atomic_store(clear_ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sm.last = last ? 1u : 0u;
+      }
+      __syncthreads();
+      mine = sm.last != 0u;
+    }
+    if (mine) {
+      if (self_topk) {
+        for (uint32_t i = threadIdx.x; i < pl.P; i += kThreads) st_agent_u32(words + i, 0u);
+      } else {
+        consume_words();
+      }
     }
   }
 }
 
-template <bool QUEST>
+// grid (chunks, query heads / G, sequences)
+template <bool QUEST, int G>
 __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
-  __shared__ DecShared sm;
+  __shared__ DecShared<G> sm;
   TL_BEGIN();
   TL(kTlStart);
-  decode_item<false, QUEST>(a, blockIdx.z, blockIdx.y, blockIdx.x, sm);
+  decode_item<false, QUEST, false, G>(a, blockIdx.z, blockIdx.y * G, blockIdx.x, sm);
   TL_FLUSH();
 }
 
@@ -1345,32 +1421,33 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
 // and handoff words are cleared by their readers, so the workspace is zero
 // again for the next launch.  No counter is shared by all workgroups
 // (same-address device atomics serialize at ~12 ns each).
-// SELF (GROUP 1, la.self_select): the decode items select for themselves; a
-// separate instantiation, so the other path keeps its own register budget.
+// SELF (la.self_select): the decode items select for themselves; a separate
+// instantiation, so the other path keeps its own register budget.  GI: query
+// heads per decode item (1, or the whole group).
 #ifdef AOAKV_TIMELINE
 // the profiling build wraps the kernel body to note its start and write the
 // notes out when the workgroup ends, whichever way the body returns
-template <int GROUP, bool QUEST, bool SELF>
+template <int GROUP, bool QUEST, bool SELF, int GI>
 __device__ __forceinline__ void layer_body(const LayerArgs& la);
 
-template <int GROUP, bool QUEST, bool SELF>
+template <int GROUP, bool QUEST, bool SELF, int GI>
 __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
   TL_BEGIN();
-  layer_body<GROUP, QUEST, SELF>(la);
+  layer_body<GROUP, QUEST, SELF, GI>(la);
   TL_FLUSH();
 }
 
-template <int GROUP, bool QUEST, bool SELF>
+template <int GROUP, bool QUEST, bool SELF, int GI>
 __device__ __forceinline__ void layer_body(const LayerArgs& la)
 #else
-template <int GROUP, bool QUEST, bool SELF>
+template <int GROUP, bool QUEST, bool SELF, int GI>
 __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la)
 #endif
 {
-  static_assert(!SELF || GROUP == 1, "self-selection needs one query head per kv head");
+  static_assert(GI == 1 || GI == GROUP, "a decode item serves one query head or the group");
   __shared__ union {
     EstTopkShared e;
-    DecShared d;
+    DecShared<GI> d;
   } sm;
   __shared__ uint32_t s_ok;
   // The error word as the launch found it: kErrWait there means an earlier
@@ -1448,8 +1525,10 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la)
   } else if (t < la.n_workers + la.n_heads + la.n_dec) {
     const uint32_t err0 = *la.d.error;
     const uint32_t u = t - la.n_workers - la.n_heads;
+    // decode items per (sequence, block of GI query heads, chunk)
     const uint32_t bh = u / la.d.max_chunks, chunk = u % la.d.max_chunks;
-    const uint32_t b = bh / la.d.Hq, hq = bh % la.d.Hq;
+    const uint32_t nblk = la.d.Hq / GI;
+    const uint32_t b = bh / nblk, hq0 = (bh % nblk) * GI;
     if constexpr (SELF) {
       // start when the head's scoring workers start (their staggered
       // schedule; heads of later rounds: the last first-round start):
@@ -1457,12 +1536,18 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la)
       // polls to the memory traffic of the first heads' scoring (23.0 vs
       // 24.15 us per layer at config 2)
       const uint32_t first_round = (la.n_workers - 1u) / la.est_chunks;
+      const uint32_t bkv = b * la.d.Hkv + hq0 / GROUP;  // the (sequence, kv head)
       const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-      sleep_until(t0, (uint64_t)(bh < first_round ? bh : first_round) * la.stagger_ps);
+      sleep_until(t0, (uint64_t)(bkv < first_round ? bkv : first_round) * la.stagger_ps);
       TL(kTlStaggerDone);
-      decode_item<true, QUEST, true>(la.d, b, hq, chunk, sm.d, &la.e, &sm.e.tk, &s_err, err0);
+      // with GI < GROUP the group's merging items count who is done with the
+      // score words on the kv head's arrival counter (unused by SELF's scoring)
+      uint32_t* ctr = GI < GROUP ? la.e.counters + bkv * kCounterStride : nullptr;
+      decode_item<true, QUEST, true, GI>(la.d, b, hq0, chunk, sm.d, &la.e, &sm.e.tk, &s_err, err0,
+                                         ctr);
     } else {
-      decode_item<true, QUEST>(la.d, b, hq, chunk, sm.d, nullptr, nullptr, &s_err, err0);
+      decode_item<true, QUEST, false, GI>(la.d, b, hq0, chunk, sm.d, nullptr, nullptr, &s_err,
+                                          err0);
     }
   }
 }
@@ -1497,23 +1582,28 @@ hipError_t launch_estimate(const EstimateArgs& a, uint32_t batch, uint32_t max_p
 hipError_t launch_layer(const LayerArgs& la, hipStream_t s) {
   const uint32_t grid = la.n_workers + la.n_heads + la.n_dec;
   const bool quest = (la.e.flags & kFlagQuestKernel) != 0u;
-  if (la.self_select != 0u) {
-    if (la.e.Hq != la.e.Hkv) return hipErrorInvalidValue;
-    if (quest) hipLaunchKernelGGL((layer_kernel<1, true, true>), dim3(grid), dim3(kThreads), 0, s, la);
-    else hipLaunchKernelGGL((layer_kernel<1, false, true>), dim3(grid), dim3(kThreads), 0, s, la);
-    return hipGetLastError();
-  }
+  const bool self = la.self_select != 0u;
+  const bool grouped = la.d.heads_per_item > 1u;
   switch (la.e.Hq / la.e.Hkv) {
-#define AOAKV_LAYER(G)                                                                       \
-  case G:                                                                                    \
-    if (quest) hipLaunchKernelGGL((layer_kernel<G, true, false>), dim3(grid), dim3(kThreads), 0, s, la); \
-    else hipLaunchKernelGGL((layer_kernel<G, false, false>), dim3(grid), dim3(kThreads), 0, s, la);      \
+#define AOAKV_LAYER_GI(G, GI)                                                                        \
+  if (self && quest) hipLaunchKernelGGL((layer_kernel<G, true, true, GI>), dim3(grid), dim3(kThreads), 0, s, la);   \
+  else if (self) hipLaunchKernelGGL((layer_kernel<G, false, true, GI>), dim3(grid), dim3(kThreads), 0, s, la);      \
+  else if (quest) hipLaunchKernelGGL((layer_kernel<G, true, false, GI>), dim3(grid), dim3(kThreads), 0, s, la);     \
+  else hipLaunchKernelGGL((layer_kernel<G, false, false, GI>), dim3(grid), dim3(kThreads), 0, s, la);
+#define AOAKV_LAYER(G)                 \
+  case G:                              \
+    if (grouped) {                     \
+      AOAKV_LAYER_GI(G, G)             \
+    } else {                           \
+      AOAKV_LAYER_GI(G, 1)             \
+    }                                  \
     break;
-    AOAKV_LAYER(1)
+    case 1: AOAKV_LAYER_GI(1, 1) break;
     AOAKV_LAYER(2)
     AOAKV_LAYER(4)
     AOAKV_LAYER(8)
 #undef AOAKV_LAYER
+#undef AOAKV_LAYER_GI
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -1529,9 +1619,23 @@ hipError_t launch_topk(const TopkArgs& a, uint32_t batch, hipStream_t s) {
 }
 
 hipError_t launch_decode(const DecodeArgs& a, uint32_t batch, hipStream_t s) {
-  dim3 grid(a.max_chunks, a.Hq, batch);
-  if (a.flags & kFlagQuestKernel) hipLaunchKernelGGL(decode_kernel<true>, grid, dim3(kThreads), 0, s, a);
-  else hipLaunchKernelGGL(decode_kernel<false>, grid, dim3(kThreads), 0, s, a);
+  // one workgroup per (chunk, block of heads_per_item query heads, sequence)
+  const uint32_t gi = a.heads_per_item > 1u ? a.Hq / a.Hkv : 1u;
+  dim3 grid(a.max_chunks, a.Hq / gi, batch);
+  const bool quest = (a.flags & kFlagQuestKernel) != 0u;
+  switch (gi) {
+#define AOAKV_DEC(G)                                                                      \
+  case G:                                                                                 \
+    if (quest) hipLaunchKernelGGL((decode_kernel<true, G>), grid, dim3(kThreads), 0, s, a); \
+    else hipLaunchKernelGGL((decode_kernel<false, G>), grid, dim3(kThreads), 0, s, a);      \
+    break;
+    AOAKV_DEC(1)
+    AOAKV_DEC(2)
+    AOAKV_DEC(4)
+    AOAKV_DEC(8)
+#undef AOAKV_DEC
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
@@ -1583,12 +1687,21 @@ uint32_t layer_stagger_ps(uint32_t est_chunks) {
 uint32_t counter_stride() { return kCounterStride; }
 // Workgroups of the self-selecting layer kernel one CU holds at once (its LDS
 // and registers decide); 0 if the runtime cannot tell.
-uint32_t layer_self_blocks_per_cu() {
+uint32_t layer_self_blocks_per_cu(uint32_t group, uint32_t heads_per_item) {
   int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, layer_kernel<1, false, true>, kThreads, 0) !=
-          hipSuccess ||
-      n < 0)
-    return 0u;
+  hipError_t e = hipErrorInvalidValue;
+  const bool gr = heads_per_item > 1u;
+#define AOAKV_OCC(G, GI) \
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, layer_kernel<G, false, true, GI>, kThreads, 0)
+  switch (group) {
+    case 1: AOAKV_OCC(1, 1); break;
+    case 2: if (gr) AOAKV_OCC(2, 2); else AOAKV_OCC(2, 1); break;
+    case 4: if (gr) AOAKV_OCC(4, 4); else AOAKV_OCC(4, 1); break;
+    case 8: if (gr) AOAKV_OCC(8, 8); else AOAKV_OCC(8, 1); break;
+    default: break;
+  }
+#undef AOAKV_OCC
+  if (e != hipSuccess || n < 0) return 0u;
   return (uint32_t)n;
 }
 

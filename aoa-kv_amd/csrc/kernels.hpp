@@ -108,8 +108,9 @@ struct EstimateArgs {
   uint32_t* counters;  // [B * Hkv]
   // single launch only: the selection again, per query head, as page + 1
   // (0 = not yet written), for the decode items of the same launch
-  uint32_t* hsel;      // [B, Hq, hsel_stride] or nullptr
+  uint32_t* hsel;      // [B, Hq, hsel_stride] or nullptr: a copy per decode item
   uint32_t hsel_stride;
+  uint32_t hsel_gi;    // query heads per decode item (rows b * Hq + hq0 are read)
   // single launch only, optional: the scores again as handoff words (bits +
   // 1, 0 = not yet written), [B, Hkv, hscore_stride]; the top-k polls these
   // instead of an arrival counter and clears them
@@ -148,10 +149,13 @@ struct DecodeArgs {
   uint32_t Hq, Hkv, S, max_chunks;
   uint32_t max_pages;  // pages per sequence the call is sized for (as the scoring's)
   uint32_t flags;      // kFlagQuestKernel: the quest_kernel selection convention
+  // query heads per workgroup: 1 (each query head its own workgroups) or
+  // Hq / Hkv (one workgroup per kv head serves its whole group)
+  uint32_t heads_per_item;
   PageGeom g;
   // single launch only: handoff buffers whose words hold value + 1 (0 = not
   // yet written); every word is cleared again by its reader
-  uint32_t* hsel;      // [B, Hq, hsel_stride] selection of this launch
+  uint32_t* hsel;      // [B, Hq, hsel_stride] selection of this launch (row b * Hq + hq0)
   uint32_t hsel_stride;
   uint32_t* hpart;     // [B*Hq, max_chunks, kPartialStride] split-K partials
   uint32_t* error;     // workspace error word (kErrWait, kErrTruncated)
@@ -176,9 +180,9 @@ struct LayerArgs {
   uint32_t est_chunks; // 128-page chunks per (sequence, head)
   uint32_t n_workers;  // scoring workgroups (<= n_est), items taken round-robin
   uint32_t n_heads;    // top-k workgroups: B * Hkv
-  uint32_t n_dec;      // decode items: B * Hq * d.max_chunks
+  uint32_t n_dec;      // decode items: B * (Hq / d.heads_per_item) * d.max_chunks
   uint32_t stagger_ps; // wall time (ps) between the scoring starts of consecutive heads
-  uint32_t self_select;  // decode items run their head's top-k themselves (n_heads = 0)
+  uint32_t self_select;  // decode items run their kv head's top-k themselves (n_heads = 0)
 };
 
 hipError_t launch_append_prefill(const AppendPrefillArgs& a, hipStream_t s);
@@ -210,7 +214,7 @@ uint32_t fused_topk_max_pages();  // ... and the fused estimate + top-k kernel
 uint32_t layer_score_workers(uint32_t n_est, uint32_t est_chunks);  // one-launch layer scorers
 uint32_t layer_stagger_ps(uint32_t est_chunks);  // one-launch scoring start offset per head (ps)
 uint32_t counter_stride();        // u32 words between per-head counters (one cache line each)
-uint32_t layer_self_blocks_per_cu();  // self-selecting layer workgroups resident per CU
+uint32_t layer_self_blocks_per_cu(uint32_t group, uint32_t heads_per_item);  // per CU
 
 // generic.hip: the other head dims (64, 128, 256) and page sizes (1..32)
 hipError_t launch_gen_append_prefill(const AppendPrefillArgs& a, uint32_t head_dim, hipStream_t s);

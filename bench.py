@@ -311,11 +311,12 @@ def gqa_bench(dev, layout, n_layers=8, hq=32, hkv=8, launches=256):
     Llama-3-8B attention shape: 32 query heads over 8 kv heads x 128, the
     config-2 context (32768 tokens, page 16) and budget (2048 tokens).
     n_layers independent layers (1.1 GB, past the memory-side cache) are
-    replayed round-robin from a HIP graph, both decode paths; the one-launch
-    layer keeps its top-k workgroups here (self-selection needs one query
-    head per kv head).  Bytes are the unique ones a layer must read: every
-    page's metadata and value statistic for the 8 kv heads, the selected
-    pages' K/V once per kv head (its 4 query heads share them), q, o and the
+    replayed round-robin from a HIP graph: both decode paths, each with
+    per-query-head decode workgroups (the default) and with one workgroup per
+    kv head serving its group (AOAKV_FLAG_GROUPED_DECODE); all four must give
+    the same bits.  Bytes are the unique ones a layer must read: every page's
+    metadata and value statistic for the 8 kv heads, the selected pages' K/V
+    once per kv head (its 4 query heads share them), q, o and the
     selection."""
     import torch
     from aoakv import ops
@@ -353,7 +354,12 @@ def gqa_bench(dev, layout, n_layers=8, hq=32, hkv=8, launches=256):
            "bytes": int(nbytes), "layers_rotated": n_layers, "launches_timed": launches}
     base = ops.FLAG_VALUE_AWARE | ops.FLAG_FIXED
     results = {}
-    for name, flags in (("two_launch", base), ("one_launch", base | ops.FLAG_SINGLE_LAUNCH)):
+    # per-query-head decode workgroups (the default) and one workgroup per kv
+    # head serving its group (AOAKV_FLAG_GROUPED_DECODE), both paths
+    grp = ops.FLAG_GROUPED_DECODE
+    for name, flags in (("two_launch", base), ("one_launch", base | ops.FLAG_SINGLE_LAUNCH),
+                        ("two_launch_grouped", base | grp),
+                        ("one_launch_grouped", base | ops.FLAG_SINGLE_LAUNCH | grp)):
         def layer(l, flags=flags):
             ops.sparse_decode_layer(q[l], o[l], kv[l], indptr, idx[l], lpl, meta[l], mindptr,
                                     midx, lvn[l], scores[l], sel[l], BUDGET, ws, P, layout, flags)
@@ -383,6 +389,9 @@ def gqa_bench(dev, layout, n_layers=8, hq=32, hkv=8, launches=256):
         del gr
     (o2, s2), (o1, s1) = results["two_launch"], results["one_launch"]
     out["one_launch_equals_two_launch"] = bool(torch.equal(o1, o2) and torch.equal(s1, s2))
+    out["grouped_equals_per_head"] = all(
+        bool(torch.equal(results[k][0], o1) and torch.equal(results[k][1], s1))
+        for k in ("two_launch_grouped", "one_launch_grouped"))
     if ops.workspace_error(ws) != 0:
         raise SystemExit(f"GQA layer: workspace error word {ops.workspace_error(ws)}")
     return out

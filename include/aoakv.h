@@ -96,6 +96,17 @@ extern "C" {
  * Not combinable with AOAKV_FLAG_FIXED.  The value statistic is still read
  * at the page's own physical index. */
 #define AOAKV_FLAG_QUEST_KERNEL 8u
+/* aoakv_decode_sparse_attn and aoakv_sparse_decode_layer with grouped query
+ * attention (num_qo_heads > num_kv_heads): one decode workgroup per (kv
+ * head, chunk of 8 selected pages) loads the chunk's K/V once and serves the
+ * kv head's whole query group, as the reference's decode block does with one
+ * threadIdx.y per query head (decode_attn.cuh:497-500, 1158-1171).  Without
+ * it (the default) every query head has its own workgroups; the query heads
+ * of a group then run on one XCD and share the K/V through its L2, with
+ * G times the parallelism -- faster on MI355X at the shapes measured
+ * (bench.py extra.gqa_32q_8kv_32k).  Same arithmetic per query head either
+ * way: the outputs are identical. */
+#define AOAKV_FLAG_GROUPED_DECODE 16u
 
 /* The workspace error word: 32-bit word AOAKV_WS_ERR_WORD of a decode
  * workspace (offset 8 bytes), OR-ed by the kernels of every entry point that

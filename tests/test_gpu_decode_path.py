@@ -531,6 +531,27 @@ def test_gqa_selection_and_decode(Hq, Hkv, L, budget):
     mask = np.repeat(sim.pages_to_token_mask(sl[None, :, None], S, L), grp, axis=1)
     ref = sim.masked_decode_attention(q, np.repeat(K, grp, 1), np.repeat(V, grp, 1), mask)
     assert np.abs(o.cpu().numpy()[0].astype(np.float32) - ref[0, :, 0].astype(np.float32)).max() <= 2e-3
+    # one decode workgroup per kv head serving its group (FLAG_GROUPED_DECODE):
+    # the same arithmetic per query head, so the same bits, in both fused
+    # paths and in the standalone decode over the selection just made
+    o_ref, sel_ref = o.cpu().numpy(), sel.cpu().numpy()
+    base = ops.FLAG_VALUE_AWARE | ops.FLAG_FIXED | ops.FLAG_GROUPED_DECODE
+    wsw = ops.decode_workspace(1, Hq, Hkv, k, max_pages=P)
+    for fl in (base, base | ops.FLAG_SINGLE_LAUNCH):
+        for wsx in (ws, wsw):
+            o.fill_(0)
+            sel.fill_(-1)
+            ops.sparse_decode_layer(*args[:13], wsx, *args[14:], flags=fl)
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(o.cpu().numpy()), bits(o_ref)), hex(fl)
+            assert np.array_equal(sel.cpu().numpy(), sel_ref), hex(fl)
+            assert ops.workspace_error(wsx) == 0
+            assert int(wsx.count_nonzero().item()) == 0, "workspace left non-zero"
+    o2 = torch.empty_like(qd)
+    ops.decode_sparse_attn(qd, o2, kv, indptr, idx, lpl, sel, budget, ws, P, Hkv, HND,
+                           flags=ops.FLAG_GROUPED_DECODE)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(o2.cpu().numpy()), bits(o_ref))
 
 
 def test_errors_are_reported_not_crashed():
