@@ -30,10 +30,14 @@ driver):
   quest_attention.py:238-245) and the causal prefill kernel;
 * decode (one new token): the decode append (``update_page_filters``,
   ``update_mean_page_filters``) and, from layer 2 on, the value-aware (or
-  plain) page scores, the group-consistent top-k under
-  ``min(kv_seq_len, token_budget)`` and the sparse attention over the chosen
-  pages, in one launch (quest_attention.py:249-356); layers 0 and 1, and any
-  layer whose budget covers the sequence, attend every page;
+  plain) page scores, the group-consistent top-k of
+  ``k = min(max(3, min(kv_seq_len, token_budget) // chunk_size), P)`` pages
+  and the sparse attention over them (quest_attention.py:249-356,
+  filter_util.py:373) -- on every step, as the reference selects on every
+  step: with ``kv_seq_len <= token_budget`` and a partial last page, k is
+  P - 1 and the lowest-scored page is dropped.  Two launches (estimate +
+  top-k, then decode), which have no bounded waits.  Layers 0 and 1 attend
+  every page;
 * several new tokens after a prefill (the driver's question stage,
   pred.py:144-215): decoded one token after another, each as a decode step.
   The reference's torch forward instead scores that block's rows against
@@ -85,6 +89,10 @@ class LayerCache:
             torch.float16, device, layout=TensorLayout.HND, num_kv_heads=hkv,
             fixed=bool(getattr(mod, "fixed", False)), value_aware=value_aware)
         self.capacity = capacity
+        # with keep_selections set, every decode token's selection (physical
+        # page ids [Hkv, k], a copy) is appended to `selections` (for checks)
+        self.keep_selections = False
+        self.selections = []
 
     @property
     def seq_len(self) -> int:
@@ -114,14 +122,18 @@ def _rope(mod, q, k, v, position_ids, kwargs):
 
 def _decode_one(mod, cache: LayerCache, q: torch.Tensor, quest: bool) -> torch.Tensor:
     """Attention of one query (Hq, D) fp16 over the cache (its token already
-    appended): the page budget from layer 2 on, every page before."""
+    appended): the budget's selection from layer 2 on (every step, as
+    quest_attention.py:324-331), every page before."""
     c = cache.ctrl
-    budget_pages = int(getattr(mod, "token_budget", 0)) // cache.chunk_size
-    c.set_page_budget(budget_pages if quest else c.max_kv_pages)
+    budget_tokens = int(getattr(mod, "token_budget", 0))
+    c.set_page_budget(budget_tokens // cache.chunk_size if quest else c.max_kv_pages)
     c.begin_forward(1, updateTensor=False)
     q3 = q.view(1, c.num_heads, c.head_dim)
-    if quest and c.need_estimate():
-        return qutils.decode_layer(q3, c, 0, single_launch=True)
+    if quest and budget_tokens > 0:
+        o = qutils.decode_layer(q3, c, 0, single_launch=False)
+        if cache.keep_selections:
+            cache.selections.append(c._sel[0, :, :c.num_selected_pages()].clone())
+        return o
     return qutils.decode_sparse_attn(q3, c, 0, None)
 
 

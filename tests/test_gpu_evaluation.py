@@ -6,12 +6,15 @@ single-token decode steps, the cache going back in as ``past_key_value``.
 
 Per call the output (``o_proj`` replaced by the identity) is held to the
 oracle's restatement of the reference forward (quest_attention.py:196-382):
-the prefill to fp64 causal attention; each decode token to
-``sim.decode_step`` (append, scores, group-consistent top-k, masked
-attention) with the selection compared tie-aware and the output within
-2e-3 of the oracle's attention over the stand-in's own pages.  Layers 0-1
-attend every page.  The question tokens are decoded one at a time here (the
-reference's block form is documented in aoakv/evaluation.py).
+the prefill to fp64 causal attention; every decode token -- each token of
+the question block as well as the single-token steps -- to ``sim.decode_step``
+(append, scores, group-consistent top-k, masked attention) with the
+selection compared tie-aware and the output within 2e-3 of the oracle's
+attention over the stand-in's own pages.  Layers 0-1 attend every page.  A
+short context (fewer tokens than the budget, a partial last page) checks
+that quest layers select on every step, as the reference does (k = P - 1
+there: the lowest page is dropped).  The question tokens are decoded one at a
+time here (the reference's block form is documented in aoakv/evaluation.py).
 """
 import sys
 import types
@@ -72,13 +75,14 @@ def _qkv(attn, x, pos):
     return f(q), f(k), f(v)
 
 
-@pytest.mark.parametrize("hq,hkv,layer_id,value_aware", [
-    (4, 4, 3, True), (8, 2, 3, True), (4, 4, 3, False), (4, 4, 1, True)])
-def test_stand_in_matches_oracle(hq, hkv, layer_id, value_aware):
-    _say(f"[eval] hq={hq} hkv={hkv} layer={layer_id} value_aware={value_aware}")
+@pytest.mark.parametrize("hq,hkv,layer_id,value_aware,L0", [
+    (4, 4, 3, True, 1500), (8, 2, 3, True, 1500), (4, 4, 3, False, 1500), (4, 4, 1, True, 1500),
+    (4, 4, 3, True, 203), (8, 2, 3, False, 203)])
+def test_stand_in_matches_oracle(hq, hkv, layer_id, value_aware, L0):
+    _say(f"[eval] hq={hq} hkv={hkv} layer={layer_id} value_aware={value_aware} L0={L0}")
     from aoakv import evaluation as ev
     group = hq // hkv
-    budget, L0, n_question, n_decode = 256, 1500, 5, 12
+    budget, n_question, n_decode = 256, 5, 12
     attn = _setup(hq, hkv, layer_id, value_aware, budget, seed=hq + layer_id)
     g = torch.Generator(device=DEV).manual_seed(3)
     hid = attn.config.hidden_size
@@ -91,6 +95,7 @@ def test_stand_in_matches_oracle(hq, hkv, layer_id, value_aware):
                             padding_mask=None)
         assert w is None and len(past) == 3 and past[-1] == L0
         assert isinstance(past[0], ev.LayerCache)
+        past[0].keep_selections = True
         q, k, v = _qkv(attn, xs[:, :L0], pos)
         ref = sim.causal_prefill_rows(q, np.repeat(k, group, 1), np.repeat(v, group, 1))
         o = out[0].view(L0, hq, 128).float().cpu().numpy()
@@ -98,6 +103,7 @@ def test_stand_in_matches_oracle(hq, hkv, layer_id, value_aware):
         state = sim.SimLayerState(k.transpose(1, 0, 2)[None], v.transpose(1, 0, 2)[None], S)
         # question block (several tokens), then decode steps
         t = L0
+        dropped = 0  # quest-layer steps that attended fewer pages than the sequence has
         for n in [n_question] + [1] * n_decode:
             pos = torch.arange(t, t + n, device=DEV)[None]
             out, _, past = attn(hidden_states=xs[:, t:t + n], attention_mask=None,
@@ -107,32 +113,38 @@ def test_stand_in_matches_oracle(hq, hkv, layer_id, value_aware):
             o = out[0].view(n, hq, 128).float().cpu().numpy()
             q, k, v = _qkv(attn, xs[:, t:t + n], pos)
             c = past[0].ctrl
+            # the stand-in's selection of each token of this call
+            sels = past[0].selections[-n:] if layer_id >= 2 else []
+            assert layer_id < 2 or len(past[0].selections) == t + n - L0
             for i in range(n):
                 qi = q[i][None, :, None, :]
                 st_k, st_v = k[i][None, :, None, :], v[i][None, :, None, :]
                 if layer_id >= 2:
                     o_ref, scores, pages = sim.decode_step(state, qi, st_k, st_v, budget, True,
                                                            value_aware, group)
-                    if i == n - 1:  # the stand-in's selection of its last token
-                        kk = c.num_selected_pages()
-                        inv = {p: j for j, p in enumerate(c.kv_cache.indicies)}
-                        mine = np.array([[inv[int(x)] for x in row]
-                                         for row in c._sel[0, :, :kk].cpu().numpy()])
-                        for hh in range(hkv):
-                            ok, why = sim.selection_matches(mine[hh], pages[0, hh, 0],
-                                                            scores[0, hh, 0], True)
-                            assert ok, (t + i, hh, why)
-                        o_ref = sim.sparse_decode_attention(
-                            qi, np.repeat(state.K, group, 1), np.repeat(state.V, group, 1),
-                            np.repeat(mine[None, :, None, :], group, 1), S, state.kv_len)
+                    # the stand-in's selection of this token: as many pages as
+                    # the oracle's k, the same set up to near-ties
+                    inv = {p: j for j, p in enumerate(c.kv_cache.indicies)}
+                    mine = np.array([[inv[int(x)] for x in row] for row in sels[i].cpu().numpy()])
+                    assert mine.shape[-1] == pages.shape[-1], (t + i, mine.shape, pages.shape)
+                    dropped += int(mine.shape[-1] < len(c.kv_cache.indicies))
+                    for hh in range(hkv):
+                        ok, why = sim.selection_matches(mine[hh], pages[0, hh, 0],
+                                                        scores[0, hh, 0], True)
+                        assert ok, (t + i, hh, why)
+                    o_ref = sim.sparse_decode_attention(
+                        qi, np.repeat(state.K, group, 1), np.repeat(state.V, group, 1),
+                        np.repeat(mine[None, :, None, :], group, 1), S, state.kv_len)
                 else:
                     state.append(st_k, st_v)
                     o_ref = sim.masked_decode_attention(qi, np.repeat(state.K, group, 1),
                                                         np.repeat(state.V, group, 1), None)
-                if layer_id < 2 or i == n - 1:
-                    err = float(np.abs(o[i] - o_ref[0, :, 0].astype(np.float32)).max())
-                    assert err <= 2e-3, (t + i, err)
+                err = float(np.abs(o[i] - o_ref[0, :, 0].astype(np.float32)).max())
+                assert err <= 2e-3, (t + i, err)
             t += n
+        if layer_id >= 2:  # every step selects, also below the budget
+            assert dropped >= 1, "no quest step dropped a page"
+
 
 
 def test_cache_capacity_is_enforced():
