@@ -40,7 +40,7 @@ SIGNATURES = {
     "aoakv_estimate_attn_score": [_p, _p, _u32, _p, _p, _p, _p, _p, _p, _p, _u32, _u32,
                                   _u32, _u32, _u32, _u32, _u32, _u32, _p],
     "aoakv_topk_filtering": [_p, _u32, _p, _p, _p, _u32, _p, _p, _u32, _u32, _u32, _u32,
-                             _u32, _p],
+                             _u32, _p, _p],
     "aoakv_decode_workspace_size": [_u32, _u32, _u32, _u32, _u32],
     "aoakv_layer_workspace_size": [_u32, _u32, _u32, _u32, _u32, _u32],
     "aoakv_workspace_init": [_p, _sz, _p],
@@ -52,6 +52,8 @@ SIGNATURES = {
     "aoakv_sparse_decode_layer_noalloc": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _u32,
                                           _p, _u32, _u32, _p, _u32, _u32, _u32, _u32, _u32,
                                           _u32, _u32, _u32, _p],
+    "aoakv_noalloc_init": [],
+    "aoakv_noalloc_error": [_p, _u32, _p],
     "aoakv_estimate_topk": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _u32, _p, _u32, _u32, _p, _p,
                             _sz, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _p],
     "aoakv_prefill_with_paged_kv_cache": [_p, _p, _p, _p, _u32, _u32, _u32, _u32, _u32,

@@ -6,6 +6,7 @@ copied or converted here: a wrong dtype / layout is an error, not a cast.
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Optional
 
 import torch
@@ -176,9 +177,12 @@ def estimate_attn_score(q, scores, metadata_data, metadata_indptr, metadata_indi
 
 
 def topk_filtering(scores, kv_indptr, kv_indices, kv_last_page_len, token_budget: int, sel_pages,
-                   page_size: int = 16, flags: int = FLAG_FIXED, token_budgets=None):
+                   page_size: int = 16, flags: int = FLAG_FIXED, token_budgets=None,
+                   workspace=None):
     """Reference: quest/ops/csrc/topk.cu:7-46.  Writes sel_pages [B, Hkv, k_max]
-    (physical page ids, ascending logical order)."""
+    (physical page ids, ascending logical order).  ``workspace``: a decode
+    workspace whose error word receives WS_ERR_TRUNCATED when a page table
+    holds more pages than a score row (None: not reported)."""
     _need(scores, "scores", torch.float32)
     _need(sel_pages, "sel_pages", torch.int32)
     for t, n in ((kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"),
@@ -189,10 +193,16 @@ def topk_filtering(scores, kv_indptr, kv_indices, kv_last_page_len, token_budget
     B, Hkv, stride = scores.shape
     if sel_pages.dim() != 3 or sel_pages.shape[:2] != (B, Hkv):
         raise ValueError("sel_pages must be [B, Hkv, k_max]")
+    err = None
+    if workspace is not None:
+        _need(workspace, "workspace", torch.uint8)
+        if workspace.numel() < 12:
+            raise ValueError("workspace too small to hold the error word")
+        err = workspace.data_ptr() + 4 * WS_ERR_WORD
     _lib.call("aoakv_topk_filtering", scores.data_ptr(), stride, kv_indptr.data_ptr(),
               kv_indices.data_ptr(), kv_last_page_len.data_ptr(), token_budget,
               _ptr(token_budgets), sel_pages.data_ptr(), sel_pages.shape[2], B, Hkv, page_size,
-              flags, _stream())
+              flags, err, _stream())
 
 
 def decode_workspace(batch: int, num_qo_heads: int, num_kv_heads: int, max_sel_pages: int,
@@ -211,7 +221,8 @@ def decode_workspace(batch: int, num_qo_heads: int, num_kv_heads: int, max_sel_p
     return ws
 
 
-# bits of the workspace error word (aoakv.h AOAKV_WS_ERR_*)
+# the workspace error word (aoakv.h AOAKV_WS_ERR_WORD) and its bits
+WS_ERR_WORD = 2
 WS_ERR_WAIT = 1
 WS_ERR_TRUNCATED = 2
 
@@ -223,7 +234,8 @@ def workspace_error(workspace: torch.Tensor) -> int:
     ``workspace_init``), WS_ERR_TRUNCATED when a device page table held more
     pages than a call was sized for.  Reads the word back, so it
     synchronizes with the stream."""
-    return int(workspace[8:12].view(torch.int32).item())
+    w = 4 * WS_ERR_WORD
+    return int(workspace[w:w + 4].view(torch.int32).item())
 
 
 def workspace_wait_failed(workspace: torch.Tensor) -> bool:
@@ -321,6 +333,22 @@ def sparse_decode_layer_noalloc(q, o, kv_data, kv_indptr, kv_indices, kv_last_pa
               metadata_indices.data_ptr(), _ptr(v_log_norm), scores.data_ptr(), scores.shape[-1],
               sel_pages.data_ptr(), sel_pages.shape[-1], token_budget, _ptr(token_budgets), B,
               max_pages, Hq, Hkv, D, S, layout, flags, _stream())
+
+
+def noalloc_init() -> None:
+    """Look up the library's scratch array on the current device
+    (aoakv_noalloc_init): call before capturing sparse_decode_layer_noalloc
+    into a graph."""
+    _lib.call("aoakv_noalloc_init")
+
+
+def noalloc_error(clear: bool = False) -> int:
+    """The current device's scratch error bits (WS_ERR_*) set by
+    sparse_decode_layer_noalloc calls (aoakv_noalloc_error); synchronizes the
+    current stream.  ``clear`` zeroes a non-zero word afterwards."""
+    bits = ctypes.c_uint32(0)
+    _lib.call("aoakv_noalloc_error", ctypes.byref(bits), 1 if clear else 0, _stream())
+    return int(bits.value)
 
 
 def estimate_topk(q, metadata_data, metadata_indptr, metadata_indices, kv_indptr, kv_indices,

@@ -134,7 +134,8 @@ def decode_topk(estimated_attn_score: torch.Tensor, iController: InferenceContro
     pages besides the last, with the quest_kernel convention."""
     c = iController
     ops.topk_filtering(c.scores, c.kv_indptr_for_append, c.kv_indices_with_last,
-                       c.kv_last_page_len_t, c.token_budget, c._sel, c.page_size, c.flags)
+                       c.kv_last_page_len_t, c.token_budget, c._sel, c.page_size, c.flags,
+                       workspace=c.workspace)
     return c.topk_dindices_buffer[0]
 
 

@@ -232,20 +232,20 @@ __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[64];
 
-int scratch_for_current_device(void** out) {
+// The scratch array's device address on the current device, resolved on the
+// first call per device (aoakv_noalloc_init makes that call outside any
+// stream capture).  `who` names the entry point in error messages.
+int scratch_for_current_device(void** out, const char* who) {
   int dev = -1;
   if (hipError_t e = hipGetDevice(&dev); e != hipSuccess)
-    return fail(AOAKV_ERR_HIP, "sparse_decode_layer_noalloc: hipGetDevice: %s",
-                hipGetErrorString(e));
+    return fail(AOAKV_ERR_HIP, "%s: hipGetDevice: %s", who, hipGetErrorString(e));
   if (dev < 0 || dev >= 64)
-    return fail(AOAKV_ERR_UNSUPPORTED, "sparse_decode_layer_noalloc: device %d out of range",
-                dev);
+    return fail(AOAKV_ERR_UNSUPPORTED, "%s: device %d out of range", who, dev);
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
     void* p = nullptr;
     if (hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)); e != hipSuccess || !p)
-      return fail(AOAKV_ERR_HIP, "sparse_decode_layer_noalloc: hipGetSymbolAddress: %s",
-                  hipGetErrorString(e));
+      return fail(AOAKV_ERR_HIP, "%s: hipGetSymbolAddress: %s", who, hipGetErrorString(e));
     g_scratch_ptr[dev] = p;
   }
   *out = g_scratch_ptr[dev];
@@ -502,7 +502,7 @@ int aoakv_topk_filtering(const float* scores, uint32_t score_stride,
                          const int32_t* kv_last_page_len, uint32_t token_budget,
                          const int32_t* token_budgets, int32_t* sel_pages, uint32_t sel_stride,
                          uint32_t batch_size, uint32_t num_kv_heads, uint32_t page_size,
-                         uint32_t flags, void* stream) {
+                         uint32_t flags, uint32_t* error_word, void* stream) {
   REQUIRE(scores && kv_indptr && kv_indices && kv_last_page_len && sel_pages,
           "topk_filtering: null pointer argument");
   REQUIRE(page_size >= 1u && page_size <= aoakv::kMaxPageSize,
@@ -532,6 +532,7 @@ int aoakv_topk_filtering(const float* scores, uint32_t score_stride,
   a.Hkv = num_kv_heads;
   a.S = page_size;
   a.flags = flags;
+  a.error = error_word;
   return hip_status(aoakv::launch_topk(a, batch_size, static_cast<hipStream_t>(stream)),
                     "topk_filtering");
 }
@@ -752,13 +753,39 @@ int aoakv_sparse_decode_layer_noalloc(
           "%zu the library holds per device (batch %u x %u query heads x %u selected pages)",
           need, kNoAllocScratchBytes, batch_size, num_qo_heads, max_sel);
   void* ws = nullptr;
-  if (int e = scratch_for_current_device(&ws)) return e;
+  if (int e = scratch_for_current_device(&ws, "sparse_decode_layer_noalloc")) return e;
   return aoakv_sparse_decode_layer(q, o, kv_data, kv_indptr, kv_indices, kv_last_page_len,
                                    metadata_data, metadata_indptr, metadata_indices, v_log_norm,
                                    scores, score_stride, sel_pages, sel_stride, token_budget,
                                    token_budgets, ws, kNoAllocScratchBytes, batch_size, max_pages,
                                    num_qo_heads, num_kv_heads, head_dim, page_size, layout, flags,
                                    stream);
+}
+
+int aoakv_noalloc_init(void) {
+  void* ws = nullptr;
+  return scratch_for_current_device(&ws, "noalloc_init");
+}
+
+int aoakv_noalloc_error(uint32_t* error_bits, uint32_t clear, void* stream) {
+  REQUIRE(error_bits, "noalloc_error: null error_bits");
+  void* ws = nullptr;
+  if (int e = scratch_for_current_device(&ws, "noalloc_error")) return e;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t* word = static_cast<uint32_t*>(ws) + aoakv::kErrWord;
+  // the word as the stream's earlier calls leave it; a synchronous copy to a
+  // stack word (no staging buffer of the library's own)
+  if (hipError_t e = hipStreamSynchronize(s); e != hipSuccess)
+    return fail(AOAKV_ERR_HIP, "noalloc_error: hipStreamSynchronize: %s", hipGetErrorString(e));
+  uint32_t bits = 0u;
+  if (hipError_t e = hipMemcpy(&bits, word, sizeof bits, hipMemcpyDeviceToHost); e != hipSuccess)
+    return fail(AOAKV_ERR_HIP, "noalloc_error: hipMemcpy: %s", hipGetErrorString(e));
+  *error_bits = bits;
+  if (clear && bits != 0u) {
+    if (hipError_t e = aoakv::launch_fill_u32(word, 1u, 0u, s); e != hipSuccess)
+      return fail(AOAKV_ERR_HIP, "noalloc_error: clear: %s", hipGetErrorString(e));
+  }
+  return AOAKV_OK;
 }
 
 int aoakv_estimate_topk(const void* q, const void* metadata_data, const int32_t* metadata_indptr,

@@ -247,17 +247,21 @@ int aoakv_estimate_attn_score(const void* q, float* scores, uint32_t score_strid
  * pages in ascending logical order; entries >= k_b untouched.
  * sel_stride >= max_b k_b.  A score row is the candidate set: at most
  * score_stride <= 16384 pages (16383 with AOAKV_FLAG_QUEST_KERNEL) per
- * (sequence, head) take part, as the reference's top-k over an [H, n] row;
- * a longer device page table is not flagged here (no workspace).  With
- * AOAKV_FLAG_QUEST_KERNEL: k_b - 1 pages chosen among the first P_b - 1
- * (score rows of P_b - 1 entries), the last page not written.
+ * (sequence, head) take part, as the reference's top-k over an [H, n] row.
+ * error_word: NULL, or a device word into which a sequence whose page table
+ * holds more pages than a score row (or than 16384) ORs
+ * AOAKV_WS_ERR_TRUNCATED (its selection is made from the row's pages, as
+ * above); the word is only ever set, the caller clears it.  A workspace's
+ * error word (byte offset 8 of a workspace, AOAKV_WS_ERR_WORD) may be
+ * passed.  With AOAKV_FLAG_QUEST_KERNEL: k_b - 1 pages chosen among the
+ * first P_b - 1 (score rows of P_b - 1 entries), the last page not written.
  */
 int aoakv_topk_filtering(const float* scores, uint32_t score_stride,
                          const int32_t* kv_indptr, const int32_t* kv_indices,
                          const int32_t* kv_last_page_len, uint32_t token_budget,
                          const int32_t* token_budgets, int32_t* sel_pages, uint32_t sel_stride,
                          uint32_t batch_size, uint32_t num_kv_heads, uint32_t page_size,
-                         uint32_t flags, void* stream);
+                         uint32_t flags, uint32_t* error_word, void* stream);
 
 /*
  * Bytes of the caller-owned workspace for aoakv_decode_sparse_attn and
@@ -341,8 +345,12 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
  * rejected with AOAKV_ERR_INVALID.  Allocates nothing.  Calls share their
  * GPU's array: two calls that overlap on one GPU (different streams, or
  * different host threads without ordering) race and give wrong results.
- * The array's error word is not reported (a device page table longer than
- * max_pages is still cut safely, as in aoakv_sparse_decode_layer).
+ * The array has an error word like a workspace's (AOAKV_WS_ERR_TRUNCATED
+ * when a device page table is longer than max_pages; the sequence is cut
+ * safely, as in aoakv_sparse_decode_layer): aoakv_noalloc_error reads and
+ * clears it.  The array's device address is looked up on the first call on
+ * a device (hipGetSymbolAddress); a caller that captures the call into a
+ * HIP graph calls aoakv_noalloc_init on that device first, outside capture.
  */
 int aoakv_sparse_decode_layer_noalloc(
     const void* q, void* o, const void* kv_data, const int32_t* kv_indptr,
@@ -352,6 +360,23 @@ int aoakv_sparse_decode_layer_noalloc(
     uint32_t token_budget, const int32_t* token_budgets, uint32_t batch_size, uint32_t max_pages,
     uint32_t num_qo_heads, uint32_t num_kv_heads, uint32_t head_dim, uint32_t page_size,
     uint32_t layout, uint32_t flags, void* stream);
+
+/*
+ * Set-up for aoakv_sparse_decode_layer_noalloc on the current device: looks
+ * up the device address of the library's scratch array once (later calls
+ * are no-ops).  Call it before capturing a noalloc call into a HIP graph.
+ * No counterpart in the reference; for callers that cannot allocate.
+ */
+int aoakv_noalloc_init(void);
+
+/*
+ * Reads the current device's scratch error word (AOAKV_WS_ERR_* bits set by
+ * aoakv_sparse_decode_layer_noalloc calls since it was last cleared) after
+ * synchronising `stream`, into *error_bits; with clear != 0 a non-zero word
+ * is then zeroed on `stream`.  Synchronises, so not for use under capture.
+ * No counterpart in the reference; for callers that cannot allocate.
+ */
+int aoakv_noalloc_error(uint32_t* error_bits, uint32_t clear, void* stream);
 
 /*
  * estimate + top-k in one launch (the first launch of

@@ -92,10 +92,10 @@ def test_validation_errors_without_gpu():
                                        qk | _lib.FLAG_FIXED, nul)
     assert rc == _lib.AOAKV_ERR_INVALID and b"QUEST_KERNEL" in lib.aoakv_last_error()
     rc = lib.aoakv_topk_filtering(1, 64, 1, 1, 1, 1024, nul, 1, 64, 1, 32, 16,
-                                  qk | _lib.FLAG_FIXED, nul)
+                                  qk | _lib.FLAG_FIXED, nul, nul)
     assert rc == _lib.AOAKV_ERR_INVALID and b"QUEST_KERNEL" in lib.aoakv_last_error()
     # unknown flag bits
-    rc = lib.aoakv_topk_filtering(1, 64, 1, 1, 1, 1024, nul, 1, 64, 1, 32, 16, 16, nul)
+    rc = lib.aoakv_topk_filtering(1, 64, 1, 1, 1, 1024, nul, 1, 64, 1, 32, 16, 16, nul, nul)
     assert rc == _lib.AOAKV_ERR_INVALID and b"unknown flags" in lib.aoakv_last_error()
     rc = lib.aoakv_decode_sparse_attn(1, 1, 1, 1, 1, 1, 1, 128, 2048, nul, 1, 1 << 30, 1, 2048,
                                       32, 32, 128, 16, 1, 2, nul)
@@ -109,7 +109,7 @@ def test_validation_errors_without_gpu():
                                        qk | _lib.FLAG_VALUE_AWARE, nul)
     assert rc == _lib.AOAKV_ERR_INVALID and b"score_stride" in lib.aoakv_last_error()
     # prefill attention reports its own status
-    rc = lib.aoakv_topk_filtering(nul, 64, 1, 1, 1, 1024, nul, 1, 64, 1, 32, 16, 2, nul)
+    rc = lib.aoakv_topk_filtering(nul, 64, 1, 1, 1, 1024, nul, 1, 64, 1, 32, 16, 2, nul, nul)
     assert rc == _lib.AOAKV_ERR_INVALID
 
 
@@ -185,3 +185,6 @@ def test_noalloc_entry_point_rejects_without_gpu():
     assert rc == _lib.AOAKV_ERR_INVALID and b"two-launch" in lib.aoakv_last_error()
     rc = lib.aoakv_sparse_decode_layer_noalloc(*args, _lib.FLAG_VALUE_AWARE, None)
     assert rc == _lib.AOAKV_ERR_INVALID and b"scratch" in lib.aoakv_last_error()
+    # the error-word reader needs somewhere to put the bits
+    rc = lib.aoakv_noalloc_error(None, 1, None)
+    assert rc == _lib.AOAKV_ERR_INVALID and b"error_bits" in lib.aoakv_last_error()

@@ -621,6 +621,20 @@ def test_page_table_longer_than_max_pages_is_flagged(single):
         outs.append((o, ops.workspace_error(ws)))
     assert outs[0][1] == 0 and outs[1][1] == ops.WS_ERR_TRUNCATED
     assert torch.equal(outs[0][0], outs[1][0])
+    # standalone top-k over the 200-entry score rows: the 300-page table is
+    # cut to the row (the 200-page table's selection) and, given a
+    # workspace, flagged in its error word
+    if not single:
+        sels = []
+        for P_table in (Pmax, Pdev):
+            ws = ops.decode_workspace(1, H, H, k, DEV)
+            sel = torch.full((1, H, k), -1, dtype=torch.int32, device=DEV)
+            ops.topk_filtering(sc_ref, t([0, P_table]), idx, lpl, budget, sel, S, ops.FLAG_FIXED,
+                               workspace=ws)
+            torch.cuda.synchronize()
+            sels.append((sel, ops.workspace_error(ws)))
+        assert sels[0][1] == 0 and sels[1][1] == ops.WS_ERR_TRUNCATED
+        assert torch.equal(sels[0][0], sel_ref) and torch.equal(sels[1][0], sel_ref)
 
 
 def test_one_launch_refuses_a_workspace_whose_wait_flag_is_set():

@@ -89,3 +89,68 @@ def test_noalloc_layer_rejects_single_launch_and_oversized_calls():
     big = (q32, torch.empty_like(q32)) + args[2:10] + (big_scores, big_sel, 131072)
     with pytest.raises(AoakvError, match="scratch"):
         ops.sparse_decode_layer_noalloc(*big, 16384, HND, ops.FLAG_VALUE_AWARE)
+
+
+def test_noalloc_error_word_and_graph_capture():
+    """The scratch error word: a device page table of 300 pages passed with
+    max_pages = 200 sets AOAKV_WS_ERR_TRUNCATED, which aoakv_noalloc_error
+    reads and clears.  Then the entry point captured into a HIP graph (after
+    aoakv_noalloc_init, outside capture) and replayed three times, with
+    eager calls of the workspace path between the replays: every replay
+    gives the workspace path's bits."""
+    import aoakv  # noqa: F401
+    from aoakv import ops
+    F = ops.FLAG_VALUE_AWARE | ops.FLAG_FIXED
+    H, L, budget, Pmax = 8, 300 * S - 5, 1024, 200
+    _say("[no-alloc] error word: 300-page table, max_pages 200")
+    ops.noalloc_init()
+    ops.noalloc_error(clear=True)          # whatever earlier calls left
+    c, q = _layer_inputs(H, L, budget, HND, 14)
+    t = lambda a: torch.tensor(a, dtype=torch.int32, device=DEV)
+    k = min(max(3, budget // S), Pmax)
+
+    def bufs():
+        return (torch.full_like(q, float("nan")),
+                torch.zeros((1, H, Pmax), dtype=torch.float32, device=DEV),
+                torch.full((1, H, k), -1, dtype=torch.int32, device=DEV))
+
+    def args(o, scores, sel, P_table):
+        return (q, o, c.kv_cache.buf_layer(0), t([0, P_table]), c.kv_indices_with_last,
+                c.kv_last_page_len_t, c.metadata_cache.buf_layer(0), t([0, -(-P_table // S)]),
+                c.metadata_indices, c.v_log_norm_layer(0), scores, sel, budget)
+
+    outs = []
+    for P_table in (Pmax, 300):
+        o, scores, sel = bufs()
+        ops.sparse_decode_layer_noalloc(*args(o, scores, sel, P_table), Pmax, HND, F)
+        outs.append((o, scores, sel, ops.noalloc_error()))
+    assert outs[0][3] == 0 and outs[1][3] == ops.WS_ERR_TRUNCATED
+    for a, b in zip(outs[0][:3], outs[1][:3]):
+        assert torch.equal(a, b)            # cut to the first 200 pages
+    assert ops.noalloc_error(clear=True) == ops.WS_ERR_TRUNCATED
+    assert ops.noalloc_error() == 0
+
+    _say("[no-alloc] graph capture, three replays")
+    ws = ops.decode_workspace(1, H, H, k, DEV)
+    o_ref, sc_ref, sel_ref = bufs()
+    ops.sparse_decode_layer(*args(o_ref, sc_ref, sel_ref, Pmax), ws, Pmax, HND, F)
+    torch.cuda.synchronize()
+    o, scores, sel = bufs()
+    a = args(o, scores, sel, Pmax)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.sparse_decode_layer_noalloc(*a, Pmax, HND, F)
+    for rep in range(3):
+        o.fill_(float("nan"))
+        scores.zero_()
+        sel.fill_(-1)
+        o2, sc2, sel2 = bufs()               # eager work between replays
+        ops.sparse_decode_layer(*args(o2, sc2, sel2, Pmax), ws, Pmax, HND, F)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o, o_ref) and torch.equal(sel, sel_ref), rep
+        assert torch.equal(scores.view(torch.int32), sc_ref.view(torch.int32)), rep
+        assert torch.equal(o2, o_ref), rep
+    assert ops.noalloc_error() == 0
+    del g
