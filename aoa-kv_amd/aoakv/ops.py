@@ -206,12 +206,18 @@ def topk_filtering(scores, kv_indptr, kv_indices, kv_last_page_len, token_budget
 
 
 def decode_workspace(batch: int, num_qo_heads: int, num_kv_heads: int, max_sel_pages: int,
-                     device="cuda", max_pages: int = 0) -> torch.Tensor:
+                     device="cuda", max_pages: int = 0, head_dim: int = 128,
+                     page_size: int = 16) -> torch.Tensor:
     """Caller-owned decode workspace (replaces BatchDecodeHandler's buffers,
     decode_handler.cuh:73-136), zeroed.  With max_pages it also holds the
-    one-launch layer's score handoff words (aoakv_layer_workspace_size)."""
+    one-launch layer's score handoff words (aoakv_layer_workspace_size).
+    Shapes other than head_dim 128 / page_size 16 run the generic kernels,
+    which use only the workspace's control words (aoakv.h
+    AOAKV_WORKSPACE_CTL_BYTES)."""
     lib = _lib.load()
-    if max_pages:
+    if (head_dim, page_size) != (128, 16):
+        n = WORKSPACE_CTL_BYTES
+    elif max_pages:
         n = lib.aoakv_layer_workspace_size(batch, num_qo_heads, num_kv_heads, 128, max_sel_pages,
                                            max_pages)
     else:
@@ -221,6 +227,8 @@ def decode_workspace(batch: int, num_qo_heads: int, num_kv_heads: int, max_sel_p
     return ws
 
 
+# bytes of a workspace's control words (aoakv.h AOAKV_WORKSPACE_CTL_BYTES)
+WORKSPACE_CTL_BYTES = 256
 # the workspace error word (aoakv.h AOAKV_WS_ERR_WORD) and its bits
 WS_ERR_WORD = 2
 WS_ERR_WAIT = 1

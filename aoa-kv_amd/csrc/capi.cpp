@@ -149,6 +149,9 @@ struct Workspace {
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// the control words at the start of every workspace (64 u32)
+constexpr size_t kCtlBytes = 256;
+
 // [ctl: 64 u32][est counters: B*Hkv lines][dec counters: B*Hq lines]
 // [partials: B*Hq*chunks*stride f32][hsel: B*Hq*max_sel u32]
 // [hpart: B*Hq*chunks*stride u32]; every region 256-byte aligned.  The
@@ -161,7 +164,7 @@ size_t ws_layout(uint32_t B, uint32_t hq, uint32_t hkv, uint32_t max_sel_pages, 
                  Workspace* w) {
   const size_t part =
       (size_t)B * hq * aoakv::decode_chunks(max_sel_pages) * aoakv::partial_stride() * 4u;
-  const size_t off_est = 256;
+  const size_t off_est = kCtlBytes;
   const size_t cnt = (size_t)aoakv::counter_stride() * 4u;  // bytes per counter
   const size_t off_dec = off_est + round_up((size_t)B * hkv * cnt, 256);
   const size_t off_part = off_dec + round_up((size_t)B * hq * cnt, 256);
@@ -179,6 +182,20 @@ size_t ws_layout(uint32_t B, uint32_t hq, uint32_t hkv, uint32_t max_sel_pages, 
     w->bytes = total;
   }
   return total;
+}
+
+// Workspace bytes a decode call needs (and, with w, its layout over base):
+// the full layout for the tuned kernels, the control words alone for the
+// generic ones, which keep no counters or partials.
+size_t decode_ws_bytes(bool tuned, uint32_t B, uint32_t hq, uint32_t hkv, uint32_t max_sel_pages,
+                       void* base, Workspace* w) {
+  if (tuned) return ws_layout(B, hq, hkv, max_sel_pages, base, w);
+  if (w) {
+    *w = Workspace{};
+    w->ctl = static_cast<uint32_t*>(base);
+    w->bytes = kCtlBytes;
+  }
+  return kCtlBytes;
 }
 
 // Scores + top-k: one fused launch when every sequence fits the fused
@@ -585,10 +602,15 @@ static int fill_decode(aoakv::DecodeArgs& a, Workspace& w, const void* q, void* 
                                         max_pages, page_size, flags);
   REQUIRE(!sel_pages || sel_stride >= min_sel_stride(flags), "decode_sparse_attn: sel_stride %u < %u",
           sel_stride, min_sel_stride(flags));
-  REQUIRE(aoakv::decode_chunks(max_sel) <= aoakv::decode_max_chunks(),
+  // the tuned kernels split each head's pages over chunks merged through the
+  // workspace; the generic ones (one workgroup per query head) use only its
+  // control words and take any number of pages
+  const bool tuned = aoakv::tuned_shape(head_dim, page_size);
+  REQUIRE(!tuned || aoakv::decode_chunks(max_sel) <= aoakv::decode_max_chunks(),
           "decode_sparse_attn: %u pages per head exceed the %u the split-K merge holds", max_sel,
           aoakv::decode_max_chunks() * 8u);
-  const size_t need = ws_layout(batch_size, num_qo_heads, num_kv_heads, max_sel, workspace, &w);
+  const size_t need =
+      decode_ws_bytes(tuned, batch_size, num_qo_heads, num_kv_heads, max_sel, workspace, &w);
   REQUIRE(workspace_bytes >= need, "decode_sparse_attn: workspace of %zu bytes < %zu needed",
           workspace_bytes, need);
   a.q = static_cast<const aoakv::f16*>(q);
@@ -606,14 +628,13 @@ static int fill_decode(aoakv::DecodeArgs& a, Workspace& w, const void* q, void* 
   a.Hq = num_qo_heads;
   a.Hkv = num_kv_heads;
   a.S = page_size;
-  a.max_chunks = aoakv::decode_chunks(max_sel);
+  a.max_chunks = tuned ? aoakv::decode_chunks(max_sel) : 0u;
   a.max_pages = max_pages;
   a.flags = flags & AOAKV_FLAG_QUEST_KERNEL;
   // grouped decode only where it changes anything (a group of 2 or more) and
   // the tuned kernels run (the generic ones serve one query head each)
-  a.heads_per_item = (flags & AOAKV_FLAG_GROUPED_DECODE) && aoakv::tuned_shape(head_dim, page_size)
-                         ? num_qo_heads / num_kv_heads
-                         : 1u;
+  a.heads_per_item =
+      (flags & AOAKV_FLAG_GROUPED_DECODE) && tuned ? num_qo_heads / num_kv_heads : 1u;
   a.g = aoakv::make_geom(layout, num_kv_heads, page_size, head_dim);
   a.error = w.ctl + aoakv::kErrWord;
   return AOAKV_OK;
@@ -747,7 +768,8 @@ int aoakv_sparse_decode_layer_noalloc(
   // the decode workspace this call lays out must fit the scratch array
   const uint32_t max_sel = max_selected(sel_pages, sel_stride, token_budget, token_budgets,
                                         max_pages, page_size, flags);
-  const size_t need = ws_layout(batch_size, num_qo_heads, num_kv_heads, max_sel, nullptr, nullptr);
+  const size_t need = decode_ws_bytes(aoakv::tuned_shape(head_dim, page_size), batch_size,
+                                      num_qo_heads, num_kv_heads, max_sel, nullptr, nullptr);
   REQUIRE(need <= kNoAllocScratchBytes,
           "sparse_decode_layer_noalloc: this call needs %zu bytes of scratch, more than the "
           "%zu the library holds per device (batch %u x %u query heads x %u selected pages)",
@@ -810,7 +832,8 @@ int aoakv_estimate_topk(const void* q, const void* metadata_data, const int32_t*
     return e;
   Workspace w{};
   const uint32_t max_sel = sel_stride < max_pages ? sel_stride : max_pages;
-  const size_t need = ws_layout(batch_size, num_qo_heads, num_kv_heads, max_sel, workspace, &w);
+  const size_t need = decode_ws_bytes(aoakv::tuned_shape(head_dim, page_size), batch_size,
+                                      num_qo_heads, num_kv_heads, max_sel, workspace, &w);
   REQUIRE(workspace_bytes >= need, "estimate_topk: workspace of %zu bytes < %zu needed",
           workspace_bytes, need);
   ea.error = w.ctl + aoakv::kErrWord;

@@ -122,6 +122,9 @@ extern "C" {
  *                           selection and output were computed on its first
  *                           pages only.  No access leaves the sized buffers. */
 #define AOAKV_WS_ERR_WORD 2u
+/* Bytes of the control words at the start of every workspace (the error
+ * word among them). */
+#define AOAKV_WORKSPACE_CTL_BYTES 256u
 #define AOAKV_WS_ERR_WAIT 1u
 #define AOAKV_WS_ERR_TRUNCATED 2u
 
@@ -267,7 +270,12 @@ int aoakv_topk_filtering(const float* scores, uint32_t score_stride,
  * Bytes of the caller-owned workspace for aoakv_decode_sparse_attn and
  * aoakv_sparse_decode_layer (replaces the buffers BatchDecodeHandler
  * allocates in begin_forward, reference decode_handler.cuh:73-136).
- * max_sel_pages: upper bound on pages attended per (sequence, head).
+ * max_sel_pages: upper bound on pages attended per (sequence, head).  The
+ * size covers the tuned kernels (head_dim 128, page_size 16), which split a
+ * head's pages into chunks of 8 merged through the workspace (at most 8192
+ * pages per head); the other shapes run kernels that keep one workgroup per
+ * query head, take any number of pages and use only the first
+ * AOAKV_WORKSPACE_CTL_BYTES of a workspace.
  */
 size_t aoakv_decode_workspace_size(uint32_t batch_size, uint32_t num_qo_heads,
                                    uint32_t num_kv_heads, uint32_t head_dim,

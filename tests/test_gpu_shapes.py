@@ -150,6 +150,111 @@ def test_decode_matches_simulation(D, S, layout, group, value_aware):
     assert np.abs(od.astype(np.float32) - dref[0, :, 0].astype(np.float32)).max() <= 2e-3
 
 
+@pytest.mark.parametrize("D,S,layout,group,value_aware", [
+    (64, 16, HND, 1, True), (256, 32, NHD, 1, False), (128, 8, HND, 2, True),
+    (128, 1, NHD, 1, True), (64, 7, HND, 4, True)])
+def test_quest_kernel_convention_matches_oracle(D, S, layout, group, value_aware):
+    """AOAKV_FLAG_QUEST_KERNEL through the generic kernels: P - 1 pages
+    scored (the last one is not), the k - 1 best of them selected, the last
+    page attended after them; against the oracle's quest_kernel_pages, as
+    test_gpu_quest_kernel.py does for (128, 16).  The three calls, the fused
+    layer call and its one-launch flag give the same bits."""
+    from aoakv.utils import (InferenceController, decode_estimate, decode_layer,
+                             decode_sparse_attn, decode_topk)
+    _say(f"[shapes] quest_kernel D={D} S={S} layout={layout} group={group} va={value_aware}")
+    Hkv, pb = 4, 23
+    Hq = Hkv * group
+    L = 40 * S + 5 if S > 1 else 300
+    K = randn16(D * 5 + S, (1, Hkv, L, D))
+    V = randn16(D * 5 + S + 1, (1, Hkv, L, D))
+    q = randn16(D * 5 + S + 2, (1, Hq, 1, D))
+    c = InferenceController(1, Hq, D, S, pb, L + S, torch.float16, DEV, layout=layout,
+                            num_kv_heads=Hkv, value_aware=value_aware, shuffle_seed=S + 9,
+                            semantics="quest_kernel")
+    _prefill(c, K[:, :, :-1], V[:, :, :-1])
+    c.end_forward()
+    _append(c, K[:, :, -1:], V[:, :, -1:])
+    st = sim.SimLayerState(K[:, :, :-1], V[:, :, :-1], S)
+    o_ref, sc_ref, pg_ref = sim.decode_step(st, q, K[:, :, -1:], V[:, :, -1:], pb * S,
+                                            fixed=False, value_aware=value_aware,
+                                            num_key_value_groups=group, semantics="quest_kernel")
+    P = math.ceil(L / S)
+    k = min(pb, P)
+    assert c.need_estimate() and c.num_selected_pages() == k < P
+    qd = torch.from_numpy(q[0, :, 0].copy()).to(DEV)[None]
+    scores = decode_estimate(qd, c, 0).cpu().numpy()
+    assert scores.shape == (Hkv, P - 1)                  # the last page is not scored
+    np.testing.assert_allclose(scores, sc_ref[0, :, 0, :P - 1], rtol=2e-6, atol=2e-5)
+    sel = decode_topk(c.scores[0, :, :P - 1], c).cpu().numpy()
+    assert sel.shape == (Hkv, k - 1)
+    inv = {p: i for i, p in enumerate(c.kv_cache.indicies)}
+    mine = np.array([[inv[int(x)] for x in row] for row in sel])
+    exact = True
+    for h in range(Hkv):
+        got = np.append(mine[h], P - 1)
+        ok, why = sim.selection_matches(got, pg_ref[0, h, 0], sc_ref[0, h, 0], forced={P - 1})
+        assert ok, (h, why)
+        assert P - 1 not in set(mine[h].tolist())
+        exact &= why == "exact"
+    o = decode_sparse_attn(qd, c, 0, c.topk_dindices_buffer).cpu().numpy()[0]
+    pages = np.concatenate([mine, np.full((Hkv, 1), P - 1)], axis=1)
+    mask = np.repeat(sim.pages_to_token_mask(pages[None, :, None], S, L), group, 1)
+    ref = sim.masked_decode_attention(q, np.repeat(st.K, group, 1), np.repeat(st.V, group, 1),
+                                      mask)[0, :, 0]
+    assert np.abs(o.astype(np.float32) - ref.astype(np.float32)).max() <= 2e-3
+    if exact:
+        assert np.abs(o.astype(np.float32) - o_ref[0, :, 0].astype(np.float32)).max() <= 2e-3
+    for single in (False, True):
+        c.topk_dindices_buffer.fill_(-1)
+        o1 = decode_layer(qd, c, 0, single_launch=single).cpu().numpy()[0]
+        assert np.array_equal(bits(o1), bits(o)), single
+        assert np.array_equal(c.topk_dindices_buffer.cpu().numpy()[0], sel), single
+    from aoakv import ops
+    assert ops.workspace_error(c.workspace) == 0
+
+
+@pytest.mark.parametrize("D,S,layout", [(128, 1, HND), (64, 4, NHD)])
+def test_decode_beyond_the_split_k_limit(D, S, layout):
+    """10000 pages per head, 9000 of them selected: more than the 8192 pages
+    per head the tuned kernels' split-K merge holds.  The generic kernels,
+    one workgroup per query head, take them with a workspace of only its
+    control words; sparse and dense decode against the oracle."""
+    from aoakv import ops
+    from aoakv.utils import decode_estimate, decode_layer, decode_sparse_attn, decode_topk
+    _say(f"[shapes] beyond split-K D={D} S={S} layout={layout}")
+    H, P, k = 2, 10000, 9000
+    L = (P - 1) * S + 1
+    K = randn16(D + 71, (1, H, L, D))
+    V = randn16(D + 72, (1, H, L, D))
+    q = randn16(D + 73, (1, H, 1, D))
+    c = _ctrl(H, D, S, L + S, layout, k * S, shuffle=S + 3)
+    assert c.workspace.numel() == ops.WORKSPACE_CTL_BYTES
+    _prefill(c, K, V)
+    c.begin_forward(1)
+    st = sim.SimLayerState(K, V, S)
+    qd = torch.from_numpy(q[0, :, 0].copy()).to(DEV)[None]
+    assert c.need_estimate() and c.num_selected_pages() == k
+    scores = decode_estimate(qd, c, 0).cpu().numpy()
+    sc_ref, pg_ref = sim.select_pages(st, q, k * S, True, True, 1)
+    np.testing.assert_allclose(scores, sc_ref[0, :, 0], rtol=2e-6, atol=2e-5)
+    decode_topk(c.scores[0, :, :P], c)
+    sel = c.topk_dindices_buffer[0].cpu().numpy()
+    inv = {p: i for i, p in enumerate(c.kv_cache.indicies)}
+    mine = np.array([[inv[int(x)] for x in row] for row in sel])
+    for h in range(H):
+        ok, why = sim.selection_matches(mine[h], pg_ref[0, h, 0], sc_ref[0, h, 0], True)
+        assert ok, (h, why)
+    o = decode_sparse_attn(qd, c, 0, c.topk_dindices_buffer).cpu().numpy()[0]
+    ref = sim.sparse_decode_attention(q, st.K, st.V, mine[None, :, None, :], S, L)
+    assert np.abs(o.astype(np.float32) - ref[0, :, 0].astype(np.float32)).max() <= 2e-3
+    o1 = decode_layer(qd, c, 0).cpu().numpy()[0]
+    assert np.array_equal(bits(o1), bits(o))
+    od = decode_sparse_attn(qd, c, 0, None).cpu().numpy()[0]
+    dref = sim.masked_decode_attention(q, st.K, st.V, None)
+    assert np.abs(od.astype(np.float32) - dref[0, :, 0].astype(np.float32)).max() <= 2e-3
+    assert ops.workspace_error(c.workspace) == 0
+
+
 @pytest.mark.parametrize("D,S,layout", [(64, 16, HND), (256, 16, NHD), (128, 8, NHD),
                                         (128, 32, HND), (128, 1, HND), (256, 7, HND)])
 @pytest.mark.parametrize("L,Lq,group", [(300, 300, 1), (333, 70, 2)])
