@@ -726,10 +726,11 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
       la.e.hscore = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + words_off);
       la.e.hscore_stride = max_pages;
     }
-    la.est_chunks = aoakv::est_chunks(max_pages);
+    const uint32_t group = num_qo_heads / num_kv_heads;
+    la.est_chunks = aoakv::est_chunks(max_pages, group);
     la.n_est = batch_size * num_kv_heads * la.est_chunks;
     la.n_workers = aoakv::layer_score_workers(la.n_est, la.est_chunks);
-    la.stagger_ps = aoakv::layer_stagger_ps(la.est_chunks);
+    la.stagger_ps = aoakv::layer_stagger_ps(la.est_chunks, group, batch_size * num_kv_heads);
     la.n_dec = batch_size * (num_qo_heads / da.heads_per_item) * da.max_chunks;
     // score words and the whole launch resident at once: each decode item
     // selects its kv head's pages itself (no top-k workgroups, no selection

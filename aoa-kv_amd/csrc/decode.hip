@@ -25,6 +25,29 @@ namespace aoakv {
 constexpr int kThreads = 256;
 constexpr int kEstPagesPerWave = 32;                     // 8 steps x 4 rows
 constexpr int kEstPagesPerBlock = kEstPagesPerWave * 4;  // 128
+// Pages per scoring item: with a GQA group of G query heads a page costs G
+// bounds, so an item takes 128 / G pages (the same arithmetic per item, G
+// times the items to spread over the CUs).
+template <int GROUP>
+constexpr uint32_t est_block_pages() {
+  return (uint32_t)kEstPagesPerBlock / (uint32_t)GROUP;
+}
+__host__ __device__ constexpr uint32_t est_block_pages_of(uint32_t group) {
+  return (uint32_t)kEstPagesPerBlock / group;
+}
+// Items of the scoring kernel without the fused top-k (the three-call
+// path's estimate): half as large at GROUP = 1, so each CU holds more items'
+// dependent page-table and metadata chains in flight (config 2: 9.0 against
+// 10.6 us; a quarter as large: 9.1).  The fused kernel keeps 128 pages: its
+// last item per head selects, and with twice the items that tail grew (14.1
+// against 13.7 us).  The page scores do not depend on the item size.
+template <int GROUP, bool FUSED>
+constexpr uint32_t est_kernel_block_pages() {
+  return GROUP == 1 && !FUSED ? est_block_pages<1>() / 2u : est_block_pages<GROUP>();
+}
+__host__ __device__ constexpr uint32_t est_kernel_block_pages_of(uint32_t group, bool fused) {
+  return group == 1u && !fused ? est_block_pages_of(1u) / 2u : est_block_pages_of(group);
+}
 constexpr int kDecPagesPerWave = 2;
 constexpr int kDecPagesPerBlock = kDecPagesPerWave * 4;  // 8
 constexpr int kPartialStride = kHeadDim + 4;             // o[128], m, l, pad
@@ -549,9 +572,9 @@ constexpr uint32_t kFusedTopkMaxPages = kStageMaxPages;
 // page scores (+ optional fused top-k)
 // ======================================================================
 
-// Grid (page chunks of 128, kv heads, batch); a wave scores 32 consecutive
-// pages = two metadata pages (page_size 16), so its metadata page indices
-// are two scalar loads.
+// Grid (page chunks of 128 / GROUP, kv heads, batch); a wave scores 32 /
+// GROUP consecutive pages, one or (GROUP = 1) two metadata pages (page_size
+// 16), so its metadata page indices are one or two scalar loads.
 struct EstShared {
   float sc[kEstPagesPerBlock];
   uint32_t last;
@@ -580,11 +603,11 @@ __device__ inline uint32_t est_pages(const EstimateArgs& a, uint32_t b, uint32_t
   return P;
 }
 
-// Scores pages [128*chunk, 128*chunk + 128) of (sequence b, kv head h) and
-// stores them (agent-coherent).  Returns false, uniformly, when the chunk
+// Scores pages [n*chunk, n*chunk + n) of (sequence b, kv head h), n =
+// est_block_pages<GROUP>(), and stores them (agent-coherent).  Returns false, uniformly, when the chunk
 // holds no page.  A sequence whose page table exceeds what the call covers
 // sets kErrTruncated (once, from its first chunk).
-template <int GROUP>
+template <int GROUP, uint32_t kPPB = est_block_pages<GROUP>()>
 __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, uint32_t h,
                                            uint32_t chunk, EstShared& sm) {
   float* s_sc = sm.sc;
@@ -595,7 +618,10 @@ __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, ui
   uint32_t pbeg;
   bool clamped;
   const uint32_t P = est_pages(a, b, &pbeg, &clamped);
-  if (chunk * kEstPagesPerBlock >= P) return false;  // uniform per block
+  constexpr uint32_t kPPW = kPPB / 4u;  // pages per wave: 32, 16, 8 or 4
+  static_assert(kPPW % 4u == 0u && kPageSize % kPPW == 0u || kPPW == 2u * kPageSize,
+                "a wave's pages lie in one or two metadata pages");
+  if (chunk * kPPB >= P) return false;  // uniform per block
   if (clamped && chunk == 0u && threadIdx.x == 0u) flag_error(a.error, kErrTruncated);
   const uint32_t mbeg = (uint32_t)a.meta_indptr[b];
   const uint32_t d0 = l16 * kVec;
@@ -607,16 +633,17 @@ __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, ui
   // make the compiler wait for it before issuing the next one.  Issue order:
   // the page id for the value statistic, the metadata page ids, q, the 16
   // metadata vectors, then the value statistic (used only after scoring).
-  const uint32_t pblk = chunk * kEstPagesPerBlock;  // < P
-  const uint32_t page0 = pblk + wave * kEstPagesPerWave;
-  uint32_t pj = page0 + (lane % (uint32_t)kEstPagesPerWave);  // lane j: page page0 + j % 32
+  const uint32_t pblk = chunk * kPPB;  // < P
+  const uint32_t page0 = pblk + wave * kPPW;
+  uint32_t pj = page0 + (lane % kPPW);  // lane j: page page0 + j % kPPW
   pj = pj < P ? pj : P - 1u;
   const uint32_t phys_j = (uint32_t)a.kv_indices[pbeg + pj];
   __builtin_amdgcn_sched_barrier(0);  // keep the issue order written here
   const uint32_t pl0 = page0 < P ? page0 : pblk;  // a live page of the wave's first half
   const uint32_t pl1 = pl0 + kPageSize < P ? pl0 + kPageSize : pl0;
   const uint32_t mp0 = (uint32_t)a.meta_indices[mbeg + pl0 / kPageSize];
-  const uint32_t mp1 = (uint32_t)a.meta_indices[mbeg + pl1 / kPageSize];
+  const uint32_t mp1 =
+      kPPW > kPageSize ? (uint32_t)a.meta_indices[mbeg + pl1 / kPageSize] : mp0;
 
   // Per dim, the larger of q*Kmax and q*Kmin is q*Kmax where q >= 0 and
   // q*Kmin where q < 0 (Kmax >= Kmin; fp16 products are exact in fp32).  So
@@ -636,12 +663,13 @@ __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, ui
     }
   }
 
-  constexpr int kSteps = kEstPagesPerWave / 4;
+  constexpr int kSteps = (int)kPPW / 4;
   H8 kmx[kSteps], kmn[kSteps];
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
-    const uint32_t mp = s < kSteps / 2 ? mp0 : mp1;
-    const size_t off = elem_off(a.g, mp, 0, h, (s * 4 + row) % kPageSize) + d0;
+    // page page0 + 4s + row: its metadata page and slot
+    const uint32_t mp = (uint32_t)(s * 4) < kPageSize ? mp0 : mp1;
+    const size_t off = elem_off(a.g, mp, 0, h, (page0 + s * 4 + row) % kPageSize) + d0;
     kmx[s] = ld16(a.meta + off);
     kmn[s] = ld16(a.meta + off + a.g.kv);
   }
@@ -693,14 +721,14 @@ __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, ui
   for (int s = 0; s < kSteps; ++s) {
     float score = sc[s];
     if (value_aware) score = score + 2.0f * __shfl(lvn_lane, s * 4 + (int)row);
-    if (l16 == 0u) s_sc[wave * kEstPagesPerWave + s * 4 + row] = score;
+    if (l16 == 0u) s_sc[wave * kPPW + s * 4 + row] = score;
   }
   __syncthreads();
   float* out = a.scores + ((size_t)b * a.Hkv + h) * a.score_stride;
   {
-    const uint32_t p = chunk * kEstPagesPerBlock + threadIdx.x;
+    const uint32_t p = chunk * kPPB + threadIdx.x;
     const uint32_t nstore = (a.flags & kFlagQuestKernel) ? P - 1u : P;
-    if (threadIdx.x < (uint32_t)kEstPagesPerBlock && p < nstore) {
+    if (threadIdx.x < kPPB && p < nstore) {
       st_agent(out + p, s_sc[threadIdx.x]);
       if (a.hscore != nullptr)
         st_agent_u32(a.hscore + ((size_t)b * a.Hkv + h) * a.hscore_stride + p,
@@ -760,16 +788,17 @@ __device__ __forceinline__ void select_item(const EstimateArgs& a, uint32_t b, u
 
 // Scores one chunk; with a.sel set, the last block of the head to finish
 // also selects its pages (arrival counter per head).
-template <int GROUP>
+template <int GROUP, bool FUSED>
 __device__ __forceinline__ void estimate_item(const EstimateArgs& a, uint32_t b, uint32_t h,
                                               uint32_t chunk, EstShared& sm, TopkShared* tk) {
   // the fused top-k's shape, loaded up front (off the handoff path)
   SelPlan plan{};
   if (a.sel != nullptr) plan = plan_select(a, b);
-  if (!score_item<GROUP>(a, b, h, chunk, sm)) return;
+  constexpr uint32_t kPPB = est_kernel_block_pages<GROUP, FUSED>();
+  if (!score_item<GROUP, kPPB>(a, b, h, chunk, sm)) return;
   if (a.sel == nullptr) return;
   uint32_t pbeg;
-  const uint32_t nch = (est_pages(a, b, &pbeg) + kEstPagesPerBlock - 1) / kEstPagesPerBlock;
+  const uint32_t nch = (est_pages(a, b, &pbeg) + kPPB - 1u) / kPPB;
   if (!arrive_last(&a.counters[(b * a.Hkv + h) * kCounterStride], nch, &sm.last)) return;
   select_item<GROUP>(a, b, h, plan, *tk);
 }
@@ -778,11 +807,11 @@ template <int GROUP, bool FUSED>
 __global__ __launch_bounds__(kThreads) void estimate_kernel(EstimateArgs a) {
   if constexpr (FUSED) {
     __shared__ EstTopkShared sm;
-    estimate_item<GROUP>(a, blockIdx.z, blockIdx.y, blockIdx.x, sm.e, &sm.tk);
+    estimate_item<GROUP, true>(a, blockIdx.z, blockIdx.y, blockIdx.x, sm.e, &sm.tk);
   } else {
     __shared__ EstShared sm;
     a.sel = nullptr;
-    estimate_item<GROUP>(a, blockIdx.z, blockIdx.y, blockIdx.x, sm, nullptr);
+    estimate_item<GROUP, false>(a, blockIdx.z, blockIdx.y, blockIdx.x, sm, nullptr);
   }
 }
 
@@ -1498,7 +1527,7 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la)
     uint32_t pbeg;
     const uint32_t P = est_pages(la.e, b, &pbeg);
     if (P == 0u) return;
-    const uint32_t nch = (P + kEstPagesPerBlock - 1) / kEstPagesPerBlock;
+    const uint32_t nch = (P + est_block_pages<GROUP>() - 1u) / est_block_pages<GROUP>();
     const SelPlan plan = plan_select(la.e, b);
     if (threadIdx.x == 0u) s_err = err0;
     __syncthreads();
@@ -1561,8 +1590,9 @@ __global__ void fill_u32_kernel(uint32_t* p, size_t n, uint32_t v) {
 
 hipError_t launch_estimate(const EstimateArgs& a, uint32_t batch, uint32_t max_pages,
                            hipStream_t s) {
-  dim3 grid((max_pages + kEstPagesPerBlock - 1) / kEstPagesPerBlock, a.Hkv, batch);
   const bool fused = a.sel != nullptr;
+  const uint32_t ppb = est_kernel_block_pages_of(a.Hq / a.Hkv, fused);
+  dim3 grid((max_pages + ppb - 1u) / ppb, a.Hkv, batch);
   switch (a.Hq / a.Hkv) {
 #define AOAKV_EST(G)                                                                   \
   case G:                                                                              \
@@ -1609,8 +1639,9 @@ hipError_t launch_layer(const LayerArgs& la, hipStream_t s) {
   return hipGetLastError();
 }
 
-uint32_t est_chunks(uint32_t max_pages) {
-  return (max_pages + kEstPagesPerBlock - 1) / kEstPagesPerBlock;
+uint32_t est_chunks(uint32_t max_pages, uint32_t group) {
+  const uint32_t n = est_block_pages_of(group);
+  return (max_pages + n - 1u) / n;
 }
 
 hipError_t launch_topk(const TopkArgs& a, uint32_t batch, hipStream_t s) {
@@ -1659,9 +1690,14 @@ uint32_t fused_topk_max_pages() { return kFusedTopkMaxPages; }
 // handoff words), us per layer by workers: 416: 23.41, 448: 23.32, 464:
 // 23.24, 480: 23.16, 496: 24.01, 512: 23.71.  Between 256 (one per CU) and
 // 480 (with the 32 top-k and 512 decode workgroups of config 2, all 1024
-// workgroups that four per CU allow are resident together).
+// workgroups that four per CU allow are resident together).  With at most
+// kFewHeads (sequence, kv head) pairs, every item has a worker: a second
+// round would hold a quarter of the heads (GQA, 32 query / 8 kv heads, 64
+// items per head: 384 workers 15.8 us, 512 workers 15.4).
+constexpr uint32_t kFewHeads = 8u;
 uint32_t layer_score_workers(uint32_t n_est, uint32_t est_chunks) {
   if (n_est <= 256u) return n_est;
+  if (n_est <= 512u && n_est / est_chunks <= kFewHeads) return n_est;
   const uint32_t last_round = 2u * est_chunks;
   uint32_t w = n_est > last_round ? n_est - last_round : 256u;
   w = w < 256u ? 256u : w;
@@ -1678,11 +1714,15 @@ uint32_t layer_score_workers(uint32_t n_est, uint32_t est_chunks) {
 // offset holds whatever the clock.  Config 2 (16 chunks per head: 1.05 MB),
 // us per layer by bytes per ns: 5600: 24.06, 6100: 23.69, 6600: 23.35-23.39,
 // 7100: 23.20-23.26, 7600: 23.31, 8200: 23.49, 9000: 23.85 (the former
-// core-cycle stagger at its best, 376 cycles per head: 23.26).
-uint32_t layer_stagger_ps(uint32_t est_chunks) {
-  constexpr uint64_t kChunkBytes = kEstPagesPerBlock * (2u * kHeadDim * 2u + 2u);
+// core-cycle stagger at its best, 376 cycles per head: 23.26).  With at
+// most kFewHeads heads every head starts at once: their metadata is a short
+// stream whose heads all end in the same round (GQA above with 512 workers:
+// no stagger 15.1 us, 7,100 B/ns 15.4, 14,000 B/ns 15.4).
+uint32_t layer_stagger_ps(uint32_t est_chunks, uint32_t group, uint32_t heads) {
+  if (heads <= kFewHeads) return 0u;
+  const uint64_t chunk_bytes = est_block_pages_of(group) * (2u * kHeadDim * 2u + 2u);
   constexpr uint64_t kStreamBytesPerNs = 7100u;
-  return (uint32_t)((uint64_t)est_chunks * kChunkBytes * 1000u / kStreamBytesPerNs);
+  return (uint32_t)((uint64_t)est_chunks * chunk_bytes * 1000u / kStreamBytesPerNs);
 }
 uint32_t counter_stride() { return kCounterStride; }
 // Workgroups of the self-selecting layer kernel one CU holds at once (its LDS

@@ -177,7 +177,7 @@ struct LayerArgs {
   EstimateArgs e;      // with sel / counters / hsel of the top-k
   DecodeArgs d;        // with hsel / hpart / error
   uint32_t n_est;      // scoring items: B * Hkv * est_chunks
-  uint32_t est_chunks; // 128-page chunks per (sequence, head)
+  uint32_t est_chunks; // scoring items (128 / group pages each) per (sequence, kv head)
   uint32_t n_workers;  // scoring workgroups (<= n_est), items taken round-robin
   uint32_t n_heads;    // top-k workgroups: B * Hkv
   uint32_t n_dec;      // decode items: B * (Hq / d.heads_per_item) * d.max_chunks
@@ -192,7 +192,7 @@ hipError_t launch_estimate(const EstimateArgs& a, uint32_t batch, uint32_t max_p
                            hipStream_t s);
 hipError_t launch_topk(const TopkArgs& a, uint32_t batch, hipStream_t s);
 hipError_t launch_layer(const LayerArgs& la, hipStream_t s);
-uint32_t est_chunks(uint32_t max_pages);
+uint32_t est_chunks(uint32_t max_pages, uint32_t group);  // scoring items per (sequence, kv head)
 hipError_t launch_decode(const DecodeArgs& a, uint32_t batch, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s);
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t s);
@@ -212,7 +212,7 @@ uint32_t decode_max_chunks();  // split-K chunks per head the merge holds
 uint32_t topk_max_pages();     // pages per (sequence, head) top-k supports
 uint32_t fused_topk_max_pages();  // ... and the fused estimate + top-k kernel
 uint32_t layer_score_workers(uint32_t n_est, uint32_t est_chunks);  // one-launch layer scorers
-uint32_t layer_stagger_ps(uint32_t est_chunks);  // one-launch scoring start offset per head (ps)
+uint32_t layer_stagger_ps(uint32_t est_chunks, uint32_t group, uint32_t heads);  // one-launch scoring start offset per head (ps)
 uint32_t counter_stride();        // u32 words between per-head counters (one cache line each)
 uint32_t layer_self_blocks_per_cu(uint32_t group, uint32_t heads_per_item);  // per CU
 

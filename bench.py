@@ -306,18 +306,10 @@ def ragged_batch_bench(dev, layout, reps=20):
     return out
 
 
-def gqa_bench(dev, layout, n_layers=8, hq=32, hkv=8, launches=256):
-    """The GQA path (group-consistent selection, filter_util.py:351-368) at a
-    Llama-3-8B attention shape: 32 query heads over 8 kv heads x 128, the
-    config-2 context (32768 tokens, page 16) and budget (2048 tokens).
-    n_layers independent layers (1.1 GB, past the memory-side cache) are
-    replayed round-robin from a HIP graph: both decode paths, each with
-    per-query-head decode workgroups (the default) and with one workgroup per
-    kv head serving its group (AOAKV_FLAG_GROUPED_DECODE); all four must give
-    the same bits.  Bytes are the unique ones a layer must read: every page's
-    metadata and value statistic for the 8 kv heads, the selected pages' K/V
-    once per kv head (its 4 query heads share them), q, o and the
-    selection."""
+def gqa_inputs(dev, layout, n_layers=8, hq=32, hkv=8):
+    """Inputs of the GQA bench: n_layers independent layers of hq query heads
+    over hkv kv heads x 128 at the config-2 context and budget, and
+    layer(l, flags), one sparse_decode_layer call on layer l."""
     import torch
     from aoakv import ops
     Pm = math.ceil(P / S)
@@ -348,6 +340,29 @@ def gqa_bench(dev, layout, n_layers=8, hq=32, hkv=8, launches=256):
     sel = torch.zeros((n_layers, 1, hkv, K_SEL), dtype=torch.int32, device=dev)
     o = torch.zeros((n_layers, 1, hq, D), dtype=torch.float16, device=dev)
     ws = ops.decode_workspace(1, hq, hkv, K_SEL, dev, max_pages=P)
+
+    def layer(l, flags):
+        ops.sparse_decode_layer(q[l], o[l], kv[l], indptr, idx[l], lpl, meta[l], mindptr,
+                                midx, lvn[l], scores[l], sel[l], BUDGET, ws, P, layout, flags)
+    return {"o": o, "sel": sel, "ws": ws, "layer": layer}
+
+
+def gqa_bench(dev, layout, n_layers=8, hq=32, hkv=8, launches=256):
+    """The GQA path (group-consistent selection, filter_util.py:351-368) at a
+    Llama-3-8B attention shape: 32 query heads over 8 kv heads x 128, the
+    config-2 context (32768 tokens, page 16) and budget (2048 tokens).
+    n_layers independent layers (1.1 GB, past the memory-side cache) are
+    replayed round-robin from a HIP graph: both decode paths, each with
+    per-query-head decode workgroups (the default) and with one workgroup per
+    kv head serving its group (AOAKV_FLAG_GROUPED_DECODE); all four must give
+    the same bits.  Bytes are the unique ones a layer must read: every page's
+    metadata and value statistic for the 8 kv heads, the selected pages' K/V
+    once per kv head (its 4 query heads share them), q, o and the
+    selection."""
+    import torch
+    from aoakv import ops
+    G = gqa_inputs(dev, layout, n_layers, hq, hkv)
+    o, sel, ws = G["o"], G["sel"], G["ws"]
     nbytes = (hkv * P * (2 * D * 2 + 2) + hkv * K_SEL * S * D * 2 * 2 + hkv * K_SEL * 4 +
               2 * hq * D * 2)
     out = {"shape": f"{hq} query heads / {hkv} kv heads x {D}, {L} ctx, page {S}, budget {BUDGET}",
@@ -361,8 +376,7 @@ def gqa_bench(dev, layout, n_layers=8, hq=32, hkv=8, launches=256):
                         ("two_launch_grouped", base | grp),
                         ("one_launch_grouped", base | ops.FLAG_SINGLE_LAUNCH | grp)):
         def layer(l, flags=flags):
-            ops.sparse_decode_layer(q[l], o[l], kv[l], indptr, idx[l], lpl, meta[l], mindptr,
-                                    midx, lvn[l], scores[l], sel[l], BUDGET, ws, P, layout, flags)
+            G["layer"](l, flags)
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
@@ -544,14 +558,16 @@ TL_NAMES = ["start", "stagger_done", "scored0", "scored1", "scores_seen", "row_l
             "selected", "sel_in_hand", "attended", "partial", "merge_loaded", "output"]
 
 
-def timeline_pass(dev, layout, fn_layer, n_layers, samples=16, tick_ns=10.0, isolated=None):
-    """Per-phase timeline of the one-launch layer (config 2), from the
-    profiling build (AOAKV_LIB=aoa-kv_amd/aoakv/libaoakv_timeline.so).  Each
-    sample launch runs right behind a replay of the 32-layer graph, as in the
-    timed loop; its workgroups' phase timestamps (s_memrealtime, 100 MHz,
-    noted in LDS and written out as each workgroup ends) are read back and
-    reduced per head.  `isolated` kernels are timed the same way, alone
-    behind the replay.  Returns a dict (JSON)."""
+def timeline_pass(dev, layout, fn_layer, n_layers, samples=16, tick_ns=10.0, isolated=None,
+                  hq=None, hkv=None):
+    """Per-phase timeline of the one-launch layer (config 2, or hq query heads
+    over hkv kv heads), from the profiling build
+    (AOAKV_LIB=aoa-kv_amd/aoakv/libaoakv_timeline.so).  Each sample launch
+    runs right behind a replay of the n_layers graph, as in the timed loop;
+    its workgroups' phase timestamps (s_memrealtime, 100 MHz, noted in LDS
+    and written out as each workgroup ends) are read back and reduced per
+    query head.  `isolated` kernels are timed the same way, alone behind the
+    replay.  Returns a dict (JSON)."""
     import ctypes
     import numpy as np
     import torch
@@ -578,10 +594,17 @@ def timeline_pass(dev, layout, fn_layer, n_layers, samples=16, tick_ns=10.0, iso
             fn_layer(l)
     g.replay()
     torch.cuda.synchronize()
-    H_, E_ = H, 16          # heads, 128-page scoring chunks per head (config 2)
-    n_workers = 480 if H_ * E_ > 256 else H_ * E_
+    H_ = hq or H            # query heads
+    KV_ = hkv or H_         # kv heads
+    E_ = P // (128 // (H_ // KV_))  # scoring items per kv head (128 / group pages each)
+    n_est = KV_ * E_        # scoring workers as the library sizes them
+    if n_est <= 256 or (n_est <= 512 and KV_ <= 8):
+        n_workers = n_est
+    else:
+        n_workers = min(max(n_est - 2 * E_, 256), 480)
     dec0 = n_workers        # self-selecting layer: no top-k workgroups
-    def score_row(h, c):    # (workgroup, event) of head h's scoring chunk c: item
+
+    def score_row(h, c):    # (workgroup, event) of kv head h's scoring chunk c: item
         i = h * E_ + c      # i is worker i % n_workers's item number i // n_workers
         return i % n_workers, 2 + i // n_workers
 
@@ -605,7 +628,7 @@ def timeline_pass(dev, layout, fn_layer, n_layers, samples=16, tick_ns=10.0, iso
         us = lambda x: (x - t0) * tick_ns / 1000.0
         heads = []
         for h in range(H_):
-            stored = [t[score_row(h, c)] for c in range(E_)]
+            stored = [t[score_row(h // (H_ // KV_), c)] for c in range(E_)]
             dec = [dec_row(h, c) for c in range(16)]
             row = {"head": h, "scored": us(max(stored))}
             for ev, name in ((1, "dec_start"), (4, "scores_seen"), (5, "row_loaded"),
@@ -690,6 +713,10 @@ def main():
     ap.add_argument("--timeline-pass", action="store_true",
                     help="per-phase timeline of the one-launch layer from the profiling build "
                          "(AOAKV_LIB=aoa-kv_amd/aoakv/libaoakv_timeline.so); one JSON line")
+    ap.add_argument("--gqa-pass", action="store_true",
+                    help="only the GQA layer (32 query / 8 kv heads, config 2's context and "
+                         "budget): its four timings as one JSON line, or with --timeline-pass "
+                         "its one-launch timeline")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="for rocprofv3 --pmc: a 64 MiB device copy x3 (calibration), then one "
                          "eager pass of the 32 one-launch layers; prints nothing else")
@@ -726,6 +753,17 @@ def main():
             res[f"prefill_{Lp // 1024}k_us"] = round(us, 1)
             res[f"prefill_{Lp // 1024}k_TFLOPs"] = round(tf, 1)
             res[f"prefill_{Lp // 1024}k_mfma_frac"] = round(tf / 2500.0, 4)
+        print(json.dumps(res))
+        return
+
+    if args.gqa_pass:
+        if args.timeline_pass:
+            G = gqa_inputs(dev, layout)
+            fl = ops.FLAG_VALUE_AWARE | ops.FLAG_FIXED | ops.FLAG_SINGLE_LAUNCH
+            res = timeline_pass(dev, layout, lambda l: G["layer"](l, fl), 8, hq=32, hkv=8)
+        else:
+            res = gqa_bench(dev, layout, launches=max(steps // 8, 256))
+        res["build"] = so_identity()
         print(json.dumps(res))
         return
 
