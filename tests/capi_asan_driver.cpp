@@ -1,7 +1,7 @@
 // Host-side checks of the C ABI (include/aoakv.h) for an AddressSanitizer
-// build: tests/test_capi_asan.py compiles the library's sources host-only
-// (no device code) with -fsanitize=address on the host pass, links this
-// driver and runs it on the CPU.  Every call either fails validation before
+// build: tests/test_capi_asan.py compiles the library's sources with
+// -fsanitize=address on the host pass (the device code, built as usual,
+// never runs here), links this driver and runs it on the CPU.  Every call either fails validation before
 // any HIP call or, with well-formed shapes, walks the host path to the
 // launch (workspace layout, selection sizing, argument packing), which then
 // fails for want of a device or of device code: AOAKV_ERR_HIP is accepted
@@ -10,6 +10,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
 
 #include "../include/aoakv.h"
 
