@@ -23,8 +23,9 @@
 // chunks permuted per row (k_swz / v_swz below), so the K reads of a wave
 // and the V transpose reads hit distinct banks (no LDS bank conflicts,
 // measured with SQ_LDS_BANK_CONFLICT).  Each wave
-// loads the 16 rows of one page per tile, so its page id is one scalar load,
-// fetched a tile ahead.  The V^T operand of O^T += V^T P^T is read from the
+// loads 16 rows per tile: one page of 16 tokens, half a page of 32 or two
+// pages of 8, so its page ids are one or two scalar loads, fetched a tile
+// ahead.  The V^T operand of O^T += V^T P^T is read from the
 // row-major V tile with ds_read_b64_tr_b16: in each 16-lane group, output
 // lane 4a+b receives element b of the 8-byte blocks addressed by lanes a,
 // a+4, a+8, a+12 (checked on the hardware), so four lanes pointing at four
@@ -80,7 +81,10 @@ __device__ inline int v_swz(int r) { return 4 * (r & 3); }
 // byte offset of 16-byte chunk j of key row r in a K tile
 __device__ inline int tile_off(int r, int j) { return r * kPfRowBytes + 16 * (j ^ k_swz(r)); }
 
+// S: tokens per page (8, 16 or 32).
+template <int S>
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
+  static_assert(S == 8 || S == 16 || S == 32, "a wave's 16 rows: two pages, one, or half of one");
   // two buffers of [K | V] tiles, separate objects so the compiler sees that
   // the loads into one never alias the reads of the other (no wait on them)
   __shared__ __attribute__((aligned(16))) char s_buf0[2 * kPfTileBytes];
@@ -104,7 +108,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
   const uint32_t hkv = h / (a.Hq / a.H);   // its kv head (GQA groups share K/V)
   const uint32_t qt = nqt - 1u - item % nqt;  // heaviest query tiles first
   const uint32_t off = L - Lq;                 // position of query 0
-  const uint32_t npages = (L + kPageSize - 1) / kPageSize;
+  const uint32_t npages = (L + S - 1) / S;
 
   const uint32_t q = qt * kPfQueriesPerBlock + wave * kPfQueriesPerWave + c;
   const bool q_live = q < Lq;
@@ -127,27 +131,34 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
                                                           16 * s + 8 * g)
                      : half8{};
 
-  // ---- tile loader: wave w fills rows 16w .. 16w+15 (one page) of K and V,
-  // 4 rows (1 KB) per instruction; lane l lands at byte 16*l of its
-  // instruction's rows, i.e. row l/16, chunk slot l%16 -> it fetches the
-  // global chunk (l%16) ^ (row % 16).  A page past the sequence reads the
-  // last page (its keys are masked).
+  // ---- tile loader: wave w fills rows 16w .. 16w+15 of K and V (keys
+  // 64 t + 16 w ..), 4 rows (1 KB) per instruction; lane l lands at byte
+  // 16*l of its instruction's rows, i.e. row l/16, chunk slot l%16 -> it
+  // fetches the global chunk (l%16) ^ (row % 16).  The rows' pages: .x for
+  // rows 0..7 of the wave, .y for rows 8..15 (the same page unless S = 8).
+  // A page past the sequence reads the last page (its keys are masked).
   // The page table is read through the constant address space: the kernel
   // never writes it, and a scalar load keeps it off the vector memory
   // counter that the K/V tile loads are waited on with.
   const __attribute__((address_space(4))) int32_t* kv_idx =
       (const __attribute__((address_space(4))) int32_t*)a.kv_indices;
-  auto page_of = [&](uint32_t tile) -> uint32_t {
-    uint32_t p = tile * (kPfTileKeys / kPageSize) + (uint32_t)wave;
-    p = p < npages ? p : npages - 1u;
-    return (uint32_t)kv_idx[p];
+  auto page_of = [&](uint32_t tile) -> uint2 {
+    const uint32_t key0 = tile * kPfTileKeys + 16u * (uint32_t)wave;  // the wave's first row
+    uint32_t p0 = key0 / S, p1 = (key0 + 8u) / S;
+    p0 = p0 < npages ? p0 : npages - 1u;
+    p1 = p1 < npages ? p1 : npages - 1u;
+    const uint32_t x = (uint32_t)kv_idx[p0];
+    return uint2{x, S == 8 ? (uint32_t)kv_idx[p1] : x};
   };
+  // token slot of the wave's row 0 in its page
+  const uint32_t slot0 = S == 32 ? 16u * ((uint32_t)wave % 2u) : 0u;
   const int lrow = lane / 16, lslot = lane % 16;
-  auto load_tile = [&](char* buf, uint32_t phys) {
+  auto load_tile = [&](char* buf, uint2 phys) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * wave + 4 * i + lrow;  // row in the tile; r % 16 = 4i + lrow
-      const size_t e = elem_off(a.g, phys, 0, hkv, (uint32_t)(r & 15));
+      const uint32_t pg = i < 2 ? phys.x : phys.y;  // rows 0..7 / 8..15 of the wave
+      const size_t e = elem_off(a.g, pg, 0, hkv, (slot0 + (uint32_t)(r & 15)) % S);
       __builtin_amdgcn_global_load_lds(a.kv + e + 8 * (lslot ^ k_swz(r)),
                                        buf + (16 * wave + 4 * i) * kPfRowBytes, 16, 0, 0);
       __builtin_amdgcn_global_load_lds(a.kv + e + a.g.kv + 8 * (lslot ^ v_swz(r)),
@@ -296,7 +307,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
   };
 
   load_tile(s_buf0, page_of(0u));
-  uint32_t phys_next = page_of(1u);
+  uint2 phys_next = page_of(1u);
   // two tiles per trip: even tiles in buffer 0, odd tiles in buffer 1
   for (uint32_t it = 0; it < ntiles; it += 2) {
 #pragma unroll
@@ -344,10 +355,16 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
   }
 }
 
-hipError_t launch_prefill(const PrefillArgs& a, hipStream_t s) {
+hipError_t launch_prefill(const PrefillArgs& a, uint32_t page_size, hipStream_t s) {
   const uint32_t nqt = (a.Lq + kPfQueriesPerBlock - 1) / kPfQueriesPerBlock;
   const uint32_t per = (nqt * a.Hq + kXcds - 1) / kXcds;
-  hipLaunchKernelGGL(prefill_kernel, dim3(per * kXcds), dim3(kPfThreads), 0, s, a);
+  const dim3 grid(per * kXcds), block(kPfThreads);
+  switch (page_size) {
+    case 8: hipLaunchKernelGGL(prefill_kernel<8>, grid, block, 0, s, a); break;
+    case 16: hipLaunchKernelGGL(prefill_kernel<16>, grid, block, 0, s, a); break;
+    case 32: hipLaunchKernelGGL(prefill_kernel<32>, grid, block, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

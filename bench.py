@@ -182,14 +182,16 @@ def decode_appends(dev, layout, n_app=512, mode="append", graph=True):
     return eager, e0.elapsed_time(e1) * 1e3 / n_app
 
 
-def prefill_bench(dev, layout, L, reps=5):
-    """Config 4: causal paged prefill, 32 heads x 128, q/K/V ~ N(0, 0.5^2).
-    FLOPs as the reference's nvbench counts them (bench_prefill.cu:109-111):
-    L * (2L - L) * 2 * H * D."""
+def prefill_bench(dev, layout, L, reps=5, page_size=S):
+    """Config 4: causal paged prefill, 32 heads x 128, q/K/V ~ N(0, 0.5^2)
+    (pages of 16 tokens; page_size 8 or 32 for the same kernel's other
+    instantiations).  FLOPs as the reference's nvbench counts them
+    (bench_prefill.cu:109-111): L * (2L - L) * 2 * H * D."""
     import torch
     from aoakv import ops
     from aoakv.utils import InferenceController, append_kv
-    c = InferenceController(1, H, D, S, 64, L + S, torch.float16, dev, layout=layout)
+    c = InferenceController(1, H, D, page_size, 64, L + page_size, torch.float16, dev,
+                            layout=layout)
     g = torch.Generator(device=dev).manual_seed(0)
     q = (torch.randn((L, H, D), generator=g, device=dev) * 0.5).half()
     k = (torch.randn((L, H, D), generator=g, device=dev) * 0.5).half()
@@ -753,6 +755,11 @@ def main():
             res[f"prefill_{Lp // 1024}k_us"] = round(us, 1)
             res[f"prefill_{Lp // 1024}k_TFLOPs"] = round(tf, 1)
             res[f"prefill_{Lp // 1024}k_mfma_frac"] = round(tf / 2500.0, 4)
+        for ps in (8, 32):  # the same kernel on pages of 8 and 32 tokens
+            us, tf = prefill_bench(dev, layout, 8192, page_size=ps)
+            res[f"prefill_8k_page{ps}_us"] = round(us, 1)
+            res[f"prefill_8k_page{ps}_TFLOPs"] = round(tf, 1)
+        res["build"] = so_identity()
         print(json.dumps(res))
         return
 
@@ -957,6 +964,10 @@ def main():
             extra[f"prefill_{Lp // 1024}k_us"] = round(us, 1)
             extra[f"prefill_{Lp // 1024}k_TFLOPs"] = round(tf, 1)
             extra[f"prefill_{Lp // 1024}k_mfma_frac"] = round(tf / 2500.0, 4)
+        for ps in (8, 32):  # the same MFMA kernel on pages of 8 and 32 tokens
+            us, tf = prefill_bench(dev, layout, 8192, page_size=ps)
+            extra[f"prefill_8k_page{ps}_us"] = round(us, 1)
+            extra[f"prefill_8k_page{ps}_TFLOPs"] = round(tf, 1)
         log("[bench] config 5 (ragged batch) ...")
         extra["config5_ragged_batch16"] = ragged_batch_bench(dev, layout)
         log("[bench] GQA layer (32 / 8 heads) ...")
