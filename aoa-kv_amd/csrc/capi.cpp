@@ -53,10 +53,11 @@ int hip_status(hipError_t e, const char* what) {
 // at once: CUs times the kernel's occupancy per CU (four at 36 KB of LDS and
 // 112 VGPRs).  0 if the device cannot be queried.  Cached per device (benign
 // races: every writer stores the same value).
-uint32_t resident_layer_workgroups(uint32_t group, uint32_t heads_per_item) {
-  static uint32_t cache[64][8];
-  const uint32_t gi = (group == 1u ? 0u : group == 2u ? 1u : group == 4u ? 2u : 3u) +
-                      (heads_per_item > 1u ? 4u : 0u);
+uint32_t resident_layer_workgroups(uint32_t group, uint32_t heads_per_item, uint32_t score_heads) {
+  static uint32_t cache[64][9];
+  const uint32_t gi = score_heads == 2u ? 8u
+                      : (group == 1u ? 0u : group == 2u ? 1u : group == 4u ? 2u : 3u) +
+                            (heads_per_item > 1u ? 4u : 0u);
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0u;
   if (cache[dev][gi] == 0u) {
@@ -64,7 +65,8 @@ uint32_t resident_layer_workgroups(uint32_t group, uint32_t heads_per_item) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         cus <= 0)
       return 0u;
-    cache[dev][gi] = aoakv::layer_self_blocks_per_cu(group, heads_per_item) * (uint32_t)cus;
+    cache[dev][gi] =
+        aoakv::layer_self_blocks_per_cu(group, heads_per_item, score_heads) * (uint32_t)cus;
   }
   return cache[dev][gi];
 }
@@ -727,9 +729,18 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
       la.e.hscore_stride = max_pages;
     }
     const uint32_t group = num_qo_heads / num_kv_heads;
-    la.est_chunks = aoakv::est_chunks(max_pages, group);
-    la.n_est = batch_size * num_kv_heads * la.est_chunks;
+    // NHD: a head's metadata entries are 256-byte pieces 8 KB apart, so the
+    // scoring items take two adjacent heads (512-byte runs) over half the
+    // pages; they hand every score over as a word, so only with the words
+    la.score_heads = layout == AOAKV_LAYOUT_NHD && group == 1u && num_kv_heads % 2u == 0u &&
+                             la.e.hscore != nullptr
+                         ? 2u
+                         : 1u;
+    la.est_chunks = aoakv::est_chunks(max_pages, group * la.score_heads);
+    la.n_est = batch_size * (num_kv_heads / la.score_heads) * la.est_chunks;
     la.n_workers = aoakv::layer_score_workers(la.n_est, la.est_chunks);
+    // (per scoring unit: est_chunks items of 128 / (group * score_heads)
+    // pages over score_heads heads, the same bytes per item)
     la.stagger_ps = aoakv::layer_stagger_ps(la.est_chunks, group, batch_size * num_kv_heads);
     la.n_dec = batch_size * (num_qo_heads / da.heads_per_item) * da.max_chunks;
     // score words and the whole launch resident at once: each decode item
@@ -741,7 +752,7 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
     la.self_select = la.e.hscore != nullptr &&
                              la.n_workers + la.n_dec <=
                                  resident_layer_workgroups(num_qo_heads / num_kv_heads,
-                                                           da.heads_per_item)
+                                                           da.heads_per_item, la.score_heads)
                          ? 1u
                          : 0u;
     la.n_heads = la.self_select ? 0u : batch_size * num_kv_heads;

@@ -604,12 +604,17 @@ __device__ inline uint32_t est_pages(const EstimateArgs& a, uint32_t b, uint32_t
 }
 
 // Scores pages [n*chunk, n*chunk + n) of (sequence b, kv head h), n =
-// est_block_pages<GROUP>(), and stores them (agent-coherent).  Returns false, uniformly, when the chunk
+// kPPB, and stores them (agent-coherent).  With HPI = 2 (NHD layout, GROUP
+// 1) the item covers kv heads h and h + 1 and kPPB pages of each: a step's
+// four rows read pages p and p + 1 of both heads, so each pair of rows reads
+// one 512-byte run (the two heads' adjacent 256-byte entries) instead of
+// two 256-byte pieces 8 KB apart.  Returns false, uniformly, when the chunk
 // holds no page.  A sequence whose page table exceeds what the call covers
 // sets kErrTruncated (once, from its first chunk).
-template <int GROUP, uint32_t kPPB = est_block_pages<GROUP>()>
+template <int GROUP, uint32_t kPPB = est_block_pages<GROUP>(), int HPI = 1>
 __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, uint32_t h,
                                            uint32_t chunk, EstShared& sm) {
+  static_assert(HPI == 1 || (HPI == 2 && GROUP == 1 && kPPB == 64u), "head pairs: GROUP 1");
   float* s_sc = sm.sc;
   const uint32_t lane = __lane_id();
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -621,6 +626,9 @@ __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, ui
   constexpr uint32_t kPPW = kPPB / 4u;  // pages per wave: 32, 16, 8 or 4
   static_assert(kPPW % 4u == 0u && kPageSize % kPPW == 0u || kPPW == 2u * kPageSize,
                 "a wave's pages lie in one or two metadata pages");
+  // step s, row r: page page0 + kPS * s + (r >> (HPI - 1)) of head h + (r & (HPI - 1))
+  constexpr uint32_t kPS = 4u / (uint32_t)HPI;                   // pages per step
+  const uint32_t rpage = row >> (HPI - 1), hrow = h + (row & (uint32_t)(HPI - 1));
   if (chunk * kPPB >= P) return false;  // uniform per block
   if (clamped && chunk == 0u && threadIdx.x == 0u) flag_error(a.error, kErrTruncated);
   const uint32_t mbeg = (uint32_t)a.meta_indptr[b];
@@ -635,8 +643,10 @@ __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, ui
   // metadata vectors, then the value statistic (used only after scoring).
   const uint32_t pblk = chunk * kPPB;  // < P
   const uint32_t page0 = pblk + wave * kPPW;
-  uint32_t pj = page0 + (lane % kPPW);  // lane j: page page0 + j % kPPW
+  // lane j (< 32) holds the value statistic of step j / 4, row j % 4
+  uint32_t pj = page0 + (lane % (kPPW * HPI)) / HPI;
   pj = pj < P ? pj : P - 1u;
+  const uint32_t hj = h + (lane % (uint32_t)HPI);
   const uint32_t phys_j = (uint32_t)a.kv_indices[pbeg + pj];
   __builtin_amdgcn_sched_barrier(0);  // keep the issue order written here
   const uint32_t pl0 = page0 < P ? page0 : pblk;  // a live page of the wave's first half
@@ -654,7 +664,7 @@ __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, ui
   uint32_t psel[GROUP][kVec / 2];  // v_perm_b32 selectors: src0 = Kmax, src1 = Kmin
 #pragma unroll
   for (int g = 0; g < GROUP; ++g) {
-    const H8 qq = ld16(a.q + ((size_t)b * a.Hq + h * GROUP + g) * kHeadDim + d0);
+    const H8 qq = ld16(a.q + ((size_t)b * a.Hq + hrow * GROUP + g) * kHeadDim + d0);
 #pragma unroll
     for (int m = 0; m < kVec / 2; ++m) {
       q2[g][m] = half_pair(qq, m);
@@ -663,21 +673,22 @@ __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, ui
     }
   }
 
-  constexpr int kSteps = (int)kPPW / 4;
+  constexpr int kSteps = (int)(kPPW / kPS);
   H8 kmx[kSteps], kmn[kSteps];
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
-    // page page0 + 4s + row: its metadata page and slot
-    const uint32_t mp = (uint32_t)(s * 4) < kPageSize ? mp0 : mp1;
-    const size_t off = elem_off(a.g, mp, 0, h, (page0 + s * 4 + row) % kPageSize) + d0;
+    // page page0 + kPS * s + rpage: its metadata page and slot
+    const uint32_t mp = (uint32_t)s * kPS < kPageSize ? mp0 : mp1;
+    const size_t off =
+        elem_off(a.g, mp, 0, hrow, (page0 + (uint32_t)s * kPS + rpage) % kPageSize) + d0;
     kmx[s] = ld16(a.meta + off);
     kmn[s] = ld16(a.meta + off + a.g.kv);
   }
   __builtin_amdgcn_sched_barrier(0);
   // without the value term v_log_norm may be null: read q instead (unused)
-  const f16 lvn_raw = *(value_aware ? a.v_log_norm + (size_t)phys_j * a.Hkv + h : a.q);
+  const f16 lvn_raw = *(value_aware ? a.v_log_norm + (size_t)phys_j * a.Hkv + hj : a.q);
 
-  float sc[kSteps];  // score of page page0 + 4s + row (same in all lanes of the row)
+  float sc[kSteps];  // score of step s's page of this row (same in all lanes of the row)
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
     float x[GROUP];
@@ -721,18 +732,20 @@ __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, ui
   for (int s = 0; s < kSteps; ++s) {
     float score = sc[s];
     if (value_aware) score = score + 2.0f * __shfl(lvn_lane, s * 4 + (int)row);
-    if (l16 == 0u) s_sc[wave * kPPW + s * 4 + row] = score;
+    // s_sc: [HPI heads][kPPB pages]
+    if (l16 == 0u)
+      s_sc[(row & (uint32_t)(HPI - 1)) * kPPB + wave * kPPW + (uint32_t)s * kPS + rpage] = score;
   }
   __syncthreads();
-  float* out = a.scores + ((size_t)b * a.Hkv + h) * a.score_stride;
   {
-    const uint32_t p = chunk * kPPB + threadIdx.x;
+    const uint32_t hh = threadIdx.x / kPPB;  // < HPI for the storing threads
+    const uint32_t p = chunk * kPPB + threadIdx.x % kPPB;
     const uint32_t nstore = (a.flags & kFlagQuestKernel) ? P - 1u : P;
-    if (threadIdx.x < kPPB && p < nstore) {
-      st_agent(out + p, s_sc[threadIdx.x]);
+    if (threadIdx.x < kPPB * HPI && p < nstore) {
+      const size_t bh = (size_t)b * a.Hkv + h + hh;
+      st_agent(a.scores + bh * a.score_stride + p, s_sc[threadIdx.x]);
       if (a.hscore != nullptr)
-        st_agent_u32(a.hscore + ((size_t)b * a.Hkv + h) * a.hscore_stride + p,
-                     to_word(s_sc[threadIdx.x]));
+        st_agent_u32(a.hscore + bh * a.hscore_stride + p, to_word(s_sc[threadIdx.x]));
     }
   }
 
@@ -1452,28 +1465,30 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
 // (same-address device atomics serialize at ~12 ns each).
 // SELF (la.self_select): the decode items select for themselves; a separate
 // instantiation, so the other path keeps its own register budget.  GI: query
-// heads per decode item (1, or the whole group).
+// heads per decode item (1, or the whole group).  HPI: kv heads per scoring
+// item (2: NHD head pairs, score_item; the heads' scores go out as words).
 #ifdef AOAKV_TIMELINE
 // the profiling build wraps the kernel body to note its start and write the
 // notes out when the workgroup ends, whichever way the body returns
-template <int GROUP, bool QUEST, bool SELF, int GI>
+template <int GROUP, bool QUEST, bool SELF, int GI, int HPI = 1>
 __device__ __forceinline__ void layer_body(const LayerArgs& la);
 
-template <int GROUP, bool QUEST, bool SELF, int GI>
+template <int GROUP, bool QUEST, bool SELF, int GI, int HPI = 1>
 __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la) {
   TL_BEGIN();
-  layer_body<GROUP, QUEST, SELF, GI>(la);
+  layer_body<GROUP, QUEST, SELF, GI, HPI>(la);
   TL_FLUSH();
 }
 
-template <int GROUP, bool QUEST, bool SELF, int GI>
+template <int GROUP, bool QUEST, bool SELF, int GI, int HPI>
 __device__ __forceinline__ void layer_body(const LayerArgs& la)
 #else
-template <int GROUP, bool QUEST, bool SELF, int GI>
+template <int GROUP, bool QUEST, bool SELF, int GI, int HPI = 1>
 __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la)
 #endif
 {
   static_assert(GI == 1 || GI == GROUP, "a decode item serves one query head or the group");
+  static_assert(HPI == 1 || GROUP == 1, "head-paired scoring items: GROUP 1");
   __shared__ union {
     EstTopkShared e;
     DecShared<GI> d;
@@ -1499,13 +1514,15 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la)
     TL(kTlStaggerDone);
     int tl_item = 0;
     for (uint32_t i = t; i < la.n_est; i += la.n_workers) {
+      // bh: (sequence, kv head) -- or head pair, HPI = 2
       const uint32_t bh = i / la.est_chunks, chunk = i % la.est_chunks;
-      const uint32_t b = bh / la.e.Hkv, h = bh % la.e.Hkv;
-      if (score_item<GROUP>(la.e, b, h, chunk, sm.e.e)) {
+      const uint32_t hu = la.e.Hkv / HPI;  // scoring units per sequence
+      const uint32_t b = bh / hu, h = (bh % hu) * HPI;
+      if (score_item<GROUP, est_block_pages<GROUP>() / HPI, HPI>(la.e, b, h, chunk, sm.e.e)) {
         TL(tl_item == 0 ? kTlScored0 : kTlScored1);
         ++tl_item;
         (void)tl_item;
-        if (SELF || la.e.hscore != nullptr) {  // (SELF runs on score words only)
+        if (SELF || HPI == 2 || la.e.hscore != nullptr) {  // (SELF, HPI 2: score words only)
           // the scores went out as handoff words: only end this item's use
           // of LDS before the next item's
           __syncthreads();
@@ -1566,8 +1583,9 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la)
       // 24.15 us per layer at config 2)
       const uint32_t first_round = (la.n_workers - 1u) / la.est_chunks;
       const uint32_t bkv = b * la.d.Hkv + hq0 / GROUP;  // the (sequence, kv head)
+      const uint32_t unit = bkv / HPI;                   // its scoring unit
       const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-      sleep_until(t0, (uint64_t)(bkv < first_round ? bkv : first_round) * la.stagger_ps);
+      sleep_until(t0, (uint64_t)(unit < first_round ? unit : first_round) * la.stagger_ps);
       TL(kTlStaggerDone);
       // with GI < GROUP the group's merging items count who is done with the
       // score words on the kv head's arrival counter (unused by SELF's scoring)
@@ -1614,6 +1632,15 @@ hipError_t launch_layer(const LayerArgs& la, hipStream_t s) {
   const bool quest = (la.e.flags & kFlagQuestKernel) != 0u;
   const bool self = la.self_select != 0u;
   const bool grouped = la.d.heads_per_item > 1u;
+  if (la.score_heads == 2u) {  // NHD head pairs (GROUP 1, score words)
+    if (la.e.Hq != la.e.Hkv || la.e.Hkv % 2u != 0u || la.e.hscore == nullptr)
+      return hipErrorInvalidValue;
+    if (self && quest) hipLaunchKernelGGL((layer_kernel<1, true, true, 1, 2>), dim3(grid), dim3(kThreads), 0, s, la);
+    else if (self) hipLaunchKernelGGL((layer_kernel<1, false, true, 1, 2>), dim3(grid), dim3(kThreads), 0, s, la);
+    else if (quest) hipLaunchKernelGGL((layer_kernel<1, true, false, 1, 2>), dim3(grid), dim3(kThreads), 0, s, la);
+    else hipLaunchKernelGGL((layer_kernel<1, false, false, 1, 2>), dim3(grid), dim3(kThreads), 0, s, la);
+    return hipGetLastError();
+  }
   switch (la.e.Hq / la.e.Hkv) {
 #define AOAKV_LAYER_GI(G, GI)                                                                        \
   if (self && quest) hipLaunchKernelGGL((layer_kernel<G, true, true, GI>), dim3(grid), dim3(kThreads), 0, s, la);   \
@@ -1727,14 +1754,20 @@ uint32_t layer_stagger_ps(uint32_t est_chunks, uint32_t group, uint32_t heads) {
 uint32_t counter_stride() { return kCounterStride; }
 // Workgroups of the self-selecting layer kernel one CU holds at once (its LDS
 // and registers decide); 0 if the runtime cannot tell.
-uint32_t layer_self_blocks_per_cu(uint32_t group, uint32_t heads_per_item) {
+uint32_t layer_self_blocks_per_cu(uint32_t group, uint32_t heads_per_item, uint32_t score_heads) {
   int n = 0;
   hipError_t e = hipErrorInvalidValue;
   const bool gr = heads_per_item > 1u;
 #define AOAKV_OCC(G, GI) \
   e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, layer_kernel<G, false, true, GI>, kThreads, 0)
   switch (group) {
-    case 1: AOAKV_OCC(1, 1); break;
+    case 1:
+      if (score_heads == 2u)
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, layer_kernel<1, false, true, 1, 2>,
+                                                         kThreads, 0);
+      else
+        AOAKV_OCC(1, 1);
+      break;
     case 2: if (gr) AOAKV_OCC(2, 2); else AOAKV_OCC(2, 1); break;
     case 4: if (gr) AOAKV_OCC(4, 4); else AOAKV_OCC(4, 1); break;
     case 8: if (gr) AOAKV_OCC(8, 8); else AOAKV_OCC(8, 1); break;

@@ -189,6 +189,7 @@ struct LayerArgs {
   uint32_t n_dec;      // decode items: B * (Hq / d.heads_per_item) * d.max_chunks
   uint32_t stagger_ps; // wall time (ps) between the scoring starts of consecutive heads
   uint32_t self_select;  // decode items run their kv head's top-k themselves (n_heads = 0)
+  uint32_t score_heads;  // kv heads per scoring item: 1, or 2 (NHD pairs, GROUP 1, score words)
 };
 
 hipError_t launch_append_prefill(const AppendPrefillArgs& a, hipStream_t s);
@@ -220,7 +221,7 @@ uint32_t fused_topk_max_pages();  // ... and the fused estimate + top-k kernel
 uint32_t layer_score_workers(uint32_t n_est, uint32_t est_chunks);  // one-launch layer scorers
 uint32_t layer_stagger_ps(uint32_t est_chunks, uint32_t group, uint32_t heads);  // one-launch scoring start offset per head (ps)
 uint32_t counter_stride();        // u32 words between per-head counters (one cache line each)
-uint32_t layer_self_blocks_per_cu(uint32_t group, uint32_t heads_per_item);  // per CU
+uint32_t layer_self_blocks_per_cu(uint32_t group, uint32_t heads_per_item, uint32_t score_heads);  // per CU
 
 // generic.hip: the other head dims (64, 128, 256) and page sizes (1..32)
 hipError_t launch_gen_append_prefill(const AppendPrefillArgs& a, uint32_t head_dim, hipStream_t s);

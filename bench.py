@@ -561,7 +561,7 @@ TL_NAMES = ["start", "stagger_done", "scored0", "scored1", "scores_seen", "row_l
 
 
 def timeline_pass(dev, layout, fn_layer, n_layers, samples=16, tick_ns=10.0, isolated=None,
-                  hq=None, hkv=None):
+                  hq=None, hkv=None, score_heads=1):
     """Per-phase timeline of the one-launch layer (config 2, or hq query heads
     over hkv kv heads), from the profiling build
     (AOAKV_LIB=aoa-kv_amd/aoakv/libaoakv_timeline.so).  Each sample launch
@@ -569,7 +569,8 @@ def timeline_pass(dev, layout, fn_layer, n_layers, samples=16, tick_ns=10.0, iso
     its workgroups' phase timestamps (s_memrealtime, 100 MHz, noted in LDS
     and written out as each workgroup ends) are read back and reduced per
     query head.  `isolated` kernels are timed the same way, alone behind the
-    replay.  Returns a dict (JSON)."""
+    replay.  score_heads: kv heads per scoring item (2: the NHD layout's head
+    pairs).  Returns a dict (JSON)."""
     import ctypes
     import numpy as np
     import torch
@@ -598,8 +599,10 @@ def timeline_pass(dev, layout, fn_layer, n_layers, samples=16, tick_ns=10.0, iso
     torch.cuda.synchronize()
     H_ = hq or H            # query heads
     KV_ = hkv or H_         # kv heads
-    E_ = P // (128 // (H_ // KV_))  # scoring items per kv head (128 / group pages each)
-    n_est = KV_ * E_        # scoring workers as the library sizes them
+    # scoring items per scoring unit (a kv head, or a head pair): 128 /
+    # (group * score_heads) pages each
+    E_ = P // (128 // ((H_ // KV_) * score_heads))
+    n_est = (KV_ // score_heads) * E_  # scoring workers as the library sizes them
     if n_est <= 256 or (n_est <= 512 and KV_ <= 8):
         n_workers = n_est
     else:
@@ -607,7 +610,7 @@ def timeline_pass(dev, layout, fn_layer, n_layers, samples=16, tick_ns=10.0, iso
     dec0 = n_workers        # self-selecting layer: no top-k workgroups
 
     def score_row(h, c):    # (workgroup, event) of kv head h's scoring chunk c: item
-        i = h * E_ + c      # i is worker i % n_workers's item number i // n_workers
+        i = (h // score_heads) * E_ + c  # worker i % n_workers's item number i // n_workers
         return i % n_workers, 2 + i // n_workers
 
     def dec_row(h, c):      # workgroup of head h's decode chunk c
@@ -828,7 +831,10 @@ def main():
                                            ("selected", 6), ("output", 11)], H),
                ("decode_kernel", dec, [("attended", 8), ("partial", 9), ("output", 11)],
                 H * K_SEL // 8)]
-        print(json.dumps(timeline_pass(dev, layout, layer1, n_layers, isolated=iso)))
+        # the NHD layout's scoring items take two adjacent heads
+        pairs = 2 if layout == ops.NHD and H % 2 == 0 else 1
+        print(json.dumps(timeline_pass(dev, layout, layer1, n_layers, isolated=iso,
+                                       score_heads=pairs)))
         return
 
     def capture(fn, n):
