@@ -758,6 +758,23 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
     la.n_heads = la.self_select ? 0u : batch_size * num_kv_heads;
     return hip_status(aoakv::launch_layer(la, s), "sparse_decode_layer");
   }
+  if (tuned && max_pages <= aoakv::fused_topk_max_pages()) {
+    // two launches: the scores alone (the unfused kernel, smaller items),
+    // then decode items that each select their kv head's pages from the
+    // complete scores (16 copies of every top-k, none waiting on another
+    // workgroup) and write their chunk's entries of sel_pages.  Config 2:
+    // 24.7-25.1 us per layer, against 25.6 with the top-k fused into the
+    // scoring launch's last item per head (13.7 + 12.1); starting the kv
+    // heads' decode items 0.1-0.3 us apart was slower (25.1-30.0).
+    if (int e = hip_status(aoakv::launch_estimate(ea, batch_size, max_pages, s), "estimate"))
+      return e;
+    aoakv::EstimateArgs es = ea;
+    es.sel = sel_pages;
+    es.sel_stride = sel_stride;
+    es.token_budget = token_budget;
+    es.token_budgets = token_budgets;
+    return hip_status(aoakv::launch_decode(da, batch_size, s, &es), "sparse_decode_layer/decode");
+  }
   if (int e = launch_estimate_topk(ea, w, sel_pages, sel_stride, token_budget, token_budgets,
                                    batch_size, max_pages, head_dim, page_size, flags, s))
     return e;

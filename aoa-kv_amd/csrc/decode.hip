@@ -951,7 +951,9 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
                                             const EstimateArgs* ea = nullptr,
                                             TopkShared* tk = nullptr, uint32_t* s_err = nullptr,
                                             uint32_t err0 = 0u, uint32_t* clear_ctr = nullptr) {
-  static_assert(!SELF || HANDOFF, "self-selection is a one-launch mode");
+  // SELF without HANDOFF (the two-launch decode): the scores are complete
+  // (written by the previous launch), read as floats, nothing to wait for
+  // or clear
   const uint32_t lane = __lane_id();
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t row = lane / kLanesPerRow;
@@ -1003,7 +1005,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   uint32_t* words = nullptr;
   if constexpr (SELF) {
     pl = plan_select(*ea, b);
-    words = ea->hscore + ((size_t)b * ea->Hkv + hkv) * ea->hscore_stride;
+    if (HANDOFF) words = ea->hscore + ((size_t)b * ea->Hkv + hkv) * ea->hscore_stride;
   }
   // waits until the score words [0, pl.P) are written, then clears them
   auto consume_words = [&]() {
@@ -1027,7 +1029,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   if (P != P_table && chunk == 0u && threadIdx.x == 0u) flag_error(a.error, kErrTruncated);
   if (P == 0u || lpl == 0u || lpl > S) {  // malformed page table
     // the words were written all the same: consumed once per kv head
-    if (SELF && chunk == 0u && hq0 % group == 0u) consume_words();
+    if (SELF && HANDOFF && chunk == 0u && hq0 % group == 0u) consume_words();
     return;
   }
   // physical id of the sequence's last page (the one holding lpl tokens)
@@ -1059,8 +1061,9 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
     const int32_t* ids = e.kv_indices + pl.pbeg;
     self_topk = pl.k != 0u && pl.k < pl.P;
     if (self_topk)
-      topk_staged<true>(nullptr, pl.P, pl.k, (e.flags & kFlagFixed) != 0u, ids, nullptr, *tk,
-                        nullptr, 0u, 0u, words, a.error);
+      topk_staged<true>(HANDOFF ? nullptr : e.scores + ((size_t)b * e.Hkv + hkv) * e.score_stride,
+                        pl.P, pl.k, (e.flags & kFlagFixed) != 0u, ids, nullptr, *tk, nullptr, 0u,
+                        0u, words, a.error);
     const uint32_t nout = self_topk ? pl.k : (pl.k == 0u ? 0u : pl.P);
     // entry i (page 0 past the selection; an entry the top-k did not yield
     // means the shapes disagree: flagged like a wait that gave up)
@@ -1402,7 +1405,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
       }
     }
   }
-  if constexpr (SELF) {
+  if constexpr (SELF && HANDOFF) {
     // every chunk's partial arrived, and each chunk stored its partial after
     // its top-k had read the score words: clear them (without a top-k no one
     // waited for them, so wait first).  With G < group the group's other
@@ -1431,13 +1434,25 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   }
 }
 
-// grid (chunks, query heads / G, sequences)
-template <bool QUEST, int G>
-__global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
-  __shared__ DecShared<G> sm;
+// grid (chunks, query heads / G, sequences).  SELF: no selection rows; every
+// item runs its kv head's top-k on the scores the previous launch wrote (e:
+// the scoring call's arguments with sel, budgets and flags) and writes its
+// chunk's entries of the selection.
+template <bool QUEST, int G, bool SELF = false>
+__global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a, EstimateArgs e) {
   TL_BEGIN();
   TL(kTlStart);
-  decode_item<false, QUEST, false, G>(a, blockIdx.z, blockIdx.y * G, blockIdx.x, sm);
+  if constexpr (SELF) {
+    __shared__ union {
+      TopkShared tk;
+      DecShared<G> d;
+    } sm;
+    decode_item<false, QUEST, true, G>(a, blockIdx.z, blockIdx.y * G, blockIdx.x, sm.d, &e,
+                                       &sm.tk);
+  } else {
+    __shared__ DecShared<G> sm;
+    decode_item<false, QUEST, false, G>(a, blockIdx.z, blockIdx.y * G, blockIdx.x, sm);
+  }
   TL_FLUSH();
 }
 
@@ -1676,16 +1691,24 @@ hipError_t launch_topk(const TopkArgs& a, uint32_t batch, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_decode(const DecodeArgs& a, uint32_t batch, hipStream_t s) {
+hipError_t launch_decode(const DecodeArgs& a, uint32_t batch, hipStream_t s,
+                         const EstimateArgs* self) {
   // one workgroup per (chunk, block of heads_per_item query heads, sequence)
   const uint32_t gi = a.heads_per_item > 1u ? a.Hq / a.Hkv : 1u;
   dim3 grid(a.max_chunks, a.Hq / gi, batch);
   const bool quest = (a.flags & kFlagQuestKernel) != 0u;
+  const EstimateArgs e = self != nullptr ? *self : EstimateArgs{};
   switch (gi) {
-#define AOAKV_DEC(G)                                                                      \
-  case G:                                                                                 \
-    if (quest) hipLaunchKernelGGL((decode_kernel<true, G>), grid, dim3(kThreads), 0, s, a); \
-    else hipLaunchKernelGGL((decode_kernel<false, G>), grid, dim3(kThreads), 0, s, a);      \
+#define AOAKV_DEC(G)                                                                          \
+  case G:                                                                                     \
+    if (self != nullptr) {                                                                    \
+      if (quest) hipLaunchKernelGGL((decode_kernel<true, G, true>), grid, dim3(kThreads), 0, s, a, e); \
+      else hipLaunchKernelGGL((decode_kernel<false, G, true>), grid, dim3(kThreads), 0, s, a, e);      \
+    } else if (quest) {                                                                       \
+      hipLaunchKernelGGL((decode_kernel<true, G>), grid, dim3(kThreads), 0, s, a, e);         \
+    } else {                                                                                  \
+      hipLaunchKernelGGL((decode_kernel<false, G>), grid, dim3(kThreads), 0, s, a, e);        \
+    }                                                                                         \
     break;
     AOAKV_DEC(1)
     AOAKV_DEC(2)

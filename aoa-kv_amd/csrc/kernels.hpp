@@ -200,7 +200,10 @@ hipError_t launch_estimate(const EstimateArgs& a, uint32_t batch, uint32_t max_p
 hipError_t launch_topk(const TopkArgs& a, uint32_t batch, hipStream_t s);
 hipError_t launch_layer(const LayerArgs& la, hipStream_t s);
 uint32_t est_chunks(uint32_t max_pages, uint32_t group);  // scoring items per (sequence, kv head)
-hipError_t launch_decode(const DecodeArgs& a, uint32_t batch, hipStream_t s);
+// self: the decode items select for themselves from the scores of the
+// previous launch (the scoring call's arguments, with sel / budgets / flags)
+hipError_t launch_decode(const DecodeArgs& a, uint32_t batch, hipStream_t s,
+                         const EstimateArgs* self = nullptr);
 hipError_t launch_fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s);
 hipError_t launch_prefill(const PrefillArgs& a, uint32_t page_size, hipStream_t s);
 
