@@ -206,22 +206,18 @@ def topk_filtering(scores, kv_indptr, kv_indices, kv_last_page_len, token_budget
 
 
 def decode_workspace(batch: int, num_qo_heads: int, num_kv_heads: int, max_sel_pages: int,
-                     device="cuda", max_pages: int = 0, head_dim: int = 128,
-                     page_size: int = 16) -> torch.Tensor:
+                     device="cuda", max_pages: int = 0, head_dim: int = 128) -> torch.Tensor:
     """Caller-owned decode workspace (replaces BatchDecodeHandler's buffers,
     decode_handler.cuh:73-136), zeroed.  With max_pages it also holds the
     one-launch layer's score handoff words (aoakv_layer_workspace_size).
-    Shapes other than head_dim 128 / page_size 16 run the generic kernels,
-    which use only the workspace's control words (aoakv.h
-    AOAKV_WORKSPACE_CTL_BYTES)."""
+    Its split-K partials hold head_dim + 4 floats per chunk."""
     lib = _lib.load()
-    if (head_dim, page_size) != (128, 16):
-        n = WORKSPACE_CTL_BYTES
-    elif max_pages:
-        n = lib.aoakv_layer_workspace_size(batch, num_qo_heads, num_kv_heads, 128, max_sel_pages,
-                                           max_pages)
+    if max_pages:
+        n = lib.aoakv_layer_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim,
+                                           max_sel_pages, max_pages)
     else:
-        n = lib.aoakv_decode_workspace_size(batch, num_qo_heads, num_kv_heads, 128, max_sel_pages)
+        n = lib.aoakv_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim,
+                                            max_sel_pages)
     ws = torch.empty(n, dtype=torch.uint8, device=device)
     _lib.call("aoakv_workspace_init", ws.data_ptr(), n, _stream())
     return ws

@@ -103,7 +103,7 @@ class InferenceController:
                                 device=device)
         self.workspace = ops.decode_workspace(1, num_heads, self.num_kv_heads, max_kv_pages,
                                               device, max_pages=max_kv_pages,
-                                              head_dim=head_dim, page_size=page_size)
+                                              head_dim=head_dim)
         # check the workspace error word after every fused decode layer call
         # (synchronizes: for debugging; check_errors() once per token is cheap)
         self.debug_checks = False

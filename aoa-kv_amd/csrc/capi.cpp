@@ -156,16 +156,17 @@ constexpr size_t kCtlBytes = 256;
 
 // [ctl: 64 u32][est counters: B*Hkv lines][dec counters: B*Hq lines]
 // [partials: B*Hq*chunks*stride f32][hsel: B*Hq*max_sel u32]
-// [hpart: B*Hq*chunks*stride u32]; every region 256-byte aligned.  The
+// [hpart: B*Hq*chunks*stride u32]; stride = head_dim + 4 (o, m, l, pad),
+// chunks of 8 selected pages; every region 256-byte aligned.  The
 // control words sit at offset 0 so a caller can read the error flag (word
 // 2) without knowing the shapes.  All of it starts zeroed
 // (aoakv_workspace_init) and every launch leaves all of it zeroed again
 // (the offsets depend on the call's selection size, so a region that must
 // start at zero in one call can lie where another call kept other data).
-size_t ws_layout(uint32_t B, uint32_t hq, uint32_t hkv, uint32_t max_sel_pages, void* base,
-                 Workspace* w) {
+size_t ws_layout(uint32_t B, uint32_t hq, uint32_t hkv, uint32_t max_sel_pages, uint32_t head_dim,
+                 void* base, Workspace* w) {
   const size_t part =
-      (size_t)B * hq * aoakv::decode_chunks(max_sel_pages) * aoakv::partial_stride() * 4u;
+      (size_t)B * hq * aoakv::decode_chunks(max_sel_pages) * (head_dim + 4u) * 4u;
   const size_t off_est = kCtlBytes;
   const size_t cnt = (size_t)aoakv::counter_stride() * 4u;  // bytes per counter
   const size_t off_dec = off_est + round_up((size_t)B * hkv * cnt, 256);
@@ -184,20 +185,6 @@ size_t ws_layout(uint32_t B, uint32_t hq, uint32_t hkv, uint32_t max_sel_pages, 
     w->bytes = total;
   }
   return total;
-}
-
-// Workspace bytes a decode call needs (and, with w, its layout over base):
-// the full layout for the tuned kernels, the control words alone for the
-// generic ones, which keep no counters or partials.
-size_t decode_ws_bytes(bool tuned, uint32_t B, uint32_t hq, uint32_t hkv, uint32_t max_sel_pages,
-                       void* base, Workspace* w) {
-  if (tuned) return ws_layout(B, hq, hkv, max_sel_pages, base, w);
-  if (w) {
-    *w = Workspace{};
-    w->ctl = static_cast<uint32_t*>(base);
-    w->bytes = kCtlBytes;
-  }
-  return kCtlBytes;
 }
 
 // Scores + top-k: one fused launch when every sequence fits the fused
@@ -559,8 +546,8 @@ int aoakv_topk_filtering(const float* scores, uint32_t score_stride,
 size_t aoakv_decode_workspace_size(uint32_t batch_size, uint32_t num_qo_heads,
                                    uint32_t num_kv_heads, uint32_t head_dim,
                                    uint32_t max_sel_pages) {
-  (void)head_dim;
-  return ws_layout(batch_size, num_qo_heads, num_kv_heads, max_sel_pages, nullptr, nullptr);
+  return ws_layout(batch_size, num_qo_heads, num_kv_heads, max_sel_pages, head_dim, nullptr,
+                   nullptr);
 }
 
 // The one-launch layer's score handoff words follow the decode workspace's
@@ -570,9 +557,8 @@ static size_t score_words_offset(size_t decode_bytes) { return round_up(decode_b
 size_t aoakv_layer_workspace_size(uint32_t batch_size, uint32_t num_qo_heads,
                                   uint32_t num_kv_heads, uint32_t head_dim,
                                   uint32_t max_sel_pages, uint32_t max_pages) {
-  (void)head_dim;
-  const size_t dec = ws_layout(batch_size, num_qo_heads, num_kv_heads, max_sel_pages, nullptr,
-                               nullptr);
+  const size_t dec = ws_layout(batch_size, num_qo_heads, num_kv_heads, max_sel_pages, head_dim,
+                               nullptr, nullptr);
   return score_words_offset(dec) + (size_t)batch_size * num_kv_heads * max_pages * 4u;
 }
 
@@ -604,15 +590,15 @@ static int fill_decode(aoakv::DecodeArgs& a, Workspace& w, const void* q, void* 
                                         max_pages, page_size, flags);
   REQUIRE(!sel_pages || sel_stride >= min_sel_stride(flags), "decode_sparse_attn: sel_stride %u < %u",
           sel_stride, min_sel_stride(flags));
-  // the tuned kernels split each head's pages over chunks merged through the
-  // workspace; the generic ones (one workgroup per query head) use only its
-  // control words and take any number of pages
+  // both decode kernels split each head's pages over chunks of 8 merged
+  // through the workspace; the tuned merge holds at most decode_max_chunks
+  // of them, the generic one (chunk order, one workgroup) any number
   const bool tuned = aoakv::tuned_shape(head_dim, page_size);
   REQUIRE(!tuned || aoakv::decode_chunks(max_sel) <= aoakv::decode_max_chunks(),
           "decode_sparse_attn: %u pages per head exceed the %u the split-K merge holds", max_sel,
           aoakv::decode_max_chunks() * 8u);
   const size_t need =
-      decode_ws_bytes(tuned, batch_size, num_qo_heads, num_kv_heads, max_sel, workspace, &w);
+      ws_layout(batch_size, num_qo_heads, num_kv_heads, max_sel, head_dim, workspace, &w);
   REQUIRE(workspace_bytes >= need, "decode_sparse_attn: workspace of %zu bytes < %zu needed",
           workspace_bytes, need);
   a.q = static_cast<const aoakv::f16*>(q);
@@ -630,7 +616,7 @@ static int fill_decode(aoakv::DecodeArgs& a, Workspace& w, const void* q, void* 
   a.Hq = num_qo_heads;
   a.Hkv = num_kv_heads;
   a.S = page_size;
-  a.max_chunks = tuned ? aoakv::decode_chunks(max_sel) : 0u;
+  a.max_chunks = aoakv::decode_chunks(max_sel);
   a.max_pages = max_pages;
   a.flags = flags & AOAKV_FLAG_QUEST_KERNEL;
   // grouped decode only where it changes anything (a group of 2 or more) and
@@ -797,8 +783,8 @@ int aoakv_sparse_decode_layer_noalloc(
   // the decode workspace this call lays out must fit the scratch array
   const uint32_t max_sel = max_selected(sel_pages, sel_stride, token_budget, token_budgets,
                                         max_pages, page_size, flags);
-  const size_t need = decode_ws_bytes(aoakv::tuned_shape(head_dim, page_size), batch_size,
-                                      num_qo_heads, num_kv_heads, max_sel, nullptr, nullptr);
+  const size_t need =
+      ws_layout(batch_size, num_qo_heads, num_kv_heads, max_sel, head_dim, nullptr, nullptr);
   REQUIRE(need <= kNoAllocScratchBytes,
           "sparse_decode_layer_noalloc: this call needs %zu bytes of scratch, more than the "
           "%zu the library holds per device (batch %u x %u query heads x %u selected pages)",
@@ -861,8 +847,8 @@ int aoakv_estimate_topk(const void* q, const void* metadata_data, const int32_t*
     return e;
   Workspace w{};
   const uint32_t max_sel = sel_stride < max_pages ? sel_stride : max_pages;
-  const size_t need = decode_ws_bytes(aoakv::tuned_shape(head_dim, page_size), batch_size,
-                                      num_qo_heads, num_kv_heads, max_sel, workspace, &w);
+  const size_t need =
+      ws_layout(batch_size, num_qo_heads, num_kv_heads, max_sel, head_dim, workspace, &w);
   REQUIRE(workspace_bytes >= need, "estimate_topk: workspace of %zu bytes < %zu needed",
           workspace_bytes, need);
   ea.error = w.ctl + aoakv::kErrWord;

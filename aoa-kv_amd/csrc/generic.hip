@@ -10,9 +10,9 @@
 //     reductions inside a group are butterflies of wave shuffles;
 //   * page scores: one lane group per page, then the existing top-k kernel
 //     (which takes any page size);
-//   * decode: one workgroup per (sequence, query head) over all of its
-//     selected pages, online softmax per lane group, merged in LDS (no
-//     split-K, no workspace beyond the error word);
+//   * decode: split over chunks of kGenChunkPages selected pages, one
+//     workgroup per (chunk, query head, sequence), online softmax per lane
+//     group, merged in LDS, then across chunks by the last to arrive;
 //   * prefill: one lane group per query, keys in order with an online
 //     softmax, no MFMA (the tuned MFMA kernel covers (128, 16)).
 // Arithmetic follows the tuned kernels where they define the reference's
@@ -314,26 +314,33 @@ __global__ __launch_bounds__(256) void gen_estimate_kernel(EstimateArgs a) {
 
 // ---------------------------------------------------------------- decode
 // Attention of query head hq of sequence b over its selected pages (or all
-// of them): one workgroup; wave w takes entries w, w + 4, ..., lane group v
-// of a wave the page's tokens v, v + 64/N, ...  Logits fp16(q.k), then
-// fp16(. / sqrt(d)) (quest_attention.py:265-268); online softmax in fp32;
-// the groups' (m, l, o) merged in LDS.  The quest_kernel convention attends
-// the last page after the nsel selected ones.
+// of them), split over chunks of kGenChunkPages entries: one workgroup per
+// (chunk, query head, sequence); wave w takes the chunk's entries w, w + 4,
+// ..., lane group v of a wave the page's tokens v, v + 64/N, ...  Logits
+// fp16(q.k), then fp16(. / sqrt(d)) (quest_attention.py:265-268); online
+// softmax in fp32; the groups' (m, l, o) merged in LDS into the chunk's
+// partial.  A head of one chunk writes its output directly; otherwise the
+// last chunk to arrive at the head's counter merges the partials in chunk
+// order (the same arithmetic whichever workgroup merges) and clears them.
+// The quest_kernel convention attends the last page after the nsel selected
+// ones.
 template <int D>
 __global__ __launch_bounds__(256) void gen_decode_kernel(DecodeArgs a) {
   constexpr uint32_t N = D / 8, GPW = kWave / N, G = 4u * GPW;  // groups per wave / block
+  constexpr uint32_t kStride = (uint32_t)D + 4u;                // partial: o[D], m, l, pad
   __shared__ float s_o[G][D];
   __shared__ float s_ml[G][2];
+  __shared__ uint32_t s_last;
   const uint32_t l = threadIdx.x % N, grp = threadIdx.x / N;
   const uint32_t wave = threadIdx.x / kWave, v = grp % GPW;
-  const uint32_t hq = blockIdx.x, b = blockIdx.y;
+  const uint32_t chunk = blockIdx.x, hq = blockIdx.y, b = blockIdx.z;
   const uint32_t hkv = hq / (a.Hq / a.Hkv);
   const bool quest = (a.flags & kFlagQuestKernel) != 0u;
   const uint32_t S = a.S;
   const uint32_t pbeg = (uint32_t)a.kv_indptr[b];
   const uint32_t P_table = (uint32_t)a.kv_indptr[b + 1] - pbeg;
   const uint32_t P = P_table < a.max_pages ? P_table : a.max_pages;
-  if (P != P_table && threadIdx.x == 0u) flag_error(a.error, kErrTruncated);
+  if (P != P_table && chunk == 0u && threadIdx.x == 0u) flag_error(a.error, kErrTruncated);
   const uint32_t lpl = (uint32_t)a.kv_last_page_len[b];
   if (P == 0u || lpl == 0u || lpl > S) return;  // malformed page table
   const uint32_t budget = a.token_budgets ? (uint32_t)a.token_budgets[b] : a.token_budget;
@@ -343,6 +350,13 @@ __global__ __launch_bounds__(256) void gen_decode_kernel(DecodeArgs a) {
     const uint32_t row_cap = a.sel_stride + (quest ? 1u : 0u);
     if (npages > row_cap) npages = row_cap;
   }
+  // the grid holds max_chunks chunks per head: never index partials past it
+  if (npages > a.max_chunks * kGenChunkPages) {
+    npages = a.max_chunks * kGenChunkPages;
+    if (chunk == 0u && threadIdx.x == 0u) flag_error(a.error, kErrTruncated);
+  }
+  const uint32_t nch = (npages + kGenChunkPages - 1u) / kGenChunkPages;
+  if (chunk >= nch) return;  // uniform per block
   const uint32_t nsel = (quest && a.sel != nullptr) ? npages - 1u : npages;
   const int32_t* sel_row = a.sel ? a.sel + ((size_t)b * a.Hkv + hkv) * a.sel_stride : nullptr;
   const uint32_t last_phys = (uint32_t)a.kv_indices[pbeg + P - 1u];
@@ -351,7 +365,9 @@ __global__ __launch_bounds__(256) void gen_decode_kernel(DecodeArgs a) {
   float m = -INFINITY, lsum = 0.f, o[kVec];
 #pragma unroll
   for (int j = 0; j < kVec; ++j) o[j] = 0.f;
-  for (uint32_t i = wave; i < npages; i += 4u) {
+  const uint32_t i1 = (chunk + 1u) * kGenChunkPages < npages ? (chunk + 1u) * kGenChunkPages
+                                                             : npages;
+  for (uint32_t i = chunk * kGenChunkPages + wave; i < i1; i += 4u) {
     uint32_t phys;
     if (a.sel == nullptr) phys = (uint32_t)a.kv_indices[pbeg + i];
     else phys = i < nsel ? (uint32_t)sel_row[i] : last_phys;
@@ -379,8 +395,9 @@ __global__ __launch_bounds__(256) void gen_decode_kernel(DecodeArgs a) {
     s_ml[grp][1] = lsum;
   }
   __syncthreads();
-  if (threadIdx.x < (uint32_t)D) {
-    const uint32_t d = threadIdx.x;
+  const size_t bh = (size_t)b * a.Hq + hq;
+  const uint32_t d = threadIdx.x;
+  if (d < (uint32_t)D) {
     float M = -INFINITY;
     for (uint32_t g2 = 0; g2 < G; ++g2) M = fmaxf(M, s_ml[g2][0]);
     float acc = 0.f, Ls = 0.f;
@@ -389,8 +406,39 @@ __global__ __launch_bounds__(256) void gen_decode_kernel(DecodeArgs a) {
       acc = acc + w * s_o[g2][d];
       Ls = Ls + w * s_ml[g2][1];
     }
-    a.o[((size_t)b * a.Hq + hq) * D + d] = r16(acc / Ls);
+    if (nch == 1u) {
+      a.o[bh * D + d] = r16(acc / Ls);
+    } else {
+      float* part = a.partial + (bh * a.max_chunks + chunk) * kStride;
+      st_agent(part + d, acc);
+      if (d == 0u) {
+        st_agent(part + D, M);
+        st_agent(part + D + 1u, Ls);
+      }
+    }
   }
+  if (nch == 1u) return;
+  if (!arrive_last(&a.counters[bh * kCounterStride], nch, &s_last)) return;
+  // the last chunk to arrive: merge every chunk's partial in chunk order,
+  // then clear the partials (the whole workspace stays zero between calls)
+  if (d < (uint32_t)D) {
+    const float* base = a.partial + bh * a.max_chunks * kStride;
+    float M = -INFINITY, Ls = 0.f, acc = 0.f;
+    for (uint32_t c = 0; c < nch; ++c) {
+      const float* part = base + c * kStride;
+      const float mc = ld_agent(part + D), lc = ld_agent(part + D + 1u), oc = ld_agent(part + d);
+      const float Mn = fmaxf(M, mc);
+      const float keep = M == -INFINITY ? 0.f : __expf(M - Mn);
+      const float w = mc == -INFINITY ? 0.f : __expf(mc - Mn);
+      Ls = Ls * keep + w * lc;
+      acc = acc * keep + w * oc;
+      M = Mn;
+    }
+    a.o[bh * D + d] = r16(acc / Ls);
+  }
+  __syncthreads();  // every thread has read the partials
+  uint32_t* pw = reinterpret_cast<uint32_t*>(a.partial + bh * a.max_chunks * kStride);
+  for (uint32_t i = threadIdx.x; i < nch * kStride; i += 256u) st_agent_u32(pw + i, 0u);
 }
 
 // ---------------------------------------------------------------- prefill
@@ -520,7 +568,8 @@ hipError_t launch_gen_estimate(const EstimateArgs& a, uint32_t batch, uint32_t m
 }
 
 hipError_t launch_gen_decode(const DecodeArgs& a, uint32_t batch, uint32_t D_, hipStream_t s) {
-  AOAKV_GEN_D(D_, hipLaunchKernelGGL(gen_decode_kernel<D>, dim3(a.Hq, batch), dim3(256), 0, s, a))
+  AOAKV_GEN_D(D_, hipLaunchKernelGGL(gen_decode_kernel<D>, dim3(a.max_chunks, a.Hq, batch),
+                                      dim3(256), 0, s, a))
   return hipGetLastError();
 }
 

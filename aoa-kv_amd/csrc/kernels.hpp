@@ -27,6 +27,10 @@ __device__ inline void flag_error(uint32_t* error, uint32_t bits) {
   if (error != nullptr) atomicOr(error, bits);
 }
 
+// Selected pages per decode chunk of the generic kernels (as the tuned
+// kernels' 8): the workspace's partials are laid out per chunk of 8.
+constexpr uint32_t kGenChunkPages = 8u;
+
 // Head dims the library takes: the tuned kernels are for kHeadDim (with
 // kPageSize); 64 and 256, and other page sizes up to kMaxPageSize, run the
 // kernels of generic.hip.

@@ -123,7 +123,7 @@ extern "C" {
  *                           pages only.  No access leaves the sized buffers. */
 #define AOAKV_WS_ERR_WORD 2u
 /* Bytes of the control words at the start of every workspace (the error
- * word among them). */
+ * word among them); no call needs fewer. */
 #define AOAKV_WORKSPACE_CTL_BYTES 256u
 #define AOAKV_WS_ERR_WAIT 1u
 #define AOAKV_WS_ERR_TRUNCATED 2u
@@ -271,11 +271,10 @@ int aoakv_topk_filtering(const float* scores, uint32_t score_stride,
  * aoakv_sparse_decode_layer (replaces the buffers BatchDecodeHandler
  * allocates in begin_forward, reference decode_handler.cuh:73-136).
  * max_sel_pages: upper bound on pages attended per (sequence, head).  The
- * size covers the tuned kernels (head_dim 128, page_size 16), which split a
- * head's pages into chunks of 8 merged through the workspace (at most 8192
- * pages per head); the other shapes run kernels that keep one workgroup per
- * query head, take any number of pages and use only the first
- * AOAKV_WORKSPACE_CTL_BYTES of a workspace.
+ * decode splits a head's pages into chunks of 8 whose partials (head_dim + 4
+ * floats each) are merged through the workspace; with head_dim 128 and
+ * page_size 16 (the tuned kernels) at most 8192 pages per head, with the
+ * other shapes any number.
  */
 size_t aoakv_decode_workspace_size(uint32_t batch_size, uint32_t num_qo_heads,
                                    uint32_t num_kv_heads, uint32_t head_dim,

@@ -135,12 +135,17 @@ void host_paths() {
                                                      AOAKV_FLAG_GROUPED_DECODE), nullptr);
       EXPECT(launched_or_hip(rc));
     }
-    // the generic shapes: control words only, any number of pages
+    // the generic shapes: any number of pages (12,500 chunks of 8 here)
     int rc = aoakv_decode_sparse_attn(fake(1), fake(2), fake(3), fake<int32_t>(4),
                                       fake<int32_t>(5), fake<int32_t>(6), nul, 0, 0, nul,
-                                      fake(7), AOAKV_WORKSPACE_CTL_BYTES, 1, 100000, 8, 2, 64, 1,
-                                      layout, 0, nullptr);
+                                      fake(7), aoakv_decode_workspace_size(1, 8, 2, 64, 100000),
+                                      1, 100000, 8, 2, 64, 1, layout, 0, nullptr);
     EXPECT(launched_or_hip(rc));
+    rc = aoakv_decode_sparse_attn(fake(1), fake(2), fake(3), fake<int32_t>(4), fake<int32_t>(5),
+                                  fake<int32_t>(6), nul, 0, 0, nul, fake(7),
+                                  AOAKV_WORKSPACE_CTL_BYTES, 1, 100000, 8, 2, 64, 1, layout, 0,
+                                  nullptr);
+    EXPECT(rc == AOAKV_ERR_INVALID);  // the partials do not fit
     rc = aoakv_estimate_topk(fake(1), fake(2), fake<int32_t>(3), fake<int32_t>(4),
                              fake<int32_t>(5), fake<int32_t>(6), fake<int32_t>(7), fake(8),
                              fake<float>(9), P, fake<int32_t>(10), 128, 2048, nul, fake(11),

@@ -216,9 +216,9 @@ def test_quest_kernel_convention_matches_oracle(D, S, layout, group, value_aware
 @pytest.mark.parametrize("D,S,layout", [(128, 1, HND), (64, 4, NHD)])
 def test_decode_beyond_the_split_k_limit(D, S, layout):
     """10000 pages per head, 9000 of them selected: more than the 8192 pages
-    per head the tuned kernels' split-K merge holds.  The generic kernels,
-    one workgroup per query head, take them with a workspace of only its
-    control words; sparse and dense decode against the oracle."""
+    per head (1024 chunks) the tuned kernels' split-K merge holds.  The
+    generic kernels' merge (chunk order, one workgroup) takes the 1125
+    chunks; sparse and dense decode against the oracle."""
     from aoakv import ops
     from aoakv.utils import decode_estimate, decode_layer, decode_sparse_attn, decode_topk
     _say(f"[shapes] beyond split-K D={D} S={S} layout={layout}")
@@ -228,7 +228,6 @@ def test_decode_beyond_the_split_k_limit(D, S, layout):
     V = randn16(D + 72, (1, H, L, D))
     q = randn16(D + 73, (1, H, 1, D))
     c = _ctrl(H, D, S, L + S, layout, k * S, shuffle=S + 3)
-    assert c.workspace.numel() == ops.WORKSPACE_CTL_BYTES
     _prefill(c, K, V)
     c.begin_forward(1)
     st = sim.SimLayerState(K, V, S)
