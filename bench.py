@@ -413,6 +413,92 @@ def gqa_bench(dev, layout, n_layers=8, hq=32, hkv=8, launches=256):
     return out
 
 
+def generic_shapes_bench(dev, layout, n_layers=4, launches=200):
+    """The shapes outside the tuned (128, 16) kernels at config 2's context
+    (32768 tokens) and budget (2048 tokens), H heads: the decode layer
+    (two launches: the generic scoring kernel and the standalone top-k, then
+    the split-K generic decode) and its scoring and decode kernels alone, us
+    per call from a HIP graph over n_layers rotated layers (past the
+    memory-side cache).  Keys (f"d{D}_s{S}"): head dim D, page size S."""
+    import torch
+    from aoakv import ops
+    out = {}
+    for D_, S_, H_ in ((64, 16, 32), (256, 16, 16), (128, 8, 32), (128, 32, 32)):
+        P_ = L // S_
+        Pm = math.ceil(P_ / S_)
+        shape = ((n_layers, P_, 2, H_, S_, D_) if layout == ops.HND
+                 else (n_layers, P_, 2, S_, H_, D_))
+        kv = torch.empty(shape, dtype=torch.float16, device=dev)
+        meta = torch.empty((n_layers, Pm) + shape[2:], dtype=torch.float16, device=dev)
+        lvn = torch.empty((n_layers, P_, H_), dtype=torch.float16, device=dev)
+        vmean = torch.empty((n_layers, P_, H_, D_), dtype=torch.float16, device=dev)
+        idx = torch.empty((n_layers, P_), dtype=torch.int32, device=dev)
+        midx = torch.arange(Pm, dtype=torch.int32, device=dev)
+        g = torch.Generator(device=dev).manual_seed(900 + D_ + S_)
+        q = torch.randn((n_layers, 1, H_, D_), generator=g, device=dev).half()
+        for l in range(n_layers):
+            k = torch.randn((L, H_, D_), generator=g, device=dev).half()
+            v = torch.randn((L, H_, D_), generator=g, device=dev).half()
+            idx[l] = torch.randperm(P_, generator=torch.Generator().manual_seed(l)).to(
+                device=dev, dtype=torch.int32)
+            ops.append_kv_cache_prefill(k, v, kv[l], idx[l], P_, S_, meta[l], midx, lvn[l],
+                                        vmean[l], layout)
+            del k, v
+        indptr = torch.tensor([0, P_], dtype=torch.int32, device=dev)
+        mindptr = torch.tensor([0, Pm], dtype=torch.int32, device=dev)
+        lpl = torch.tensor([S_], dtype=torch.int32, device=dev)
+        k_sel = min(max(3, BUDGET // S_), P_)
+        scores = torch.zeros((n_layers, 1, H_, P_), dtype=torch.float32, device=dev)
+        sel = torch.zeros((n_layers, 1, H_, k_sel), dtype=torch.int32, device=dev)
+        o = torch.zeros((n_layers, 1, H_, D_), dtype=torch.float16, device=dev)
+        ws = ops.decode_workspace(1, H_, H_, k_sel, dev, head_dim=D_)
+        fl = ops.FLAG_VALUE_AWARE | ops.FLAG_FIXED
+
+        def layer(l):
+            ops.sparse_decode_layer(q[l], o[l], kv[l], indptr, idx[l], lpl, meta[l], mindptr,
+                                    midx, lvn[l], scores[l], sel[l], BUDGET, ws, P_, layout, fl)
+
+        def est(l):
+            ops.estimate_attn_score(q[l], scores[l], meta[l], mindptr, midx, indptr, idx[l], lpl,
+                                    lvn[l], P_, layout, fl)
+
+        def dec(l):
+            ops.decode_sparse_attn(q[l], o[l], kv[l], indptr, idx[l], lpl, sel[l], BUDGET, ws,
+                                   P_, H_, layout)
+        res = {}
+        for name, fn in (("layer_us", layer), ("score_us", est), ("decode_us", dec)):
+            for l in range(n_layers):
+                fn(l)
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            st = torch.cuda.Stream()
+            st.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(st):
+                fn(0)
+            torch.cuda.current_stream().wait_stream(st)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(gr):
+                for i in range(launches):
+                    fn(i % n_layers)
+            gr.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda._sleep(100000)
+            e0.record()
+            gr.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            res[name] = round(e0.elapsed_time(e1) * 1e3 / launches, 2)
+            del gr
+        if ops.workspace_error(ws) != 0:
+            raise SystemExit(f"generic shape d{D_} s{S_}: workspace error {ops.workspace_error(ws)}")
+        res["heads"] = H_
+        out[f"d{D_}_s{S_}"] = res
+        del kv, meta, lvn, vmean
+        torch.cuda.empty_cache()
+    return out
+
+
 def _threads() -> int:
     try:
         from threadpoolctl import threadpool_info
@@ -978,6 +1064,8 @@ def main():
         extra["config5_ragged_batch16"] = ragged_batch_bench(dev, layout)
         log("[bench] GQA layer (32 / 8 heads) ...")
         extra["gqa_32q_8kv_32k"] = gqa_bench(dev, layout)
+        log("[bench] generic shapes (head dims 64 / 256, pages of 8 / 32) ...")
+        extra["generic_shapes_32k"] = generic_shapes_bench(dev, layout)
         # the same 32 layers in the other cache layout (the reference's
         # drop-in layout is NHD): same seeds, so the same bits are expected
         other = ops.NHD if layout == ops.HND else ops.HND
