@@ -892,7 +892,7 @@ int aoakv_prefill_with_paged_kv_cache(const void* q, void* o, const void* kv_dat
   a.g = aoakv::make_geom(layout, num_kv_heads, page_size, head_dim);
   hipStream_t s = static_cast<hipStream_t>(stream);
   return hip_status(aoakv::prefill_tuned_shape(head_dim, page_size)
-                        ? aoakv::launch_prefill(a, page_size, s)
+                        ? aoakv::launch_prefill(a, page_size, head_dim, s)
                         : aoakv::launch_gen_prefill(a, head_dim, s),
                     "prefill_with_paged_kv_cache");
 }

@@ -39,11 +39,11 @@ constexpr uint32_t kMaxPageSize = 32;
 inline bool tuned_shape(uint32_t head_dim, uint32_t page_size) {
   return head_dim == (uint32_t)kHeadDim && page_size == (uint32_t)kPageSize;
 }
-// The MFMA prefill also takes page sizes 8 and 32 (with kHeadDim): a wave's
-// 16 key rows of a tile then lie in two pages, or in half of one.
+// The MFMA prefill takes head dims 64 and 128 with page sizes 8, 16 and 32:
+// a wave's 16 key rows of a tile lie in two pages, one, or half of one.
 inline bool prefill_tuned_shape(uint32_t head_dim, uint32_t page_size) {
-  return head_dim == (uint32_t)kHeadDim && (page_size == 8u || page_size == 16u ||
-                                            page_size == 32u);
+  return (head_dim == 64u || head_dim == (uint32_t)kHeadDim) &&
+         (page_size == 8u || page_size == 16u || page_size == 32u);
 }
 
 // RoPE frequencies f_i = rcp_scale * rcp_theta^(2i / D), i < D / 2: fixed by
@@ -209,7 +209,8 @@ uint32_t est_chunks(uint32_t max_pages, uint32_t group);  // scoring items per (
 hipError_t launch_decode(const DecodeArgs& a, uint32_t batch, hipStream_t s,
                          const EstimateArgs* self = nullptr);
 hipError_t launch_fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s);
-hipError_t launch_prefill(const PrefillArgs& a, uint32_t page_size, hipStream_t s);
+hipError_t launch_prefill(const PrefillArgs& a, uint32_t page_size, uint32_t head_dim,
+                          hipStream_t s);
 
 // RMSNorm of `rows` fp16 rows of n elements (n a multiple of 8), one weight row.
 struct RmsNormArgs {

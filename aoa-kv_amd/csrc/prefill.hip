@@ -45,8 +45,6 @@ constexpr int kPfThreads = 256;
 constexpr int kPfQueriesPerWave = 32;
 constexpr int kPfQueriesPerBlock = 128;
 constexpr int kPfTileKeys = 64;
-constexpr int kPfRowBytes = kHeadDim * 2;                   // one key row
-constexpr int kPfTileBytes = kPfTileKeys * kPfRowBytes;     // 16 KB
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr uint32_t kXcds = 8;  // MI355X: 8 XCDs, workgroups dealt to them round-robin
 
@@ -69,26 +67,53 @@ __device__ inline float pair_sum(float x) {
 // row of accumulator register i for lane group g
 __device__ inline int crow(int i, int g) { return 8 * (i / 4) + 4 * g + (i % 4); }
 
-// Chunk swizzles (16-byte chunk j of key row r sits at chunk j ^ swz(r)).
-// K is read as one chunk of 32 consecutive rows per instruction: XOR with
-// r % 16 spreads them over all 16 chunk positions.  V is read with the
-// transpose read: a 16-lane group takes 2 adjacent chunks of 4 consecutive
-// rows (the other group of the half-wave the next 2 chunks), so XOR with
-// 4 * (r % 4) gives those 16 chunks distinct positions.
-__device__ inline int k_swz(int r) { return r & 15; }
-__device__ inline int v_swz(int r) { return 4 * (r & 3); }
+// Chunk swizzles (16-byte chunk j of key row r sits at chunk j ^ swz(r));
+// a row of D dims has CH = D / 8 chunks.  K is read as one chunk of 32
+// consecutive rows per instruction: XOR with r % CH spreads them over all
+// chunk positions.  V is read with the transpose read: a 16-lane group takes
+// 2 adjacent chunks of 4 consecutive rows (the other group of the half-wave
+// the next 2 chunks), so XOR with (CH / 4) * (r % 4) gives those chunks
+// distinct positions (D = 128: 16 chunks, conflict-free as measured).
+template <int CH>
+__device__ inline int k_swz(int r) { return r & (CH - 1); }
+template <int CH>
+__device__ inline int v_swz(int r) { return (CH / 4) * (r & 3); }
 
-// byte offset of 16-byte chunk j of key row r in a K tile
-__device__ inline int tile_off(int r, int j) { return r * kPfRowBytes + 16 * (j ^ k_swz(r)); }
+// One 16-byte global -> LDS copy per lane (the lane lands at byte 16 * lane
+// of `lds`).  A plain function: the builtin's operands inside the kernel
+// template would be value-dependent, and the host pass then drops the
+// kernel's launch stub.
+__device__ inline void load_lds16(const f16* g, char* lds) {
+  __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+}
 
-// S: tokens per page (8, 16 or 32).
-template <int S>
+// byte offset of 16-byte chunk j of key row r in a K tile of D-dim rows
+template <int D>
+__device__ inline int tile_off(int r, int j) { return r * (2 * D) + 16 * (j ^ k_swz<D / 8>(r)); }
+
+// Tile geometry of a D-dim head (namespace-scope constants: the kernel's
+// lambdas use them without capturing anything).
+template <int D>
+struct PfShape {
+  static constexpr int kRowBytes = D * 2;                        // one key row
+  static constexpr int kTileBytes = kPfTileKeys * kRowBytes;     // 16 KB at D = 128
+  static constexpr int kCh = kRowBytes / 16;                     // 16-byte chunks per row
+  static constexpr int kRPI = 1024 / kRowBytes;                  // rows per load instruction
+  static constexpr int kKS = D / 16;                             // k-steps of the score MFMAs
+  static constexpr int kDB = D / 32;                             // dim blocks of O
+};
+
+// S: tokens per page (8, 16 or 32); D: head dim (64 or 128).
+template <int S, int D>
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
   static_assert(S == 8 || S == 16 || S == 32, "a wave's 16 rows: two pages, one, or half of one");
+  static_assert(D == 64 || D == 128, "head dims of the MFMA prefill");
+  using Sh = PfShape<D>;
+
   // two buffers of [K | V] tiles, separate objects so the compiler sees that
   // the loads into one never alias the reads of the other (no wait on them)
-  __shared__ __attribute__((aligned(16))) char s_buf0[2 * kPfTileBytes];
-  __shared__ __attribute__((aligned(16))) char s_buf1[2 * kPfTileBytes];
+  __shared__ __attribute__((aligned(16))) char s_buf0[2 * Sh::kTileBytes];
+  __shared__ __attribute__((aligned(16))) char s_buf1[2 * Sh::kTileBytes];
   const int tid = threadIdx.x;
   const int lane = (int)__lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -123,18 +148,18 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
   if (wq_last >= Lq) wq_last = Lq - 1u;
   const uint32_t wave_kend = a.causal ? off + wq_last + 1u : L;
 
-  // ---- this lane's query, dims 16*s + 8*g .. +8 for s = 0..7
-  half8 qreg[8];
+  // ---- this lane's query, dims 16*s + 8*g .. +8 for s < D / 16
+  half8 qreg[Sh::kKS];
 #pragma unroll
-  for (int s = 0; s < 8; ++s)
-    qreg[s] = q_live ? *reinterpret_cast<const half8*>(a.q + ((size_t)q * a.Hq + h) * kHeadDim +
+  for (int s = 0; s < Sh::kKS; ++s)
+    qreg[s] = q_live ? *reinterpret_cast<const half8*>(a.q + ((size_t)q * a.Hq + h) * D +
                                                           16 * s + 8 * g)
                      : half8{};
 
   // ---- tile loader: wave w fills rows 16w .. 16w+15 of K and V (keys
-  // 64 t + 16 w ..), 4 rows (1 KB) per instruction; lane l lands at byte
-  // 16*l of its instruction's rows, i.e. row l/16, chunk slot l%16 -> it
-  // fetches the global chunk (l%16) ^ (row % 16).  The rows' pages: .x for
+  // 64 t + 16 w ..), 1 KB (Sh::kRPI rows) per instruction; lane l lands at byte
+  // 16*l of its instruction's rows, i.e. row l/Sh::kCh, chunk slot l%Sh::kCh -> it
+  // fetches the global chunk (l%Sh::kCh) ^ swz(row).  The rows' pages: .x for
   // rows 0..7 of the wave, .y for rows 8..15 (the same page unless S = 8).
   // A page past the sequence reads the last page (its keys are masked).
   // The page table is read through the constant address space: the kernel
@@ -152,18 +177,17 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
   };
   // token slot of the wave's row 0 in its page
   const uint32_t slot0 = S == 32 ? 16u * ((uint32_t)wave % 2u) : 0u;
-  const int lrow = lane / 16, lslot = lane % 16;
+  const int lrow = lane / Sh::kCh, lslot = lane % Sh::kCh;
   auto load_tile = [&](char* buf, uint2 phys) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 16 * wave + 4 * i + lrow;  // row in the tile; r % 16 = 4i + lrow
-      const uint32_t pg = i < 2 ? phys.x : phys.y;  // rows 0..7 / 8..15 of the wave
+    for (int i = 0; i < 16 / Sh::kRPI; ++i) {
+      const int r = 16 * wave + Sh::kRPI * i + lrow;  // row in the tile; r % 16 = Sh::kRPI i + lrow
+      const uint32_t pg = Sh::kRPI * i < 8 ? phys.x : phys.y;  // rows 0..7 / 8..15 of the wave
       const size_t e = elem_off(a.g, pg, 0, hkv, (slot0 + (uint32_t)(r & 15)) % S);
-      __builtin_amdgcn_global_load_lds(a.kv + e + 8 * (lslot ^ k_swz(r)),
-                                       buf + (16 * wave + 4 * i) * kPfRowBytes, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(a.kv + e + a.g.kv + 8 * (lslot ^ v_swz(r)),
-                                       buf + kPfTileBytes + (16 * wave + 4 * i) * kPfRowBytes, 16, 0,
-                                       0);
+      load_lds16(a.kv + e + 8 * (lslot ^ k_swz<Sh::kCh>(r)),
+                 buf + (16 * wave + Sh::kRPI * i) * Sh::kRowBytes);
+      load_lds16(a.kv + e + a.g.kv + 8 * (lslot ^ v_swz<Sh::kCh>(r)),
+                 buf + Sh::kTileBytes + (16 * wave + Sh::kRPI * i) * Sh::kRowBytes);
     }
   };
 
@@ -174,25 +198,25 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
   auto v_off = [&](int t, int key0) {
     const int row = key0 + vm;
     const int dim = 32 * t + 16 * (vG % 2) + 4 * va4;
-    return row * kPfRowBytes + 16 * ((dim / 8) ^ v_swz(row)) + 2 * (dim % 8);
+    return row * Sh::kRowBytes + 16 * ((dim / 8) ^ v_swz<Sh::kCh>(row)) + 2 * (dim % 8);
   };
 
   // lane-constant byte offsets inside a tile (the loop adds the buffer base)
-  int k_off[8], v_lo[4], v_hi[4];
+  int k_off[Sh::kKS], v_lo[Sh::kDB], v_hi[Sh::kDB];
 #pragma unroll
-  for (int s8 = 0; s8 < 8; ++s8) k_off[s8] = tile_off(c, 2 * s8 + g);  // + ks * 32 rows below
+  for (int s8 = 0; s8 < Sh::kKS; ++s8) k_off[s8] = tile_off<D>(c, 2 * s8 + g);  // + ks * 32 rows below
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {  // key0 = 4g (+ ks*32 + 16*hf below) and key0 + 8
+  for (int t = 0; t < Sh::kDB; ++t) {  // key0 = 4g (+ ks*32 + 16*hf below) and key0 + 8
     v_lo[t] = v_off(t, 4 * g);
     v_hi[t] = v_off(t, 4 * g + 8);
   }
   // adding whole multiples of 16 rows keeps both swizzles: offsets step by
   // 16 rows
-  constexpr int kRow16 = 16 * kPfRowBytes;
+  constexpr int kRow16 = 16 * Sh::kRowBytes;
 
-  floatx16 acc_o[4];
+  floatx16 acc_o[Sh::kDB];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) acc_o[t] = floatx16{};
+  for (int t = 0; t < Sh::kDB; ++t) acc_o[t] = floatx16{};
   float m_run = -INFINITY, l_run = 0.f;  // running max of the unscaled scores
   const float scale = a.sm_scale * kLog2e;
   // smallest query position of this wave: tiles with every key at or below
@@ -202,27 +226,27 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
   // one 64-key tile from LDS buffer `tile_base`
   auto tile = [&](const lds_char* tile_base, uint32_t k0) {
     const lds_char* sK = tile_base;
-    const lds_char* sV = tile_base + kPfTileBytes;
+    const lds_char* sV = tile_base + Sh::kTileBytes;
     // ---- S^T = K Q^T for two 32-key sub-tiles.  All 8 K fragments of a
     // sub-tile are read before its MFMAs, and the second sub-tile's reads
     // go out before the first sub-tile's MFMAs, so no MFMA waits on a
     // just-issued LDS read.
     floatx16 acc_s[2];
-    half8 kf0[8], kf1[8];
+    half8 kf0[Sh::kKS], kf1[Sh::kKS];
 #pragma unroll
-    for (int s8 = 0; s8 < 8; ++s8)
+    for (int s8 = 0; s8 < Sh::kKS; ++s8)
       kf0[s8] = *reinterpret_cast<const __attribute__((address_space(3))) half8*>(sK + k_off[s8]);
 #pragma unroll
-    for (int s8 = 0; s8 < 8; ++s8)
+    for (int s8 = 0; s8 < Sh::kKS; ++s8)
       kf1[s8] = *reinterpret_cast<const __attribute__((address_space(3))) half8*>(
           sK + k_off[s8] + 2 * kRow16);
     __builtin_amdgcn_sched_barrier(0);
     acc_s[0] = floatx16{};
 #pragma unroll
-    for (int s8 = 0; s8 < 8; ++s8) acc_s[0] = mfma32(kf0[s8], qreg[s8], acc_s[0]);
+    for (int s8 = 0; s8 < Sh::kKS; ++s8) acc_s[0] = mfma32(kf0[s8], qreg[s8], acc_s[0]);
     acc_s[1] = floatx16{};
 #pragma unroll
-    for (int s8 = 0; s8 < 8; ++s8) acc_s[1] = mfma32(kf1[s8], qreg[s8], acc_s[1]);
+    for (int s8 = 0; s8 < Sh::kKS; ++s8) acc_s[1] = mfma32(kf1[s8], qreg[s8], acc_s[1]);
     // ---- causal / length mask (only where a key can be past L or past
     // some query of the wave), running max of this query
     const bool full = k0 + kPfTileKeys <= L && (!a.causal || k0 + kPfTileKeys - 1u <= wave_q0);
@@ -267,7 +291,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
       const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale);  // m_run = -inf: 0
       l_run = l_run * alpha;
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+      for (int t = 0; t < Sh::kDB; ++t)
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc_o[t][i] *= alpha;
     }
@@ -294,12 +318,12 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
     half8 vfa[4], vfb[4];
     vfrags(0, vfa);
 #pragma unroll
-    for (int t = 0; t < 4; t += 2) {
+    for (int t = 0; t < Sh::kDB; t += 2) {
       vfrags(t + 1, vfb);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) acc_o[t] = mfma32(vfa[kk], pb[kk / 2][kk % 2], acc_o[t]);
-      if (t + 2 < 4) vfrags(t + 2, vfa);
+      if (t + 2 < Sh::kDB) vfrags(t + 2, vfa);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) acc_o[t + 1] = mfma32(vfb[kk], pb[kk / 2][kk % 2], acc_o[t + 1]);
@@ -327,10 +351,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
         // last page's unwritten slots, or the last page read again): their
         // probability is exactly 0, but 0 * NaN is NaN in the MFMA, so their
         // V rows are zeroed before any wave reads them
-        char* vbuf = (u == 0u ? s_buf0 : s_buf1) + kPfTileBytes;
+        char* vbuf = (u == 0u ? s_buf0 : s_buf1) + Sh::kTileBytes;
         const uint32_t first_dead = L - ti * kPfTileKeys;  // < kPfTileKeys
-        for (uint32_t i = first_dead * (kPfRowBytes / 16u) + threadIdx.x;
-             i < (uint32_t)kPfTileKeys * (kPfRowBytes / 16u); i += kPfThreads)
+        for (uint32_t i = first_dead * (Sh::kRowBytes / 16u) + threadIdx.x;
+             i < (uint32_t)kPfTileKeys * (Sh::kRowBytes / 16u); i += kPfThreads)
           reinterpret_cast<uint4*>(vbuf)[i] = uint4{0u, 0u, 0u, 0u};
         __syncthreads();
       }
@@ -342,9 +366,9 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
   // ---- o = O / l: lane holds its query's dims t*32 + crow(i, g)
   if (!q_live) return;
   const float inv_l = 1.f / l_run;
-  f16* orow = a.o + ((size_t)q * a.Hq + h) * kHeadDim;
+  f16* orow = a.o + ((size_t)q * a.Hq + h) * D;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
+  for (int t = 0; t < Sh::kDB; ++t) {
 #pragma unroll
     for (int i0 = 0; i0 < 16; i0 += 4) {
       half4 v;
@@ -355,17 +379,24 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
   }
 }
 
-hipError_t launch_prefill(const PrefillArgs& a, uint32_t page_size, hipStream_t s) {
+hipError_t launch_prefill(const PrefillArgs& a, uint32_t page_size, uint32_t head_dim,
+                          hipStream_t s) {
   const uint32_t nqt = (a.Lq + kPfQueriesPerBlock - 1) / kPfQueriesPerBlock;
   const uint32_t per = (nqt * a.Hq + kXcds - 1) / kXcds;
   const dim3 grid(per * kXcds), block(kPfThreads);
-  switch (page_size) {
-    case 8: hipLaunchKernelGGL(prefill_kernel<8>, grid, block, 0, s, a); break;
-    case 16: hipLaunchKernelGGL(prefill_kernel<16>, grid, block, 0, s, a); break;
-    case 32: hipLaunchKernelGGL(prefill_kernel<32>, grid, block, 0, s, a); break;
-    default: return hipErrorInvalidValue;
+#define AOAKV_PF(S_, D_)                                                     \
+  if (page_size == S_ && head_dim == D_) {                                   \
+    hipLaunchKernelGGL((prefill_kernel<S_, D_>), grid, block, 0, s, a);      \
+    return hipGetLastError();                                                \
   }
-  return hipGetLastError();
+  AOAKV_PF(8, 128)
+  AOAKV_PF(16, 128)
+  AOAKV_PF(32, 128)
+  AOAKV_PF(8, 64)
+  AOAKV_PF(16, 64)
+  AOAKV_PF(32, 64)
+#undef AOAKV_PF
+  return hipErrorInvalidValue;
 }
 
 }  // namespace aoakv

@@ -182,20 +182,20 @@ def decode_appends(dev, layout, n_app=512, mode="append", graph=True):
     return eager, e0.elapsed_time(e1) * 1e3 / n_app
 
 
-def prefill_bench(dev, layout, L, reps=5, page_size=S):
+def prefill_bench(dev, layout, L, reps=5, page_size=S, head_dim=D):
     """Config 4: causal paged prefill, 32 heads x 128, q/K/V ~ N(0, 0.5^2)
-    (pages of 16 tokens; page_size 8 or 32 for the same kernel's other
-    instantiations).  FLOPs as the reference's nvbench counts them
-    (bench_prefill.cu:109-111): L * (2L - L) * 2 * H * D."""
+    (pages of 16 tokens; page_size 8 or 32, or head_dim 64, for the same
+    kernel's other instantiations).  FLOPs as the reference's nvbench counts
+    them (bench_prefill.cu:109-111): L * (2L - L) * 2 * H * D."""
     import torch
     from aoakv import ops
     from aoakv.utils import InferenceController, append_kv
-    c = InferenceController(1, H, D, page_size, 64, L + page_size, torch.float16, dev,
+    c = InferenceController(1, H, head_dim, page_size, 64, L + page_size, torch.float16, dev,
                             layout=layout)
     g = torch.Generator(device=dev).manual_seed(0)
-    q = (torch.randn((L, H, D), generator=g, device=dev) * 0.5).half()
-    k = (torch.randn((L, H, D), generator=g, device=dev) * 0.5).half()
-    v = (torch.randn((L, H, D), generator=g, device=dev) * 0.5).half()
+    q = (torch.randn((L, H, head_dim), generator=g, device=dev) * 0.5).half()
+    k = (torch.randn((L, H, head_dim), generator=g, device=dev) * 0.5).half()
+    v = (torch.randn((L, H, head_dim), generator=g, device=dev) * 0.5).half()
     c.prepare_metadata(L)
     c.begin_forward(L)
     append_kv(k, v, c, 0)
@@ -212,7 +212,7 @@ def prefill_bench(dev, layout, L, reps=5, page_size=S):
     e1.record()
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / reps
-    flops = L * (2 * L - L) * 2 * H * D
+    flops = L * (2 * L - L) * 2 * H * head_dim
     return us, flops / (us * 1e-6) / 1e12
 
 
@@ -848,6 +848,9 @@ def main():
             us, tf = prefill_bench(dev, layout, 8192, page_size=ps)
             res[f"prefill_8k_page{ps}_us"] = round(us, 1)
             res[f"prefill_8k_page{ps}_TFLOPs"] = round(tf, 1)
+        us, tf = prefill_bench(dev, layout, 8192, head_dim=64)  # head dim 64 (32 heads)
+        res["prefill_8k_d64_us"] = round(us, 1)
+        res["prefill_8k_d64_TFLOPs"] = round(tf, 1)
         res["build"] = so_identity()
         print(json.dumps(res))
         return
@@ -1060,6 +1063,9 @@ def main():
             us, tf = prefill_bench(dev, layout, 8192, page_size=ps)
             extra[f"prefill_8k_page{ps}_us"] = round(us, 1)
             extra[f"prefill_8k_page{ps}_TFLOPs"] = round(tf, 1)
+        us, tf = prefill_bench(dev, layout, 8192, head_dim=64)  # head dim 64 (32 heads)
+        extra["prefill_8k_d64_us"] = round(us, 1)
+        extra["prefill_8k_d64_TFLOPs"] = round(tf, 1)
         log("[bench] config 5 (ragged batch) ...")
         extra["config5_ragged_batch16"] = ragged_batch_bench(dev, layout)
         log("[bench] GQA layer (32 / 8 heads) ...")
