@@ -559,7 +559,9 @@ size_t aoakv_layer_workspace_size(uint32_t batch_size, uint32_t num_qo_heads,
                                   uint32_t max_sel_pages, uint32_t max_pages) {
   const size_t dec = ws_layout(batch_size, num_qo_heads, num_kv_heads, max_sel_pages, head_dim,
                                nullptr, nullptr);
-  return score_words_offset(dec) + (size_t)batch_size * num_kv_heads * max_pages * 4u;
+  // score words: a copy per query head at most (self-selecting decode items
+  // of GQA read one each)
+  return score_words_offset(dec) + (size_t)batch_size * num_qo_heads * max_pages * 4u;
 }
 
 int aoakv_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
@@ -710,11 +712,16 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
     // with room for them (aoakv_layer_workspace_size), the scores also go to
     // the top-k as handoff words, polled directly (no arrival counter)
     const size_t words_off = score_words_offset(w.bytes);
-    if (workspace_bytes >= words_off + (size_t)batch_size * num_kv_heads * max_pages * 4u) {
+    const size_t words_row = (size_t)batch_size * num_kv_heads * max_pages * 4u;
+    if (workspace_bytes >= words_off + words_row) {
       la.e.hscore = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + words_off);
       la.e.hscore_stride = max_pages;
+      la.e.hscore_copies = 1u;
     }
     const uint32_t group = num_qo_heads / num_kv_heads;
+    // self-selecting decode items read a copy of the score words per decode
+    // block of the group, so each block's merging item clears its own
+    const uint32_t copies = group / da.heads_per_item;
     // NHD: a head's metadata entries are 256-byte pieces 8 KB apart, so the
     // scoring items take two adjacent heads (512-byte runs) over half the
     // pages; they hand every score over as a word, so only with the words
@@ -736,12 +743,14 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
     // holds, the 16 copies of every top-k cost more than the handoff they
     // save (config 5, 512 heads: 316 vs 250 us per layer).
     la.self_select = la.e.hscore != nullptr &&
+                             workspace_bytes >= words_off + words_row * copies &&
                              la.n_workers + la.n_dec <=
                                  resident_layer_workgroups(num_qo_heads / num_kv_heads,
                                                            da.heads_per_item, la.score_heads)
                          ? 1u
                          : 0u;
     la.n_heads = la.self_select ? 0u : batch_size * num_kv_heads;
+    if (la.self_select) la.e.hscore_copies = copies;
     return hip_status(aoakv::launch_layer(la, s), "sparse_decode_layer");
   }
   if (tuned && max_pages <= aoakv::fused_topk_max_pages()) {

@@ -738,14 +738,18 @@ __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, ui
   }
   __syncthreads();
   {
-    const uint32_t hh = threadIdx.x / kPPB;  // < HPI for the storing threads
-    const uint32_t p = chunk * kPPB + threadIdx.x % kPPB;
+    constexpr uint32_t kNsc = kPPB * HPI;  // scores of the item (<= 128)
+    const uint32_t j = threadIdx.x % kNsc;
+    const uint32_t hh = j / kPPB;  // < HPI
+    const uint32_t p = chunk * kPPB + j % kPPB;
     const uint32_t nstore = (a.flags & kFlagQuestKernel) ? P - 1u : P;
-    if (threadIdx.x < kPPB * HPI && p < nstore) {
-      const size_t bh = (size_t)b * a.Hkv + h + hh;
-      st_agent(a.scores + bh * a.score_stride + p, s_sc[threadIdx.x]);
-      if (a.hscore != nullptr)
-        st_agent_u32(a.hscore + bh * a.hscore_stride + p, to_word(s_sc[threadIdx.x]));
+    const size_t bh = (size_t)b * a.Hkv + h + hh;
+    if (threadIdx.x < kNsc && p < nstore) st_agent(a.scores + bh * a.score_stride + p, s_sc[j]);
+    // the handoff words: copy c of the row by threads [c * kNsc, (c + 1) * kNsc)
+    // (hscore_copies * kNsc <= 128: a copy per decode block of the group)
+    if (a.hscore != nullptr && threadIdx.x < kNsc * a.hscore_copies && p < nstore) {
+      const uint32_t c = threadIdx.x / kNsc;
+      st_agent_u32(a.hscore + (bh * a.hscore_copies + c) * a.hscore_stride + p, to_word(s_sc[j]));
     }
   }
 
@@ -792,7 +796,7 @@ __device__ __forceinline__ void select_item(const EstimateArgs& a, uint32_t b, u
   const uint32_t gi = a.hsel_gi > 1u ? a.hsel_gi : 1u;
   uint32_t* hout = handoff ? a.hsel + ((size_t)b * a.Hq + h * GROUP) * a.hsel_stride : nullptr;
   uint32_t* hwords =
-      a.hscore ? a.hscore + ((size_t)b * a.Hkv + h) * a.hscore_stride : nullptr;
+      a.hscore ? a.hscore + ((size_t)b * a.Hkv + h) * a.hscore_copies * a.hscore_stride : nullptr;
   topk_staged(a.scores + ((size_t)b * a.Hkv + h) * a.score_stride, P, k,
               (a.flags & kFlagFixed) != 0u, a.kv_indices + pbeg,
               a.sel + ((size_t)b * a.Hkv + h) * a.sel_stride, tk, hout, a.hsel_stride * gi,
@@ -936,9 +940,10 @@ struct DecShared {
 //   SELF (one launch): instead of polling a selection, the workgroup runs the
 //     kv head's top-k itself from the score words (every chunk of the head
 //     computes the same selection) and keeps its entries; the merging chunk
-//     clears the score words at the end (with G < group, the last of the
-//     group's merging chunks to finish, counted per (sequence, kv head)).
-//     clear_ctr: that counter (G < group only).
+//     clears the score words at the end.  With G < group each block of G
+//     query heads reads a copy of its own (hscore_copies = group / G rows
+//     per kv head), so its merging chunk clears that copy without waiting
+//     for the group's other heads.
 // QUEST (quest_kernel convention): the selection rows hold the pages chosen
 // besides the last page, which is always attended as the final entry
 // (quest/utils/__init__.py:237, approx_attn.cu:68-151).
@@ -950,7 +955,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
                                             uint32_t chunk, DecShared<G>& sm,
                                             const EstimateArgs* ea = nullptr,
                                             TopkShared* tk = nullptr, uint32_t* s_err = nullptr,
-                                            uint32_t err0 = 0u, uint32_t* clear_ctr = nullptr) {
+                                            uint32_t err0 = 0u) {
   // SELF without HANDOFF (the two-launch decode): the scores are complete
   // (written by the previous launch), read as floats, nothing to wait for
   // or clear
@@ -963,10 +968,6 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   const uint32_t group = a.Hq / a.Hkv;
   const uint32_t hkv = hq0 / group;
   const size_t bh0 = (size_t)b * a.Hq + hq0;  // the item's first query head
-  // the item whose merge ends the use of the kv head's score words clears
-  // them: G = group, the merging chunk; G < group, the last of the group's
-  // merging chunks (clear_ctr); a malformed sequence's first query head
-  const bool words_owner = (uint32_t)G == group || clear_ctr == nullptr;
   const uint32_t idx0 = chunk * kDecPagesPerBlock + wave * kDecPagesPerWave;
   const uint32_t* sel_row =
       a.sel ? reinterpret_cast<const uint32_t*>(a.sel) + ((size_t)b * a.Hkv + hkv) * a.sel_stride
@@ -1005,7 +1006,11 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   uint32_t* words = nullptr;
   if constexpr (SELF) {
     pl = plan_select(*ea, b);
-    if (HANDOFF) words = ea->hscore + ((size_t)b * ea->Hkv + hkv) * ea->hscore_stride;
+    // this block's copy of the kv head's score words
+    if (HANDOFF)
+      words = ea->hscore + (((size_t)b * ea->Hkv + hkv) * ea->hscore_copies +
+                            (ea->hscore_copies > 1u ? (hq0 % group) / (uint32_t)G : 0u)) *
+                               ea->hscore_stride;
   }
   // waits until the score words [0, pl.P) are written, then clears them
   auto consume_words = [&]() {
@@ -1029,7 +1034,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   if (P != P_table && chunk == 0u && threadIdx.x == 0u) flag_error(a.error, kErrTruncated);
   if (P == 0u || lpl == 0u || lpl > S) {  // malformed page table
     // the words were written all the same: consumed once per kv head
-    if (SELF && HANDOFF && chunk == 0u && hq0 % group == 0u) consume_words();
+    if (SELF && HANDOFF && chunk == 0u) consume_words();  // (this block's copy)
     return;
   }
   // physical id of the sequence's last page (the one holding lpl tokens)
@@ -1407,29 +1412,12 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   }
   if constexpr (SELF && HANDOFF) {
     // every chunk's partial arrived, and each chunk stored its partial after
-    // its top-k had read the score words: clear them (without a top-k no one
-    // waited for them, so wait first).  With G < group the group's other
-    // query heads may still be reading them: the last merging item of the
-    // group to get here clears them and resets the count.
-    bool mine = words_owner;
-    if (!mine) {
-      __syncthreads();  // every thread of this item is done with the words
-      if (threadIdx.x == 0u) {
-        const uint32_t prev =
-            __hip_atomic_fetch_add(clear_ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const bool last = prev == group / (uint32_t)G - 1u;
-        if (last) __hip_atomic_store(clear_ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        sm.last = last ? 1u : 0u;
-      }
-      __syncthreads();
-      mine = sm.last != 0u;
-    }
-    if (mine) {
-      if (self_topk) {
-        for (uint32_t i = threadIdx.x; i < pl.P; i += kThreads) st_agent_u32(words + i, 0u);
-      } else {
-        consume_words();
-      }
+    // its top-k had read this block's copy of the score words: clear it
+    // (without a top-k no one waited for them, so wait first)
+    if (self_topk) {
+      for (uint32_t i = threadIdx.x; i < pl.P; i += kThreads) st_agent_u32(words + i, 0u);
+    } else {
+      consume_words();
     }
   }
 }
@@ -1602,11 +1590,7 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la)
       const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
       sleep_until(t0, (uint64_t)(unit < first_round ? unit : first_round) * la.stagger_ps);
       TL(kTlStaggerDone);
-      // with GI < GROUP the group's merging items count who is done with the
-      // score words on the kv head's arrival counter (unused by SELF's scoring)
-      uint32_t* ctr = GI < GROUP ? la.e.counters + bkv * kCounterStride : nullptr;
-      decode_item<true, QUEST, true, GI>(la.d, b, hq0, chunk, sm.d, &la.e, &sm.e.tk, &s_err, err0,
-                                         ctr);
+      decode_item<true, QUEST, true, GI>(la.d, b, hq0, chunk, sm.d, &la.e, &sm.e.tk, &s_err, err0);
     } else {
       decode_item<true, QUEST, false, GI>(la.d, b, hq0, chunk, sm.d, nullptr, nullptr, &s_err,
                                           err0);

@@ -122,10 +122,13 @@ struct EstimateArgs {
   uint32_t hsel_stride;
   uint32_t hsel_gi;    // query heads per decode item (rows b * Hq + hq0 are read)
   // single launch only, optional: the scores again as handoff words (bits +
-  // 1, 0 = not yet written), [B, Hkv, hscore_stride]; the top-k polls these
-  // instead of an arrival counter and clears them
+  // 1, 0 = not yet written), [B, Hkv, hscore_copies, hscore_stride]; the
+  // top-k polls these instead of an arrival counter and clears them.  With
+  // self-selecting decode items, one copy per decode block of the group
+  // (group / heads_per_item), each read and cleared by that block's items
   uint32_t* hscore;
   uint32_t hscore_stride;
+  uint32_t hscore_copies;
   uint32_t* error;  // workspace error word, or nullptr (no workspace)
 };
 

@@ -282,9 +282,10 @@ size_t aoakv_decode_workspace_size(uint32_t batch_size, uint32_t num_qo_heads,
 
 /*
  * Workspace bytes for aoakv_sparse_decode_layer with AOAKV_FLAG_SINGLE_LAUNCH
- * at its fastest: the decode workspace plus one word per (sequence, kv head,
- * page) through which the launch's scoring items hand their scores to its
- * top-k (polled directly, no arrival counter).  A workspace of only
+ * at its fastest: the decode workspace plus one word per (sequence, query
+ * head, page) through which the launch's scoring items hand their scores to
+ * its top-k (polled directly, no arrival counter; with GQA a copy per query
+ * head, which that head's decode items read and clear).  A workspace of only
  * aoakv_decode_workspace_size bytes still works (counter handoff).  No
  * counterpart in the reference (its decode handler sizes its own buffers,
  * decode_handler.cuh:73-136).
