@@ -39,11 +39,12 @@ constexpr uint32_t kMaxPageSize = 32;
 inline bool tuned_shape(uint32_t head_dim, uint32_t page_size) {
   return head_dim == (uint32_t)kHeadDim && page_size == (uint32_t)kPageSize;
 }
-// The MFMA prefill takes head dims 64 and 128 with page sizes 8, 16 and 32:
-// a wave's 16 key rows of a tile lie in two pages, one, or half of one.
+// The MFMA prefill takes head dims 64, 128 and 256 with page sizes 1, 2, 4,
+// 8, 16 and 32: a wave's 16 key rows of a tile lie in 16 / S pages, or half
+// of one.
 inline bool prefill_tuned_shape(uint32_t head_dim, uint32_t page_size) {
-  return (head_dim == 64u || head_dim == (uint32_t)kHeadDim) &&
-         (page_size == 8u || page_size == 16u || page_size == 32u);
+  return (head_dim == 64u || head_dim == (uint32_t)kHeadDim || head_dim == 256u) &&
+         page_size != 0u && page_size <= 32u && (page_size & (page_size - 1u)) == 0u;
 }
 
 // RoPE frequencies f_i = rcp_scale * rcp_theta^(2i / D), i < D / 2: fixed by

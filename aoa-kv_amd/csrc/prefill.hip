@@ -24,8 +24,9 @@
 // and the V transpose reads hit distinct banks (no LDS bank conflicts,
 // measured with SQ_LDS_BANK_CONFLICT).  Each wave
 // loads 16 rows per tile: one page of 16 tokens, half a page of 32 or two
-// pages of 8, so its page ids are one or two scalar loads, fetched a tile
-// ahead.  The V^T operand of O^T += V^T P^T is read from the
+// pages of 8, so its page ids are one or two scalar loads; with pages of 1,
+// 2 or 4 tokens, each lane loads the id of the page of its rows (one vector
+// load per load instruction).  Either way fetched a tile ahead.  The V^T operand of O^T += V^T P^T is read from the
 // row-major V tile with ds_read_b64_tr_b16: in each 16-lane group, output
 // lane 4a+b receives element b of the 8-byte blocks addressed by lanes a,
 // a+4, a+8, a+12 (checked on the hardware), so four lanes pointing at four
@@ -103,11 +104,18 @@ struct PfShape {
   static constexpr int kDB = D / 32;                             // dim blocks of O
 };
 
-// S: tokens per page (8, 16 or 32); D: head dim (64 or 128).
+// Workgroups per CU: two at head dims 64 and 128 (64 KB of LDS and at most
+// 256 registers per lane each); one at 256, whose tiles take 128 KB and whose
+// O accumulators alone 128 registers (one wave per SIMD, up to 512).
+template <int D>
+constexpr int pf_blocks_per_cu() { return D == 256 ? 1 : 2; }
+
+// S: tokens per page (1, 2, 4, 8, 16 or 32); D: head dim (64, 128 or 256).
 template <int S, int D>
-__global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
-  static_assert(S == 8 || S == 16 || S == 32, "a wave's 16 rows: two pages, one, or half of one");
-  static_assert(D == 64 || D == 128, "head dims of the MFMA prefill");
+__global__ __launch_bounds__(kPfThreads, pf_blocks_per_cu<D>()) void prefill_kernel(PrefillArgs a) {
+  static_assert(S == 1 || S == 2 || S == 4 || S == 8 || S == 16 || S == 32,
+                "a wave's 16 rows: 16 / S pages, or half of one");
+  static_assert(D == 64 || D == 128 || D == 256, "head dims of the MFMA prefill");
   using Sh = PfShape<D>;
 
   // two buffers of [K | V] tiles, separate objects so the compiler sees that
@@ -159,30 +167,48 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
   // ---- tile loader: wave w fills rows 16w .. 16w+15 of K and V (keys
   // 64 t + 16 w ..), 1 KB (Sh::kRPI rows) per instruction; lane l lands at byte
   // 16*l of its instruction's rows, i.e. row l/Sh::kCh, chunk slot l%Sh::kCh -> it
-  // fetches the global chunk (l%Sh::kCh) ^ swz(row).  The rows' pages: .x for
-  // rows 0..7 of the wave, .y for rows 8..15 (the same page unless S = 8).
-  // A page past the sequence reads the last page (its keys are masked).
-  // The page table is read through the constant address space: the kernel
-  // never writes it, and a scalar load keeps it off the vector memory
-  // counter that the K/V tile loads are waited on with.
+  // fetches the global chunk (l%Sh::kCh) ^ swz(row).  The page of load
+  // instruction i's rows: S >= 8, id[i] (rows 0..7 of the wave one page,
+  // rows 8..15 the same or, S = 8, the next); S < 8, each lane's own row's
+  // page.  A page past the sequence reads the last page (its keys are
+  // masked).  With S >= 8 the page table is read through the constant
+  // address space: the kernel never writes it, and a scalar load keeps it
+  // off the vector memory counter that the K/V tile loads are waited on with.
+  constexpr int kNI = 16 / Sh::kRPI;  // load instructions per wave and tile
+  struct PageIds {
+    uint32_t id[kNI];
+  };
   const __attribute__((address_space(4))) int32_t* kv_idx =
       (const __attribute__((address_space(4))) int32_t*)a.kv_indices;
-  auto page_of = [&](uint32_t tile) -> uint2 {
+  const int lrow = lane / Sh::kCh, lslot = lane % Sh::kCh;
+  auto page_of = [&](uint32_t tile) -> PageIds {
     const uint32_t key0 = tile * kPfTileKeys + 16u * (uint32_t)wave;  // the wave's first row
-    uint32_t p0 = key0 / S, p1 = (key0 + 8u) / S;
-    p0 = p0 < npages ? p0 : npages - 1u;
-    p1 = p1 < npages ? p1 : npages - 1u;
-    const uint32_t x = (uint32_t)kv_idx[p0];
-    return uint2{x, S == 8 ? (uint32_t)kv_idx[p1] : x};
+    PageIds ph;
+    if constexpr (S >= 8) {
+      uint32_t p0 = key0 / S, p1 = (key0 + 8u) / S;
+      p0 = p0 < npages ? p0 : npages - 1u;
+      p1 = p1 < npages ? p1 : npages - 1u;
+      const uint32_t x = (uint32_t)kv_idx[p0];
+      const uint32_t y = S == 8 ? (uint32_t)kv_idx[p1] : x;
+#pragma unroll
+      for (int i = 0; i < kNI; ++i) ph.id[i] = Sh::kRPI * i < 8 ? x : y;
+    } else {
+#pragma unroll
+      for (int i = 0; i < kNI; ++i) {
+        uint32_t p = (key0 + (uint32_t)(Sh::kRPI * i + lrow)) / S;
+        p = p < npages ? p : npages - 1u;
+        ph.id[i] = (uint32_t)a.kv_indices[p];
+      }
+    }
+    return ph;
   };
   // token slot of the wave's row 0 in its page
   const uint32_t slot0 = S == 32 ? 16u * ((uint32_t)wave % 2u) : 0u;
-  const int lrow = lane / Sh::kCh, lslot = lane % Sh::kCh;
-  auto load_tile = [&](char* buf, uint2 phys) {
+  auto load_tile = [&](char* buf, const PageIds& phys) {
 #pragma unroll
-    for (int i = 0; i < 16 / Sh::kRPI; ++i) {
+    for (int i = 0; i < kNI; ++i) {
       const int r = 16 * wave + Sh::kRPI * i + lrow;  // row in the tile; r % 16 = Sh::kRPI i + lrow
-      const uint32_t pg = Sh::kRPI * i < 8 ? phys.x : phys.y;  // rows 0..7 / 8..15 of the wave
+      const uint32_t pg = phys.id[i];
       const size_t e = elem_off(a.g, pg, 0, hkv, (slot0 + (uint32_t)(r & 15)) % S);
       load_lds16(a.kv + e + 8 * (lslot ^ k_swz<Sh::kCh>(r)),
                  buf + (16 * wave + Sh::kRPI * i) * Sh::kRowBytes);
@@ -227,26 +253,62 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
   auto tile = [&](const lds_char* tile_base, uint32_t k0) {
     const lds_char* sK = tile_base;
     const lds_char* sV = tile_base + Sh::kTileBytes;
-    // ---- S^T = K Q^T for two 32-key sub-tiles.  All 8 K fragments of a
+    // ---- S^T = K Q^T for two 32-key sub-tiles.  All K fragments of a
     // sub-tile are read before its MFMAs, and the second sub-tile's reads
     // go out before the first sub-tile's MFMAs, so no MFMA waits on a
-    // just-issued LDS read.
+    // just-issued LDS read.  At D = 256 (16 fragments per sub-tile) they go
+    // in batches of 8, each read while the previous batch's MFMAs run, to
+    // keep the registers of one wave per SIMD.
     floatx16 acc_s[2];
-    half8 kf0[Sh::kKS], kf1[Sh::kKS];
+    if constexpr (Sh::kKS <= 8) {
+      half8 kf0[Sh::kKS], kf1[Sh::kKS];
 #pragma unroll
-    for (int s8 = 0; s8 < Sh::kKS; ++s8)
-      kf0[s8] = *reinterpret_cast<const __attribute__((address_space(3))) half8*>(sK + k_off[s8]);
+      for (int s8 = 0; s8 < Sh::kKS; ++s8)
+        kf0[s8] = *reinterpret_cast<const __attribute__((address_space(3))) half8*>(sK + k_off[s8]);
 #pragma unroll
-    for (int s8 = 0; s8 < Sh::kKS; ++s8)
-      kf1[s8] = *reinterpret_cast<const __attribute__((address_space(3))) half8*>(
-          sK + k_off[s8] + 2 * kRow16);
-    __builtin_amdgcn_sched_barrier(0);
-    acc_s[0] = floatx16{};
+      for (int s8 = 0; s8 < Sh::kKS; ++s8)
+        kf1[s8] = *reinterpret_cast<const __attribute__((address_space(3))) half8*>(
+            sK + k_off[s8] + 2 * kRow16);
+      __builtin_amdgcn_sched_barrier(0);
+      acc_s[0] = floatx16{};
 #pragma unroll
-    for (int s8 = 0; s8 < Sh::kKS; ++s8) acc_s[0] = mfma32(kf0[s8], qreg[s8], acc_s[0]);
-    acc_s[1] = floatx16{};
+      for (int s8 = 0; s8 < Sh::kKS; ++s8) acc_s[0] = mfma32(kf0[s8], qreg[s8], acc_s[0]);
+      acc_s[1] = floatx16{};
 #pragma unroll
-    for (int s8 = 0; s8 < Sh::kKS; ++s8) acc_s[1] = mfma32(kf1[s8], qreg[s8], acc_s[1]);
+      for (int s8 = 0; s8 < Sh::kKS; ++s8) acc_s[1] = mfma32(kf1[s8], qreg[s8], acc_s[1]);
+    } else {
+      constexpr int kB = 8;                      // fragments per batch
+      constexpr int kNB = 2 * Sh::kKS / kB;      // batches per tile (both sub-tiles)
+      auto kread = [&](int bt, half8 (&kf)[kB]) {  // batch bt: sub-tile bt / (kNB / 2)
+#pragma unroll
+        for (int j = 0; j < kB; ++j) {
+          const int s8 = (bt % (kNB / 2)) * kB + j;
+          kf[j] = *reinterpret_cast<const __attribute__((address_space(3))) half8*>(
+              sK + k_off[s8] + (bt / (kNB / 2)) * 2 * kRow16);
+        }
+      };
+      half8 kfa[kB], kfb[kB];
+      acc_s[0] = floatx16{};
+      acc_s[1] = floatx16{};
+      kread(0, kfa);
+#pragma unroll
+      for (int bt = 0; bt < kNB; bt += 2) {
+        kread(bt + 1, kfb);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < kB; ++j) {
+          const int s8 = (bt % (kNB / 2)) * kB + j;
+          acc_s[bt / (kNB / 2)] = mfma32(kfa[j], qreg[s8], acc_s[bt / (kNB / 2)]);
+        }
+        if (bt + 2 < kNB) kread(bt + 2, kfa);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < kB; ++j) {
+          const int s8 = ((bt + 1) % (kNB / 2)) * kB + j;
+          acc_s[(bt + 1) / (kNB / 2)] = mfma32(kfb[j], qreg[s8], acc_s[(bt + 1) / (kNB / 2)]);
+        }
+      }
+    }
     // ---- causal / length mask (only where a key can be past L or past
     // some query of the wave), running max of this query
     const bool full = k0 + kPfTileKeys <= L && (!a.causal || k0 + kPfTileKeys - 1u <= wave_q0);
@@ -331,7 +393,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillArgs a) {
   };
 
   load_tile(s_buf0, page_of(0u));
-  uint2 phys_next = page_of(1u);
+  PageIds phys_next = page_of(1u);
   // two tiles per trip: even tiles in buffer 0, odd tiles in buffer 1
   for (uint32_t it = 0; it < ntiles; it += 2) {
 #pragma unroll
@@ -389,12 +451,24 @@ hipError_t launch_prefill(const PrefillArgs& a, uint32_t page_size, uint32_t hea
     hipLaunchKernelGGL((prefill_kernel<S_, D_>), grid, block, 0, s, a);      \
     return hipGetLastError();                                                \
   }
+  AOAKV_PF(1, 128)
+  AOAKV_PF(2, 128)
+  AOAKV_PF(4, 128)
   AOAKV_PF(8, 128)
   AOAKV_PF(16, 128)
   AOAKV_PF(32, 128)
+  AOAKV_PF(1, 64)
+  AOAKV_PF(2, 64)
+  AOAKV_PF(4, 64)
   AOAKV_PF(8, 64)
   AOAKV_PF(16, 64)
   AOAKV_PF(32, 64)
+  AOAKV_PF(1, 256)
+  AOAKV_PF(2, 256)
+  AOAKV_PF(4, 256)
+  AOAKV_PF(8, 256)
+  AOAKV_PF(16, 256)
+  AOAKV_PF(32, 256)
 #undef AOAKV_PF
   return hipErrorInvalidValue;
 }

@@ -184,8 +184,8 @@ def decode_appends(dev, layout, n_app=512, mode="append", graph=True):
 
 def prefill_bench(dev, layout, L, reps=5, page_size=S, head_dim=D):
     """Config 4: causal paged prefill, 32 heads x 128, q/K/V ~ N(0, 0.5^2)
-    (pages of 16 tokens; page_size 8 or 32, or head_dim 64, for the same
-    kernel's other instantiations).  FLOPs as the reference's nvbench counts
+    (pages of 16 tokens; page_size 1, 8 or 32, or head_dim 64 or 256, for
+    the same kernel's other instantiations).  FLOPs as the reference's nvbench counts
     them (bench_prefill.cu:109-111): L * (2L - L) * 2 * H * D."""
     import torch
     from aoakv import ops
@@ -844,13 +844,14 @@ def main():
             res[f"prefill_{Lp // 1024}k_us"] = round(us, 1)
             res[f"prefill_{Lp // 1024}k_TFLOPs"] = round(tf, 1)
             res[f"prefill_{Lp // 1024}k_mfma_frac"] = round(tf / 2500.0, 4)
-        for ps in (8, 32):  # the same kernel on pages of 8 and 32 tokens
+        for ps in (1, 8, 32):  # the same kernel on pages of 1, 8 and 32 tokens
             us, tf = prefill_bench(dev, layout, 8192, page_size=ps)
             res[f"prefill_8k_page{ps}_us"] = round(us, 1)
             res[f"prefill_8k_page{ps}_TFLOPs"] = round(tf, 1)
-        us, tf = prefill_bench(dev, layout, 8192, head_dim=64)  # head dim 64 (32 heads)
-        res["prefill_8k_d64_us"] = round(us, 1)
-        res["prefill_8k_d64_TFLOPs"] = round(tf, 1)
+        for hd in (64, 256):  # head dims 64 and 256 (32 heads)
+            us, tf = prefill_bench(dev, layout, 8192, head_dim=hd)
+            res[f"prefill_8k_d{hd}_us"] = round(us, 1)
+            res[f"prefill_8k_d{hd}_TFLOPs"] = round(tf, 1)
         res["build"] = so_identity()
         print(json.dumps(res))
         return
@@ -1059,13 +1060,14 @@ def main():
             extra[f"prefill_{Lp // 1024}k_us"] = round(us, 1)
             extra[f"prefill_{Lp // 1024}k_TFLOPs"] = round(tf, 1)
             extra[f"prefill_{Lp // 1024}k_mfma_frac"] = round(tf / 2500.0, 4)
-        for ps in (8, 32):  # the same MFMA kernel on pages of 8 and 32 tokens
+        for ps in (1, 8, 32):  # the same MFMA kernel on pages of 1, 8 and 32 tokens
             us, tf = prefill_bench(dev, layout, 8192, page_size=ps)
             extra[f"prefill_8k_page{ps}_us"] = round(us, 1)
             extra[f"prefill_8k_page{ps}_TFLOPs"] = round(tf, 1)
-        us, tf = prefill_bench(dev, layout, 8192, head_dim=64)  # head dim 64 (32 heads)
-        extra["prefill_8k_d64_us"] = round(us, 1)
-        extra["prefill_8k_d64_TFLOPs"] = round(tf, 1)
+        for hd in (64, 256):  # head dims 64 and 256 (32 heads)
+            us, tf = prefill_bench(dev, layout, 8192, head_dim=hd)
+            extra[f"prefill_8k_d{hd}_us"] = round(us, 1)
+            extra[f"prefill_8k_d{hd}_TFLOPs"] = round(tf, 1)
         log("[bench] config 5 (ragged batch) ...")
         extra["config5_ragged_batch16"] = ragged_batch_bench(dev, layout)
         log("[bench] GQA layer (32 / 8 heads) ...")

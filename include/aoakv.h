@@ -414,7 +414,9 @@ int aoakv_estimate_topk(const void* q, const void* metadata_data, const int32_t*
  * h / (num_qo_heads / num_kv_heads)).  The queries are the last qo_len
  * positions of the L = (num_kv_pages-1)*page_size + kv_last_page_len
  * cached tokens; query i attends keys <= L - qo_len + i when causal.
- * fp16 inputs, fp32 accumulation (MFMA), fp16 output.
+ * fp16 inputs, fp32 accumulation, fp16 output: on the matrix cores (MFMA)
+ * for head_dim 64 / 128 / 256 at page sizes 1, 2, 4, 8, 16 and 32, on a
+ * vector kernel for the other page sizes.
  */
 int aoakv_prefill_with_paged_kv_cache(const void* q, void* o, const void* kv_data,
                                       const int32_t* kv_indices, uint32_t num_kv_pages,

@@ -257,13 +257,15 @@ def test_decode_beyond_the_split_k_limit(D, S, layout):
 @pytest.mark.parametrize("D,S,layout", [(64, 16, HND), (256, 16, NHD), (128, 8, NHD),
                                         (128, 32, HND), (128, 8, HND), (128, 32, NHD),
                                         (64, 8, NHD), (64, 32, HND), (64, 16, NHD),
-                                        (128, 1, HND), (256, 7, HND)])
+                                        (128, 1, HND), (256, 7, HND), (64, 1, NHD),
+                                        (128, 2, NHD), (64, 4, HND), (128, 4, NHD),
+                                        (256, 1, HND), (256, 32, HND), (256, 8, NHD)])
 @pytest.mark.parametrize("L,Lq,group", [(300, 300, 1), (333, 70, 2), (1100, 1100, 1),
                                         (777, 300, 4)])
 def test_prefill_matches_causal_attention(D, S, layout, L, Lq, group):
     from aoakv import ops
     _say(f"[shapes] prefill D={D} S={S} layout={layout} L={L} Lq={Lq} group={group}")
-    if L > 1000 and not (D in (64, 128) and S in (8, 16, 32)):
+    if L > 1000 and not (D in (64, 128, 256) and S in (1, 2, 4, 8, 16, 32)):
         pytest.skip("the long case is for the MFMA kernel's page sizes (several query tiles)")
     Hkv = 2
     Hq = Hkv * group
