@@ -523,6 +523,25 @@ def test_gqa_selection_and_decode(Hq, Hkv, L, budget):
     args = (qd, o, kv, indptr, idx, lpl, meta, mindptr, midx, lvn, scores, sel, budget, ws, P, HND)
     ops.sparse_decode_layer(*args)
     _single_launch_matches(args, {}, o.cpu().numpy(), sel.cpu().numpy(), ws)
+    # a workspace with the score words once per kv head, not once per query
+    # head: the one-launch layer then runs one top-k workgroup per kv head on
+    # the words (no self-selecting copies), with the same bits
+    from aoakv import _lib
+    lib = _lib.load()
+    n1 = -(-lib.aoakv_decode_workspace_size(1, Hq, Hkv, D, k) // 256) * 256 + Hkv * P * 4
+    assert n1 < lib.aoakv_layer_workspace_size(1, Hq, Hkv, D, k, P)
+    ws1 = torch.zeros(n1, dtype=torch.uint8, device=DEV)
+    o_two, sel_two = o.cpu().numpy(), sel.cpu().numpy()
+    for rep in range(2):
+        o.fill_(0)
+        sel.fill_(-1)
+        ops.sparse_decode_layer(*args[:13], ws1, *args[14:],
+                                flags=ops.FLAG_VALUE_AWARE | ops.FLAG_FIXED | ops.FLAG_SINGLE_LAUNCH)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(o.cpu().numpy()), bits(o_two)), rep
+        assert np.array_equal(sel.cpu().numpy(), sel_two), rep
+        assert ops.workspace_error(ws1) == 0
+        assert int(ws1.count_nonzero().item()) == 0, "workspace left non-zero"
     sc = scores.cpu().numpy()[0]
     np.testing.assert_allclose(sc, scores_ref[0, :, 0], rtol=1e-5, atol=1e-4)
     sl = sel.cpu().numpy()[0]
