@@ -365,26 +365,56 @@ __global__ __launch_bounds__(256) void gen_decode_kernel(DecodeArgs a) {
   float m = -INFINITY, lsum = 0.f, o[kVec];
 #pragma unroll
   for (int j = 0; j < kVec; ++j) o[j] = 0.f;
-  const uint32_t i1 = (chunk + 1u) * kGenChunkPages < npages ? (chunk + 1u) * kGenChunkPages
-                                                             : npages;
-  for (uint32_t i = chunk * kGenChunkPages + wave; i < i1; i += 4u) {
+  const uint32_t ib = chunk * kGenChunkPages;  // the chunk's first entry (< npages)
+  const uint32_t i1 = ib + kGenChunkPages < npages ? ib + kGenChunkPages : npages;
+  // The wave's (at most two) pages, entries ib + wave and ib + wave + 4, and
+  // their token counts (0: no page).  Group v takes tokens v, v + GPW, ...
+  // of each page.  The K/V loads go out in batches of kB (page, token)
+  // slots, all of a batch before any is used (unconditional loads of
+  // clamped addresses: a slot past its page's tokens reads the page's slot
+  // 0, a missing page the chunk's first), so a wave waits on memory once
+  // per batch instead of once per token slot; the arithmetic runs in the
+  // same order as token by token.
+  constexpr uint32_t kTPG = (kMaxPageSize + GPW - 1u) / GPW;  // token slots of a group per page
+  constexpr uint32_t kF = 2u * kTPG;                          // ... over the wave's two pages
+  constexpr uint32_t kB = kF < 8u ? kF : 8u;                  // slots loaded together
+  uint32_t ph[2], nt[2];
+#pragma unroll
+  for (uint32_t k = 0; k < 2u; ++k) {
+    const uint32_t i = ib + wave + 4u * k;
+    const uint32_t ic = i < i1 ? i : ib;
     uint32_t phys;
-    if (a.sel == nullptr) phys = (uint32_t)a.kv_indices[pbeg + i];
-    else phys = i < nsel ? (uint32_t)sel_row[i] : last_phys;
-    const uint32_t ntok = phys == last_phys ? lpl : S;
-    for (uint32_t t = v; t < ntok; t += GPW) {
-      const H8 kk = ld16(a.kv + elem_off(a.g, phys, 0, hkv, t) + l * kVec);
-      const H8 vv = ld16(a.kv + elem_off(a.g, phys, 1, hkv, t) + l * kVec);
+    if (a.sel == nullptr) phys = (uint32_t)a.kv_indices[pbeg + ic];
+    else phys = ic < nsel ? (uint32_t)sel_row[ic] : last_phys;
+    ph[k] = phys;
+    nt[k] = i < i1 ? (phys == last_phys ? lpl : S) : 0u;
+  }
+  for (uint32_t f0 = 0; f0 < kF; f0 += kB) {
+    H8 kk[kB], vv[kB];
+#pragma unroll
+    for (uint32_t u = 0; u < kB; ++u) {
+      const uint32_t f = f0 + u, k = f / kTPG, j = f % kTPG;
+      if (GPW * j >= S) continue;  // uniform: slots past the page size
+      const uint32_t t = v + GPW * j;
+      const uint32_t tc = t < nt[k] ? t : 0u;
+      kk[u] = ld16(a.kv + elem_off(a.g, ph[k], 0, hkv, tc) + l * kVec);
+      vv[u] = ld16(a.kv + elem_off(a.g, ph[k], 1, hkv, tc) + l * kVec);
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kB; ++u) {
+      const uint32_t f = f0 + u, k = f / kTPG, j = f % kTPG;
+      const uint32_t t = v + GPW * j;
+      if (GPW * j >= S || t >= nt[k]) continue;  // (whole lane groups)
       float acc = 0.f;
 #pragma unroll
-      for (int j = 0; j < kVec; ++j) acc = acc + (float)q.v[j] * (float)kk.v[j];
+      for (int jj = 0; jj < kVec; ++jj) acc = acc + (float)q.v[jj] * (float)kk[u].v[jj];
       const float x = (float)r16((float)r16(grp_sum<N>(acc)) / sqrt_d<D>());
       const float mn = fmaxf(m, x);
       const float c = m == -INFINITY ? 0.f : __expf(m - mn);
       const float p = __expf(x - mn);
       lsum = lsum * c + p;
 #pragma unroll
-      for (int j = 0; j < kVec; ++j) o[j] = o[j] * c + p * (float)vv.v[j];
+      for (int jj = 0; jj < kVec; ++jj) o[jj] = o[jj] * c + p * (float)vv[u].v[jj];
       m = mn;
     }
   }
@@ -422,17 +452,29 @@ __global__ __launch_bounds__(256) void gen_decode_kernel(DecodeArgs a) {
   // the last chunk to arrive: merge every chunk's partial in chunk order,
   // then clear the partials (the whole workspace stays zero between calls)
   if (d < (uint32_t)D) {
+    // in groups of 16 chunks, every load of a group issued before any is
+    // used (one memory round trip per group), folded in chunk order
     const float* base = a.partial + bh * a.max_chunks * kStride;
     float M = -INFINITY, Ls = 0.f, acc = 0.f;
-    for (uint32_t c = 0; c < nch; ++c) {
-      const float* part = base + c * kStride;
-      const float mc = ld_agent(part + D), lc = ld_agent(part + D + 1u), oc = ld_agent(part + d);
-      const float Mn = fmaxf(M, mc);
-      const float keep = M == -INFINITY ? 0.f : __expf(M - Mn);
-      const float w = mc == -INFINITY ? 0.f : __expf(mc - Mn);
-      Ls = Ls * keep + w * lc;
-      acc = acc * keep + w * oc;
-      M = Mn;
+    for (uint32_t c0 = 0; c0 < nch; c0 += 16u) {
+      float mc[16], lc[16], oc[16];
+#pragma unroll
+      for (uint32_t u = 0; u < 16u; ++u) {
+        const float* part = base + (c0 + u < nch ? c0 + u : nch - 1u) * kStride;
+        mc[u] = ld_agent(part + D);
+        lc[u] = ld_agent(part + D + 1u);
+        oc[u] = ld_agent(part + d);
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < 16u; ++u) {
+        if (c0 + u >= nch) break;  // uniform
+        const float Mn = fmaxf(M, mc[u]);
+        const float keep = M == -INFINITY ? 0.f : __expf(M - Mn);
+        const float w = mc[u] == -INFINITY ? 0.f : __expf(mc[u] - Mn);
+        Ls = Ls * keep + w * lc[u];
+        acc = acc * keep + w * oc[u];
+        M = Mn;
+      }
     }
     a.o[bh * D + d] = r16(acc / Ls);
   }
