@@ -267,14 +267,40 @@ __global__ __launch_bounds__(256) void gen_estimate_kernel(EstimateArgs a) {
 #pragma unroll
   for (int g = 0; g < GROUP; ++g)
     q[g] = ld16(a.q + ((size_t)b * a.Hq + h * GROUP + g) * D + l * kVec);
-  const uint32_t p_end = (blockIdx.x + 1u) * kGenPagesPerBlock < nstore
-                             ? (blockIdx.x + 1u) * kGenPagesPerBlock
-                             : nstore;
-  for (uint32_t p = blockIdx.x * kGenPagesPerBlock + threadIdx.x / N; p < p_end; p += PPS) {
-    const uint32_t mpage = (uint32_t)a.meta_indices[mbeg + p / a.S];
-    const size_t off = elem_off(a.g, mpage, 0, h, p % a.S) + l * kVec;
-    const H8 kmx = ld16(a.meta + off);
-    const H8 kmn = ld16(a.meta + off + a.g.kv);
+  const uint32_t pb = blockIdx.x * kGenPagesPerBlock;  // the block's first page
+  if (pb >= nstore) return;                            // uniform
+  const uint32_t p_end = pb + kGenPagesPerBlock < nstore ? pb + kGenPagesPerBlock : nstore;
+  // The block's pages in kSt steps of PPS, group g taking page pb + g + s *
+  // PPS at step s.  Every step's page-table words are loaded together, then
+  // every step's metadata and value statistic (unconditional loads of
+  // clamped pages: a page past the block's end reads its first), so the
+  // block waits on two round trips, not two or three per step; the scores
+  // are computed in the same order as step by step.
+  constexpr uint32_t kSt = kGenPagesPerBlock / PPS;
+  uint32_t mpg[kSt], phys[kSt];
+#pragma unroll
+  for (uint32_t st = 0; st < kSt; ++st) {
+    const uint32_t p = pb + threadIdx.x / N + st * PPS;
+    const uint32_t pc = p < p_end ? p : pb;
+    mpg[st] = (uint32_t)a.meta_indices[mbeg + pc / a.S];
+    phys[st] = value_aware ? (uint32_t)a.kv_indices[pbeg + pc] : 0u;
+  }
+  H8 kmxs[kSt], kmns[kSt];
+  f16 lvn[kSt];
+#pragma unroll
+  for (uint32_t st = 0; st < kSt; ++st) {
+    const uint32_t p = pb + threadIdx.x / N + st * PPS;
+    const uint32_t pc = p < p_end ? p : pb;
+    const size_t off = elem_off(a.g, mpg[st], 0, h, pc % a.S) + l * kVec;
+    kmxs[st] = ld16(a.meta + off);
+    kmns[st] = ld16(a.meta + off + a.g.kv);
+    lvn[st] = value_aware ? a.v_log_norm[(size_t)phys[st] * a.Hkv + h] : (f16)0.f;
+  }
+#pragma unroll
+  for (uint32_t st = 0; st < kSt; ++st) {
+    const uint32_t p = pb + threadIdx.x / N + st * PPS;
+    if (p >= p_end) break;  // (whole lane groups; later steps lie further on)
+    const H8 kmx = kmxs[st], kmn = kmns[st];
     float x[GROUP];
 #pragma unroll
     for (int g = 0; g < GROUP; ++g) {
@@ -301,8 +327,7 @@ __global__ __launch_bounds__(256) void gen_estimate_kernel(EstimateArgs a) {
         for (int g = 0; g < GROUP; ++g) se = se + expf(x[g] - m);
         score = logf(se) + m;
       }
-      const uint32_t phys = (uint32_t)a.kv_indices[pbeg + p];
-      score = score + 2.0f * (float)a.v_log_norm[(size_t)phys * a.Hkv + h];
+      score = score + 2.0f * (float)lvn[st];
     } else {
       score = x[0];
 #pragma unroll
