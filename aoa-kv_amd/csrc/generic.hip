@@ -33,6 +33,23 @@ __device__ inline float grp_sum(float x) {
   return x;
 }
 
+// The same sum over a lane group through DPP within a row (and, for 32
+// lanes, one LDS permute between the two rows) instead of LDS permutes
+// throughout: a few cycles per DPP step where a permute waits on the LDS
+// unit.  Groups are aligned to half-rows (N = 8), rows (16) or row pairs
+// (32), so every lane read belongs to the same group.  (Another summation
+// order than grp_sum.)
+template <uint32_t N>
+__device__ inline float grp_sum_dpp(float x) {
+  static_assert(N == 8u || N == 16u || N == 32u, "lane groups of 8, 16 or 32");
+  x = x + dpp<kQuadSwap1>(x);
+  x = x + dpp<kQuadSwap2>(x);
+  x = x + dpp<kRowHalfMirror>(x);
+  if constexpr (N >= 16u) x = x + dpp<kRowMirror>(x);
+  if constexpr (N == 32u) x = x + __shfl_xor(x, 16, kWave);
+  return x;
+}
+
 // sqrt(D) as the fp32 the simulation divides by (math.sqrt(head_dim))
 template <int D>
 __device__ __host__ constexpr float sqrt_d() {
@@ -433,7 +450,7 @@ __global__ __launch_bounds__(256) void gen_decode_kernel(DecodeArgs a) {
       float acc = 0.f;
 #pragma unroll
       for (int jj = 0; jj < kVec; ++jj) acc = acc + (float)q.v[jj] * (float)kk[u].v[jj];
-      const float x = (float)r16((float)r16(grp_sum<N>(acc)) / sqrt_d<D>());
+      const float x = (float)r16((float)r16(grp_sum_dpp<N>(acc)) / sqrt_d<D>());
       const float mn = fmaxf(m, x);
       const float c = m == -INFINITY ? 0.f : __expf(m - mn);
       const float p = __expf(x - mn);
