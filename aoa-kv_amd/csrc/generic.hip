@@ -327,7 +327,7 @@ __global__ __launch_bounds__(256) void gen_estimate_kernel(EstimateArgs a) {
         const float qv = (float)q[g].v[j];
         acc = acc + fmaxf(qv * (float)kmx.v[j], qv * (float)kmn.v[j]);
       }
-      x[g] = grp_sum<N>(acc);
+      x[g] = grp_sum_dpp<N>(acc);
     }
     float score;
     if (value_aware) {
