@@ -357,8 +357,10 @@ __global__ __launch_bounds__(256) void gen_estimate_kernel(EstimateArgs a) {
 // ---------------------------------------------------------------- decode
 // Attention of query head hq of sequence b over its selected pages (or all
 // of them), split over chunks of kGenChunkPages entries: one workgroup per
-// (chunk, query head, sequence); wave w takes the chunk's entries w, w + 4,
-// ..., lane group v of a wave the page's tokens v, v + 64/N, ...  Logits
+// (chunk, query head, sequence) of W waves; wave w takes the chunk's entries
+// w, w + W, ..., lane group v of a wave the page's tokens v, v + 64/N, ...
+// W = 8 (a page per wave) when the grid has no more workgroups than the GPU
+// has CUs, else 4 (fewer registers per workgroup, more of them resident).  Logits
 // fp16(q.k), then fp16(. / sqrt(d)) (quest_attention.py:265-268); online
 // softmax in fp32; the groups' (m, l, o) merged in LDS into the chunk's
 // partial.  A head of one chunk writes its output directly; otherwise the
@@ -366,9 +368,10 @@ __global__ __launch_bounds__(256) void gen_estimate_kernel(EstimateArgs a) {
 // order (the same arithmetic whichever workgroup merges) and clears them.
 // The quest_kernel convention attends the last page after the nsel selected
 // ones.
-template <int D>
-__global__ __launch_bounds__(256) void gen_decode_kernel(DecodeArgs a) {
-  constexpr uint32_t N = D / 8, GPW = kWave / N, G = 4u * GPW;  // groups per wave / block
+template <int D, uint32_t W>
+__global__ __launch_bounds__(W * 64) void gen_decode_kernel(DecodeArgs a) {
+  static_assert(W == 4u || W == 8u, "4 or 8 waves");
+  constexpr uint32_t N = D / 8, GPW = kWave / N, G = W * GPW;  // groups per wave / block
   constexpr uint32_t kStride = (uint32_t)D + 4u;                // partial: o[D], m, l, pad
   __shared__ float s_o[G][D];
   __shared__ float s_ml[G][2];
@@ -409,21 +412,22 @@ __global__ __launch_bounds__(256) void gen_decode_kernel(DecodeArgs a) {
   for (int j = 0; j < kVec; ++j) o[j] = 0.f;
   const uint32_t ib = chunk * kGenChunkPages;  // the chunk's first entry (< npages)
   const uint32_t i1 = ib + kGenChunkPages < npages ? ib + kGenChunkPages : npages;
-  // The wave's (at most two) pages, entries ib + wave and ib + wave + 4, and
-  // their token counts (0: no page).  Group v takes tokens v, v + GPW, ...
-  // of each page.  The K/V loads go out in batches of kB (page, token)
+  // The wave's pages, entries ib + wave, ib + wave + W, ..., and their token
+  // counts (0: no page).  Group v takes tokens v, v + GPW, ... of each.  The
+  // K/V loads go out in batches of kB (page, token)
   // slots, all of a batch before any is used (unconditional loads of
   // clamped addresses: a slot past its page's tokens reads the page's slot
   // 0, a missing page the chunk's first), so a wave waits on memory once
   // per batch instead of once per token slot; the arithmetic runs in the
   // same order as token by token.
+  constexpr uint32_t kPPW = kGenChunkPages / W;              // pages per wave
   constexpr uint32_t kTPG = (kMaxPageSize + GPW - 1u) / GPW;  // token slots of a group per page
-  constexpr uint32_t kF = 2u * kTPG;                          // ... over the wave's two pages
+  constexpr uint32_t kF = kPPW * kTPG;                        // ... over the wave's pages
   constexpr uint32_t kB = kF < 8u ? kF : 8u;                  // slots loaded together
-  uint32_t ph[2], nt[2];
+  uint32_t ph[kPPW], nt[kPPW];
 #pragma unroll
-  for (uint32_t k = 0; k < 2u; ++k) {
-    const uint32_t i = ib + wave + 4u * k;
+  for (uint32_t k = 0; k < kPPW; ++k) {
+    const uint32_t i = ib + wave + W * k;
     const uint32_t ic = i < i1 ? i : ib;
     uint32_t phys;
     if (a.sel == nullptr) phys = (uint32_t)a.kv_indices[pbeg + ic];
@@ -522,7 +526,7 @@ __global__ __launch_bounds__(256) void gen_decode_kernel(DecodeArgs a) {
   }
   __syncthreads();  // every thread has read the partials
   uint32_t* pw = reinterpret_cast<uint32_t*>(a.partial + bh * a.max_chunks * kStride);
-  for (uint32_t i = threadIdx.x; i < nch * kStride; i += 256u) st_agent_u32(pw + i, 0u);
+  for (uint32_t i = threadIdx.x; i < nch * kStride; i += W * 64u) st_agent_u32(pw + i, 0u);
 }
 
 // ---------------------------------------------------------------- prefill
@@ -652,8 +656,19 @@ hipError_t launch_gen_estimate(const EstimateArgs& a, uint32_t batch, uint32_t m
 }
 
 hipError_t launch_gen_decode(const DecodeArgs& a, uint32_t batch, uint32_t D_, hipStream_t s) {
-  AOAKV_GEN_D(D_, hipLaunchKernelGGL(gen_decode_kernel<D>, dim3(a.max_chunks, a.Hq, batch),
-                                      dim3(256), 0, s, a))
+  // 8 waves (a page each) while the grid fits the GPU's 256 CUs once over
+  // (32k context, budget 2048: head dim 256 19.9 -> 15.2 us, page size 32
+  // 18.4 -> 14.4); with more workgroups, 4 waves, of which more fit per CU
+  // (page size 8, 1,024 workgroups: 15.5 us with 4 waves, 30.9 with 8)
+  const bool wide = (size_t)a.max_chunks * a.Hq * batch <= 256u;
+  AOAKV_GEN_D(D_, {
+    if (wide)
+      hipLaunchKernelGGL((gen_decode_kernel<D, 8>), dim3(a.max_chunks, a.Hq, batch), dim3(512), 0,
+                         s, a);
+    else
+      hipLaunchKernelGGL((gen_decode_kernel<D, 4>), dim3(a.max_chunks, a.Hq, batch), dim3(256), 0,
+                         s, a);
+  })
   return hipGetLastError();
 }
 
