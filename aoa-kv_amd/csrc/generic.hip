@@ -360,8 +360,8 @@ __global__ __launch_bounds__(256) void gen_estimate_kernel(EstimateArgs a) {
 // (chunk, query head, sequence) of W waves; wave w takes the chunk's entries
 // w, w + W, ..., lane group v of a wave the page's tokens v, v + 64/N, ...
 // W = 8 (a page per wave) when the grid has no more workgroups than the GPU
-// has CUs, else 4 (fewer registers per workgroup, more of them resident).  Logits
-// fp16(q.k), then fp16(. / sqrt(d)) (quest_attention.py:265-268); online
+// has CUs, else 4 (fewer registers per workgroup, more of them resident).
+// Logits fp16(q.k), then fp16(. / sqrt(d)) (quest_attention.py:265-268); online
 // softmax in fp32; the groups' (m, l, o) merged in LDS into the chunk's
 // partial.  A head of one chunk writes its output directly; otherwise the
 // last chunk to arrive at the head's counter merges the partials in chunk
@@ -414,12 +414,12 @@ __global__ __launch_bounds__(W * 64) void gen_decode_kernel(DecodeArgs a) {
   const uint32_t i1 = ib + kGenChunkPages < npages ? ib + kGenChunkPages : npages;
   // The wave's pages, entries ib + wave, ib + wave + W, ..., and their token
   // counts (0: no page).  Group v takes tokens v, v + GPW, ... of each.  The
-  // K/V loads go out in batches of kB (page, token)
-  // slots, all of a batch before any is used (unconditional loads of
-  // clamped addresses: a slot past its page's tokens reads the page's slot
-  // 0, a missing page the chunk's first), so a wave waits on memory once
-  // per batch instead of once per token slot; the arithmetic runs in the
-  // same order as token by token.
+  // K/V loads go out in batches of kB (page, token) slots, all of a batch
+  // before any is used (unconditional loads of clamped addresses: a slot
+  // past its page's tokens reads the page's slot 0, a missing page the
+  // chunk's first), so a wave waits on memory once per batch instead of
+  // once per token slot; the arithmetic runs in the same order as token by
+  // token.
   constexpr uint32_t kPPW = kGenChunkPages / W;              // pages per wave
   constexpr uint32_t kTPG = (kMaxPageSize + GPW - 1u) / GPW;  // token slots of a group per page
   constexpr uint32_t kF = kPPW * kTPG;                        // ... over the wave's pages
