@@ -688,7 +688,17 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
   ea.flags &= kSelectFlags;
   ea.error = da.error;
   const bool tuned = aoakv::tuned_shape(head_dim, page_size);
-  if (tuned && (flags & AOAKV_FLAG_SINGLE_LAUNCH) && max_pages <= aoakv::fused_topk_max_pages()) {
+  // the one-launch grid is one dimension of 256-thread workgroups (scoring
+  // items, a top-k per kv head, decode items), and a dispatch counts its
+  // work-items in 32 bits: a larger layer (1,024 sequences of 32 heads at
+  // 512 decode chunks each, say) runs as the two launches, whose grids are
+  // three-dimensional
+  const uint64_t one_launch_grid =
+      (uint64_t)batch_size * num_kv_heads *
+          (aoakv::est_chunks(max_pages, num_qo_heads / num_kv_heads) + 1u) +
+      (uint64_t)batch_size * (num_qo_heads / da.heads_per_item) * da.max_chunks;
+  if (tuned && (flags & AOAKV_FLAG_SINGLE_LAUNCH) && max_pages <= aoakv::fused_topk_max_pages() &&
+      one_launch_grid <= aoakv::layer_max_workgroups()) {
     // one launch: scoring, top-k and decode items of every head
     aoakv::LayerArgs la{};
     la.e = ea;

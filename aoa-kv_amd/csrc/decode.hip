@@ -1598,9 +1598,11 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la)
   }
 }
 
+// grid-stride: a workspace of 16 GiB or more holds 2^32 words, more than one
+// dispatch's 32-bit work-item count
 __global__ void fill_u32_kernel(uint32_t* p, size_t n, uint32_t v) {
-  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = v;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = v;
 }
 
 // ---------------------------------------------------------------- launchers
@@ -1627,6 +1629,8 @@ hipError_t launch_estimate(const EstimateArgs& a, uint32_t batch, uint32_t max_p
 }
 
 hipError_t launch_layer(const LayerArgs& la, hipStream_t s) {
+  if ((uint64_t)la.n_workers + la.n_heads + la.n_dec > layer_max_workgroups())
+    return hipErrorInvalidConfiguration;
   const uint32_t grid = la.n_workers + la.n_heads + la.n_dec;
   const bool quest = (la.e.flags & kFlagQuestKernel) != 0u;
   const bool self = la.self_select != 0u;
@@ -1664,6 +1668,8 @@ hipError_t launch_layer(const LayerArgs& la, hipStream_t s) {
   }
   return hipGetLastError();
 }
+
+uint64_t layer_max_workgroups() { return 0xFFFFFFFFull / (uint64_t)kThreads; }
 
 uint32_t est_chunks(uint32_t max_pages, uint32_t group) {
   const uint32_t n = est_block_pages_of(group);
@@ -1706,7 +1712,8 @@ hipError_t launch_decode(const DecodeArgs& a, uint32_t batch, hipStream_t s,
 
 hipError_t launch_fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s) {
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, n, v);
+  const size_t blocks = (n + 255) / 256 < 65536u ? (n + 255) / 256 : 65536u;
+  hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p, n, v);
   return hipGetLastError();
 }
 

@@ -208,6 +208,7 @@ hipError_t launch_estimate(const EstimateArgs& a, uint32_t batch, uint32_t max_p
 hipError_t launch_topk(const TopkArgs& a, uint32_t batch, hipStream_t s);
 hipError_t launch_layer(const LayerArgs& la, hipStream_t s);
 uint32_t est_chunks(uint32_t max_pages, uint32_t group);  // scoring items per (sequence, kv head)
+uint64_t layer_max_workgroups();  // one-launch layer grid limit (32-bit work-item count)
 // self: the decode items select for themselves from the scores of the
 // previous launch (the scoring call's arguments, with sel / budgets / flags)
 hipError_t launch_decode(const DecodeArgs& a, uint32_t batch, hipStream_t s,

@@ -135,6 +135,19 @@ void host_paths() {
                                                      AOAKV_FLAG_GROUPED_DECODE), nullptr);
       EXPECT(launched_or_hip(rc));
     }
+    // more workgroups than one launch's 32-bit work-item count holds
+    // (4,096 x 16 x 256 decode items): the two launches run instead
+    {
+      const uint32_t Bb = 4096, Hb = 16, Pb = 2048, Kb = 2047;
+      const size_t wsb = aoakv_layer_workspace_size(Bb, Hb, Hb, 128, Kb, Pb);
+      EXPECT(wsb / 4u > ((size_t)1 << 32));
+      int rc = aoakv_sparse_decode_layer(
+          fake(1), fake(2), fake(3), fake<int32_t>(4), fake<int32_t>(5), fake<int32_t>(6),
+          fake(7), fake<int32_t>(8), fake<int32_t>(9), fake(10), fake<float>(11), Pb,
+          fake<int32_t>(12), Kb, Kb * 16u, nul, fake(13), wsb, Bb, Pb, Hb, Hb, 128, 16, layout,
+          AOAKV_FLAG_VALUE_AWARE | AOAKV_FLAG_FIXED | AOAKV_FLAG_SINGLE_LAUNCH, nullptr);
+      EXPECT(launched_or_hip(rc));
+    }
     // the generic shapes: any number of pages (12,500 chunks of 8 here)
     int rc = aoakv_decode_sparse_attn(fake(1), fake(2), fake(3), fake<int32_t>(4),
                                       fake<int32_t>(5), fake<int32_t>(6), nul, 0, 0, nul,
