@@ -78,7 +78,10 @@ extern "C" {
 #define AOAKV_FLAG_FIXED 2u       /* force first and last page (sim `fixed`) */
 /* aoakv_sparse_decode_layer only: run scoring, top-k and decode in ONE launch
  * (scoring workers, per-head top-k and decode items handing over through
- * the workspace) instead of two launches.  Workgroups wait on lower-indexed
+ * the workspace) instead of two launches.  A call whose rows exceed 4,096
+ * pages, or whose one-launch grid would exceed 16,777,215 workgroups (a
+ * dispatch's 32-bit work-item count at 256 per workgroup), runs as the two
+ * launches, with the same results.  Workgroups wait on lower-indexed
  * workgroups of the launch, each wait bounded; if one gives up,
  * AOAKV_WS_ERR_WAIT is set in the workspace's error word, the output is
  * invalid and handoff words may be left set.  Every later one-launch call
