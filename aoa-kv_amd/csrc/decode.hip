@@ -681,8 +681,17 @@ __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, ui
     const uint32_t mp = (uint32_t)s * kPS < kPageSize ? mp0 : mp1;
     const size_t off =
         elem_off(a.g, mp, 0, hrow, (page0 + (uint32_t)s * kPS + rpage) % kPageSize) + d0;
-    kmx[s] = ld16(a.meta + off);
-    kmn[s] = ld16(a.meta + off + a.g.kv);
+    // each metadata vector is read by one item: non-temporal loads (config
+    // 2: 21.33 -> 21.03 us per layer).  A GQA group's scoring items read
+    // plain: with non-temporal loads there the layer was slower (14.4 ->
+    // 14.7 us at 32 / 8)
+    if constexpr (GROUP == 1) {
+      kmx[s] = ld16_nt(a.meta + off);
+      kmn[s] = ld16_nt(a.meta + off + a.g.kv);
+    } else {
+      kmx[s] = ld16(a.meta + off);
+      kmn[s] = ld16(a.meta + off + a.g.kv);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
   // without the value term v_log_norm may be null: read q instead (unused)
@@ -950,7 +959,7 @@ struct DecShared {
 // One launch: err0 is the error word as read at the workgroup's start and
 // s_err an LDS word for it; with kErrWait set no handoff word is touched and
 // the group's outputs are NaN (written by its chunk 0).
-template <bool HANDOFF, bool QUEST, bool SELF = false, int G = 1>
+template <bool HANDOFF, bool QUEST, bool SELF = false, int G = 1, bool STREAM = false>
 __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uint32_t hq0,
                                             uint32_t chunk, DecShared<G>& sm,
                                             const EstimateArgs* ea = nullptr,
@@ -1120,18 +1129,23 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
       phys[s] = (uint32_t)a.kv_indices[pbeg + i];
     }
   }
+  // STREAM (no GQA: each selected page's K/V is read by this item alone):
+  // non-temporal loads, config 2 21.33 -> 20.88 us per layer.  The query
+  // heads of a GQA group read their kv head's pages through the L2, and
+  // non-temporal loads there made the layer slower (14.4 -> 14.8 us at 32 / 8)
+  auto ldkv = [](const f16* p) { return STREAM ? ld16_nt(p) : ld16(p); };
   H8 kk[kDecPagesPerWave][4], vv[kDecPagesPerWave][4];
 #pragma unroll
   for (int s = 0; s < kDecPagesPerWave; ++s) {
     const size_t kbase = elem_off(a.g, phys[s], 0, hkv, 0) + d0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) kk[s][i] = ld16(a.kv + kbase + (size_t)(i * 4 + row) * a.g.tok);
+    for (int i = 0; i < 4; ++i) kk[s][i] = ldkv(a.kv + kbase + (size_t)(i * 4 + row) * a.g.tok);
   }
 #pragma unroll
   for (int s = 0; s < kDecPagesPerWave; ++s) {
     const size_t vbase = elem_off(a.g, phys[s], 1, hkv, 0) + d0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) vv[s][i] = ld16(a.kv + vbase + (size_t)(i * 4 + row) * a.g.tok);
+    for (int i = 0; i < 4; ++i) vv[s][i] = ldkv(a.kv + vbase + (size_t)(i * 4 + row) * a.g.tok);
   }
   __builtin_amdgcn_sched_barrier(0);
   // tokens per page: the sequence's last page holds lpl of them
@@ -1426,7 +1440,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
 // item runs its kv head's top-k on the scores the previous launch wrote (e:
 // the scoring call's arguments with sel, budgets and flags) and writes its
 // chunk's entries of the selection.
-template <bool QUEST, int G, bool SELF = false>
+template <bool QUEST, int G, bool SELF = false, bool STREAM = false>
 __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a, EstimateArgs e) {
   TL_BEGIN();
   TL(kTlStart);
@@ -1435,11 +1449,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a, Estimate
       TopkShared tk;
       DecShared<G> d;
     } sm;
-    decode_item<false, QUEST, true, G>(a, blockIdx.z, blockIdx.y * G, blockIdx.x, sm.d, &e,
-                                       &sm.tk);
+    decode_item<false, QUEST, true, G, STREAM>(a, blockIdx.z, blockIdx.y * G, blockIdx.x, sm.d,
+                                               &e, &sm.tk);
   } else {
     __shared__ DecShared<G> sm;
-    decode_item<false, QUEST, false, G>(a, blockIdx.z, blockIdx.y * G, blockIdx.x, sm);
+    decode_item<false, QUEST, false, G, STREAM>(a, blockIdx.z, blockIdx.y * G, blockIdx.x, sm);
   }
   TL_FLUSH();
 }
@@ -1590,10 +1604,11 @@ __global__ __launch_bounds__(kThreads) void layer_kernel(LayerArgs la)
       const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
       sleep_until(t0, (uint64_t)(unit < first_round ? unit : first_round) * la.stagger_ps);
       TL(kTlStaggerDone);
-      decode_item<true, QUEST, true, GI>(la.d, b, hq0, chunk, sm.d, &la.e, &sm.e.tk, &s_err, err0);
+      decode_item<true, QUEST, true, GI, GROUP == 1>(la.d, b, hq0, chunk, sm.d, &la.e, &sm.e.tk,
+                                                     &s_err, err0);
     } else {
-      decode_item<true, QUEST, false, GI>(la.d, b, hq0, chunk, sm.d, nullptr, nullptr, &s_err,
-                                          err0);
+      decode_item<true, QUEST, false, GI, GROUP == 1>(la.d, b, hq0, chunk, sm.d, nullptr, nullptr,
+                                                      &s_err, err0);
     }
   }
 }
@@ -1689,22 +1704,31 @@ hipError_t launch_decode(const DecodeArgs& a, uint32_t batch, hipStream_t s,
   const bool quest = (a.flags & kFlagQuestKernel) != 0u;
   const EstimateArgs e = self != nullptr ? *self : EstimateArgs{};
   switch (gi) {
-#define AOAKV_DEC(G)                                                                          \
-  case G:                                                                                     \
-    if (self != nullptr) {                                                                    \
-      if (quest) hipLaunchKernelGGL((decode_kernel<true, G, true>), grid, dim3(kThreads), 0, s, a, e); \
-      else hipLaunchKernelGGL((decode_kernel<false, G, true>), grid, dim3(kThreads), 0, s, a, e);      \
-    } else if (quest) {                                                                       \
-      hipLaunchKernelGGL((decode_kernel<true, G>), grid, dim3(kThreads), 0, s, a, e);         \
-    } else {                                                                                  \
-      hipLaunchKernelGGL((decode_kernel<false, G>), grid, dim3(kThreads), 0, s, a, e);        \
-    }                                                                                         \
+#define AOAKV_DEC_S(G, ST)                                                                    \
+  if (self != nullptr) {                                                                      \
+    if (quest) hipLaunchKernelGGL((decode_kernel<true, G, true, ST>), grid, dim3(kThreads), 0, s, a, e); \
+    else hipLaunchKernelGGL((decode_kernel<false, G, true, ST>), grid, dim3(kThreads), 0, s, a, e);      \
+  } else if (quest) {                                                                         \
+    hipLaunchKernelGGL((decode_kernel<true, G, false, ST>), grid, dim3(kThreads), 0, s, a, e);  \
+  } else {                                                                                    \
+    hipLaunchKernelGGL((decode_kernel<false, G, false, ST>), grid, dim3(kThreads), 0, s, a, e); \
+  }
+#define AOAKV_DEC(G)   \
+  case G:              \
+    AOAKV_DEC_S(G, false) \
     break;
-    AOAKV_DEC(1)
+    case 1:  // without GQA each page's K/V has one reader: streamed
+      if (a.Hq == a.Hkv) {
+        AOAKV_DEC_S(1, true)
+      } else {
+        AOAKV_DEC_S(1, false)
+      }
+      break;
     AOAKV_DEC(2)
     AOAKV_DEC(4)
     AOAKV_DEC(8)
 #undef AOAKV_DEC
+#undef AOAKV_DEC_S
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
