@@ -1779,14 +1779,18 @@ uint32_t layer_score_workers(uint32_t n_est, uint32_t est_chunks) {
 // offset holds whatever the clock.  Config 2 (16 chunks per head: 1.05 MB),
 // us per layer by bytes per ns: 5600: 24.06, 6100: 23.69, 6600: 23.35-23.39,
 // 7100: 23.20-23.26, 7600: 23.31, 8200: 23.49, 9000: 23.85 (the former
-// core-cycle stagger at its best, 376 cycles per head: 23.26).  With at
-// most kFewHeads heads every head starts at once: their metadata is a short
+// core-cycle stagger at its best, 376 cycles per head: 23.26).  Since the
+// metadata and K/V stream with non-temporal loads (they reach HBM faster),
+// 8,500 B/ns: 6,000 21.28, 7,100 20.52-20.56, 7,600 20.32-20.35, 8,000
+// 20.21-20.25, 8,500 20.22-20.24, 9,000 20.24-20.27, 10,500 20.38-20.40
+// (480 workers; 448: 20.81, 512: 20.22-20.25 at 8,500).  With at most
+// kFewHeads heads every head starts at once: their metadata is a short
 // stream whose heads all end in the same round (GQA above with 512 workers:
 // no stagger 15.1 us, 7,100 B/ns 15.4, 14,000 B/ns 15.4).
 uint32_t layer_stagger_ps(uint32_t est_chunks, uint32_t group, uint32_t heads) {
   if (heads <= kFewHeads) return 0u;
   const uint64_t chunk_bytes = est_block_pages_of(group) * (2u * kHeadDim * 2u + 2u);
-  constexpr uint64_t kStreamBytesPerNs = 7100u;
+  constexpr uint64_t kStreamBytesPerNs = 8500u;
   return (uint32_t)((uint64_t)est_chunks * chunk_bytes * 1000u / kStreamBytesPerNs);
 }
 uint32_t counter_stride() { return kCounterStride; }
