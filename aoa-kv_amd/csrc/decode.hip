@@ -681,17 +681,12 @@ __device__ __forceinline__ bool score_item(const EstimateArgs& a, uint32_t b, ui
     const uint32_t mp = (uint32_t)s * kPS < kPageSize ? mp0 : mp1;
     const size_t off =
         elem_off(a.g, mp, 0, hrow, (page0 + (uint32_t)s * kPS + rpage) % kPageSize) + d0;
-    // each metadata vector is read by one item: non-temporal loads (config
-    // 2: 21.33 -> 21.03 us per layer).  A GQA group's scoring items read
-    // plain: with non-temporal loads there the layer was slower (14.4 ->
-    // 14.7 us at 32 / 8)
-    if constexpr (GROUP == 1) {
-      kmx[s] = ld16_nt(a.meta + off);
-      kmn[s] = ld16_nt(a.meta + off + a.g.kv);
-    } else {
-      kmx[s] = ld16(a.meta + off);
-      kmn[s] = ld16(a.meta + off + a.g.kv);
-    }
+    // each metadata vector is read by one item, once: non-temporal loads
+    // (config 2: 21.33 -> 21.03 us per layer; GQA 32 / 8 over 32 rotated
+    // layers: 15.37 -> 15.08.  Over 8 rotated layers, whose 134 MB stay in
+    // the memory-side cache, plain loads were faster: 14.37 against 14.68)
+    kmx[s] = ld16_nt(a.meta + off);
+    kmn[s] = ld16_nt(a.meta + off + a.g.kv);
   }
   __builtin_amdgcn_sched_barrier(0);
   // without the value term v_log_norm may be null: read q instead (unused)
@@ -1132,7 +1127,8 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, uint32_t b, uin
   // STREAM (no GQA: each selected page's K/V is read by this item alone):
   // non-temporal loads, config 2 21.33 -> 20.88 us per layer.  The query
   // heads of a GQA group read their kv head's pages through the L2, and
-  // non-temporal loads there made the layer slower (14.4 -> 14.8 us at 32 / 8)
+  // non-temporal loads there made the layer slower (32 / 8 over 32 rotated
+  // layers, with streamed metadata: 15.08 -> 15.21 us)
   auto ldkv = [](const f16* p) { return STREAM ? ld16_nt(p) : ld16(p); };
   H8 kk[kDecPagesPerWave][4], vv[kDecPagesPerWave][4];
 #pragma unroll
