@@ -309,8 +309,9 @@ __global__ __launch_bounds__(256) void gen_estimate_kernel(EstimateArgs a) {
     const uint32_t p = pb + threadIdx.x / N + st * PPS;
     const uint32_t pc = p < p_end ? p : pb;
     const size_t off = elem_off(a.g, mpg[st], 0, h, pc % a.S) + l * kVec;
-    kmxs[st] = ld16(a.meta + off);
-    kmns[st] = ld16(a.meta + off + a.g.kv);
+    // read once: non-temporal loads, as the tuned scoring's
+    kmxs[st] = ld16_nt(a.meta + off);
+    kmns[st] = ld16_nt(a.meta + off + a.g.kv);
     lvn[st] = value_aware ? a.v_log_norm[(size_t)phys[st] * a.Hkv + h] : (f16)0.f;
   }
 #pragma unroll
@@ -368,7 +369,9 @@ __global__ __launch_bounds__(256) void gen_estimate_kernel(EstimateArgs a) {
 // order (the same arithmetic whichever workgroup merges) and clears them.
 // The quest_kernel convention attends the last page after the nsel selected
 // ones.
-template <int D, uint32_t W>
+// STREAM: no GQA group shares the pages' K/V, which are then loaded
+// non-temporally (as in the tuned decode)
+template <int D, uint32_t W, bool STREAM>
 __global__ __launch_bounds__(W * 64) void gen_decode_kernel(DecodeArgs a) {
   static_assert(W == 4u || W == 8u, "4 or 8 waves");
   constexpr uint32_t N = D / 8, GPW = kWave / N, G = W * GPW;  // groups per wave / block
@@ -443,8 +446,10 @@ __global__ __launch_bounds__(W * 64) void gen_decode_kernel(DecodeArgs a) {
       if (GPW * j >= S) continue;  // uniform: slots past the page size
       const uint32_t t = v + GPW * j;
       const uint32_t tc = t < nt[k] ? t : 0u;
-      kk[u] = ld16(a.kv + elem_off(a.g, ph[k], 0, hkv, tc) + l * kVec);
-      vv[u] = ld16(a.kv + elem_off(a.g, ph[k], 1, hkv, tc) + l * kVec);
+      const f16* kp = a.kv + elem_off(a.g, ph[k], 0, hkv, tc) + l * kVec;
+      const f16* vp = a.kv + elem_off(a.g, ph[k], 1, hkv, tc) + l * kVec;
+      kk[u] = STREAM ? ld16_nt(kp) : ld16(kp);
+      vv[u] = STREAM ? ld16_nt(vp) : ld16(vp);
     }
 #pragma unroll
     for (uint32_t u = 0; u < kB; ++u) {
@@ -659,15 +664,23 @@ hipError_t launch_gen_decode(const DecodeArgs& a, uint32_t batch, uint32_t D_, h
   // 8 waves (a page each) while the grid fits the GPU's 256 CUs once over
   // (32k context, budget 2048: head dim 256 19.9 -> 15.2 us, page size 32
   // 18.4 -> 14.4); with more workgroups, 4 waves, of which more fit per CU
-  // (page size 8, 1,024 workgroups: 15.5 us with 4 waves, 30.9 with 8)
+  // (page size 8, 1,024 workgroups: 15.5 us with 4 waves, 30.9 with 8).
+  // Without GQA the K/V loads stream (non-temporal): over 32 rotated layers
+  // head dim 64 23.1 -> 22.2 us per layer (scores + decode), 256 34.4 ->
+  // 32.5, page size 8 41.4 -> 39.1, page size 32 27.9 -> 27.0, with the
+  // scoring's metadata streamed too
   const bool wide = (size_t)a.max_chunks * a.Hq * batch <= 256u;
+  const bool stream = a.Hq == a.Hkv;
+  const dim3 grid(a.max_chunks, a.Hq, batch);
   AOAKV_GEN_D(D_, {
-    if (wide)
-      hipLaunchKernelGGL((gen_decode_kernel<D, 8>), dim3(a.max_chunks, a.Hq, batch), dim3(512), 0,
-                         s, a);
+    if (wide && stream)
+      hipLaunchKernelGGL((gen_decode_kernel<D, 8, true>), grid, dim3(512), 0, s, a);
+    else if (wide)
+      hipLaunchKernelGGL((gen_decode_kernel<D, 8, false>), grid, dim3(512), 0, s, a);
+    else if (stream)
+      hipLaunchKernelGGL((gen_decode_kernel<D, 4, true>), grid, dim3(256), 0, s, a);
     else
-      hipLaunchKernelGGL((gen_decode_kernel<D, 4>), dim3(a.max_chunks, a.Hq, batch), dim3(256), 0,
-                         s, a);
+      hipLaunchKernelGGL((gen_decode_kernel<D, 4, false>), grid, dim3(256), 0, s, a);
   })
   return hipGetLastError();
 }

@@ -436,13 +436,15 @@ def gqa_bench(dev, layout, n_layers=32, hq=32, hkv=8, launches=256):
     return out
 
 
-def generic_shapes_bench(dev, layout, n_layers=4, launches=200):
+def generic_shapes_bench(dev, layout, n_layers=32, launches=200):
     """The shapes outside the tuned (128, 16) kernels at config 2's context
     (32768 tokens) and budget (2048 tokens), H heads: the decode layer
     (two launches: the generic scoring kernel and the standalone top-k, then
     the split-K generic decode) and its scoring and decode kernels alone, us
-    per call from a HIP graph over n_layers rotated layers (past the
-    memory-side cache).  Keys (f"d{D}_s{S}"): head dim D, page size S."""
+    per call from a HIP graph over n_layers rotated layers (32: a pass reads
+    1.1-3.2 GB, past the 256 MB memory-side cache, as a model's decode step
+    would; 4 layers stay in that cache).  Keys (f"d{D}_s{S}"): head dim D,
+    page size S."""
     import torch
     from aoakv import ops
     out = {}
