@@ -768,9 +768,10 @@ int aoakv_sparse_decode_layer(const void* q, void* o, const void* kv_data,
     // then decode items that each select their kv head's pages from the
     // complete scores (16 copies of every top-k, none waiting on another
     // workgroup) and write their chunk's entries of sel_pages.  Config 2:
-    // 24.7-25.1 us per layer, against 25.6 with the top-k fused into the
-    // scoring launch's last item per head (13.7 + 12.1); starting the kv
-    // heads' decode items 0.1-0.3 us apart was slower (25.1-30.0).
+    // 23.0 us per layer (7.9 + 15.1), against 24.1 with the top-k fused into
+    // the scoring launch's last item per head (13.0 + 11.1); before the
+    // streamed loads 24.7-25.1 against 25.6, and starting the kv heads'
+    // decode items 0.1-0.3 us apart was slower (25.1-30.0).
     if (int e = hip_status(aoakv::launch_estimate(ea, batch_size, max_pages, s), "estimate"))
       return e;
     aoakv::EstimateArgs es = ea;
