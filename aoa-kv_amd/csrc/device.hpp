@@ -64,7 +64,7 @@ __device__ inline H8 ld16(const f16* p) {
   return __builtin_bit_cast(H8, u);
 }
 // 16 bytes of data read once per launch (the K/V gather, the scoring's
-// metadata) with a non-temporal load: on the box, 256 workgroups gathering
+// metadata) with a non-temporal load: on an MI355X, 256 workgroups gathering
 // 64 KB each of random 4 KB blocks took 1.16 us at the median and 2.8 at
 // the slowest this way, against 2.6 and 6.0 us with plain loads
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
