@@ -1069,6 +1069,29 @@ def main():
         t1.record()
         torch.cuda.synchronize()
         extra["eager_us_per_layer"] = round(t0.elapsed_time(t1) * 1e3 / n_aux, 3)
+        # the same 32 layers in the other cache layout (the reference's
+        # drop-in layout is NHD): same seeds, so the same bits are expected;
+        # measured right after the main figure, before the prefill and the
+        # other extras heat the GPU
+        other = ops.NHD if layout == ops.HND else ops.HND
+        oname = "nhd" if other == ops.NHD else "hnd"
+        log(f"[bench] {oname.upper()} layout ...")
+        del B, kv, meta, lvn
+        torch.cuda.empty_cache()
+        B2 = build_layers(n_layers, other, dev)
+        o2 = torch.zeros_like(o)
+        layout_of[0] = other
+        layer1b = make_layer(B2["kv"], B2["meta"], B2["lvn"], o2, ops.FLAG_SINGLE_LAUNCH)
+        gb = capture(layer1b, n_aux)
+        gb.replay()
+        torch.cuda.synchronize()
+        us_b = replay_timed(gb, n_aux)
+        layout_of[0] = layout
+        extra[f"{oname}_us_per_layer"] = round(us_b, 3)
+        extra[f"{oname}_layer_GBps"] = round(LAYER_BYTES / (us_b * 1e-6) / 1e9, 1)
+        extra[f"{oname}_equals_{args.layout}"] = bool(torch.equal(o2, o_eager))
+        del gb, B2
+        torch.cuda.empty_cache()
         app = append_us[1:]
         app_bytes = 2 * L * H * D * 2 * 2 + H * P * 2 * D * 2 + H * P * 2 + H * P * D * 2
         extra["bulk_append_32k_us"] = round(float(np.median(app)), 2)
@@ -1099,27 +1122,6 @@ def main():
         extra["gqa_32q_8kv_32k"] = gqa_bench(dev, layout)
         log("[bench] generic shapes (head dims 64 / 256, pages of 8 / 32) ...")
         extra["generic_shapes_32k"] = generic_shapes_bench(dev, layout)
-        # the same 32 layers in the other cache layout (the reference's
-        # drop-in layout is NHD): same seeds, so the same bits are expected
-        other = ops.NHD if layout == ops.HND else ops.HND
-        oname = "nhd" if other == ops.NHD else "hnd"
-        log(f"[bench] {oname.upper()} layout ...")
-        del B, kv, meta, lvn
-        torch.cuda.empty_cache()
-        B2 = build_layers(n_layers, other, dev)
-        o2 = torch.zeros_like(o)
-        layout_of[0] = other
-        layer1b = make_layer(B2["kv"], B2["meta"], B2["lvn"], o2, ops.FLAG_SINGLE_LAUNCH)
-        gb = capture(layer1b, n_aux)
-        gb.replay()
-        torch.cuda.synchronize()
-        us_b = replay_timed(gb, n_aux)
-        layout_of[0] = layout
-        extra[f"{oname}_us_per_layer"] = round(us_b, 3)
-        extra[f"{oname}_layer_GBps"] = round(LAYER_BYTES / (us_b * 1e-6) / 1e9, 1)
-        extra[f"{oname}_equals_{args.layout}"] = bool(torch.equal(o2, o_eager))
-        del gb, B2
-        torch.cuda.empty_cache()
 
     # the measured path is one kernel per layer: it is the dominant kernel
     dom_us, dom_bytes, dom_name = us_one, LAYER_BYTES, \
